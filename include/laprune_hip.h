@@ -1,0 +1,262 @@
+/*
+ * laprune_hip.h — C ABI of the MI355X (gfx950) decode-time retrieval path.
+ *
+ * Every entry point takes caller-owned device pointers for inputs AND outputs,
+ * explicit sizes/strides and a hipStream_t, launches asynchronously on that
+ * stream and returns an int status (LAP_OK on success).  Nothing here
+ * allocates device memory: kernels that need scratch take a workspace pointer
+ * whose size is reported by the matching *_workspace_size() query.  On error
+ * the status is non-zero and lap_last_error() returns a thread-local message.
+ *
+ * Element types are passed as LAP_DTYPE_* codes.  Strides are in elements.
+ * fp16/bf16 values are raw 16-bit patterns (uint16_t in memory).
+ *
+ * Reference interfaces replaced (paths relative to the LAPrune source tree):
+ *   aq_kernels/aq_lut_gqa.cu, aq_kernels/aq_lut.cu,
+ *   aq_kernels/fused_linear_encode.cu, laprune/llm/aq_kv.py,
+ *   laprune/llm/modifiers/aq_evaluation.py.
+ */
+#ifndef LAPRUNE_HIP_H
+#define LAPRUNE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is an opaque pointer; declared here as void* so the header does
+ * not depend on the HIP headers (0 = the null stream). */
+typedef void* lap_stream_t;
+
+/* ---- status codes ------------------------------------------------------ */
+#define LAP_OK              0
+#define LAP_ERR_INVALID     1   /* bad shape / stride / dtype / range      */
+#define LAP_ERR_UNSUPPORTED 2   /* valid request this build does not serve  */
+#define LAP_ERR_HIP         3   /* HIP runtime or launch failure            */
+#define LAP_ERR_WORKSPACE   4   /* workspace missing or too small           */
+
+/* ---- element type codes ------------------------------------------------ */
+#define LAP_DTYPE_F32   0
+#define LAP_DTYPE_F16   1
+#define LAP_DTYPE_BF16  2
+#define LAP_DTYPE_U8    3
+#define LAP_DTYPE_I8    4
+#define LAP_DTYPE_I32   5
+#define LAP_DTYPE_I64   6
+
+/* ---- LUT layouts ------------------------------------------------------- */
+#define LAP_LUT_HMK   0   /* [Hq][M][K]       (reference layout)          */
+#define LAP_LUT_GMKG  1   /* [Hq/G][M][K][G]  (interleaved, scorer LDS)   */
+
+/* ---- top-k key modes ---------------------------------------------------- */
+#define LAP_KEY_F16   0   /* rank the fp16 score itself                     */
+#define LAP_KEY_BF16  1   /* rank bf16(fp16 score): the model-dtype cast    */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* lap_last_error(void);
+/* ABI version: bumped when any signature below changes. */
+int lap_abi_version(void);
+/* Device facts used for launch shaping (current device). */
+int lap_device_info(int* cu_count, int* lds_bytes_per_block, int* wave_size);
+
+/* ======================================================================= *
+ * A1  LUT builder                                                          *
+ * Replaces: laprune/llm/aq_kv.py:681-682 (torch.matmul(q, C.reshape(MK,d).t())
+ *   .reshape(Hq,M,K)), fp32 form aq_kv.py:620 (einsum "mkd,qd->qmk").
+ * lut[h,m,k] = fp16_rne( fmaf-chain over d = 0..D-1 of q[h,d]*C[m,k,d] ),
+ * accumulated sequentially in fp32 from 0.
+ *   q          [Hq][D], row stride q_row_stride, dtype f32/f16/bf16
+ *   codebooks  [M][K][D] contiguous, dtype f32/f16
+ *   lut_out    fp16, layout LAP_LUT_HMK or LAP_LUT_GMKG (needs Hq % G == 0)
+ * ======================================================================= */
+int lap_lut_build(const void* q, int q_dtype, int64_t q_row_stride,
+                  const void* codebooks, int cb_dtype,
+                  int Hq, int D, int M, int K, int G, int layout,
+                  void* lut_out, lap_stream_t stream);
+
+/* ======================================================================= *
+ * A2  GQA LUT scorers                                                      *
+ * Score accumulation contract (all scorers): acc = 0.0f; for m ascending:
+ * acc += (float)lut_fp16[h, m, code]; out = fp16_rne(acc).
+ * ======================================================================= */
+
+/* Replaces: aq_lut_gather_grouped, aq_kernels/aq_lut_gqa.cu:460-534
+ * (kernels :111-149 and :157-212).
+ *   lut    fp16, layout LAP_LUT_HMK ([Hkv*G][M][K]) or LAP_LUT_GMKG
+ *   codes  u8 [Hkv][T][M] with strides (codes_stride_h, codes_stride_t, 1)
+ *   out    fp16 [Hkv*G][T] contiguous
+ * G in 1..4. */
+int lap_lut_score_grouped(const void* lut, int lut_layout,
+                          const uint8_t* codes, int64_t codes_stride_h,
+                          int64_t codes_stride_t,
+                          int Hkv, int G, int T, int M, int K,
+                          void* out, lap_stream_t stream);
+
+/* Replaces: aq_lut_gather (bound as aq_lut_gather_gqa),
+ * aq_kernels/aq_lut_gqa.cu:350-422 (kernel :20-76).
+ *   lut      fp16 [H][M_stride][K] contiguous, H = Hkv*G (any G >= 1)
+ *   codes    u8 [Hkv][T][M_stride], strides (cs_h, cs_t, 1)
+ *   indices  int64 [H][N] or NULL (dense: N = T); an index outside [0,T)
+ *            scores 0
+ *   out      fp16 [H][N]
+ * Only m in [M_start, M_end) is summed. */
+int lap_lut_score_gqa(const void* lut, const uint8_t* codes,
+                      int64_t codes_stride_h, int64_t codes_stride_t,
+                      int Hkv, int G, int T, int M_stride, int K,
+                      int M_start, int M_end,
+                      const int64_t* indices, int N,
+                      void* out, lap_stream_t stream);
+
+/* Replaces: aq_lut_gather_forward, aq_kernels/aq_lut.cu:641-738
+ * (kernels :581-639).
+ *   lut    [Q][M*K], dtype f16 or f32 (f32 sums in f32, no rounding to f16)
+ *   codes  [Q][N][M] contiguous, dtype u8/i8/i64; the low 8 bits are read as
+ *          an unsigned code and clamped to [0, K-1]
+ *   out    [Q][N], same dtype as lut */
+int lap_lut_score_mha(const void* lut, int lut_dtype,
+                      const void* codes, int codes_dtype,
+                      int Q, int N, int M, int K,
+                      void* out, lap_stream_t stream);
+
+/* Replaces: aq_lut_forward, aq_kernels/aq_lut.cu:445-574 (kernels :37-149).
+ * Direct scoring without a LUT: score[q,n] = sum over m (code valid) of
+ * dot(q, C[m,code]) in one fp32 accumulator.
+ *   f32: acc = fmaf(q[i], c[i], acc) for m, then i ascending
+ *   f16: per pair (i, i+1): p = fp16_rne(q*c) lanewise; acc += (p0 + p1)
+ *   q [Q][D], codebooks [M][K][D], codes [Q][N][M] (u8/i8/i64; low 8 bits),
+ *   out [Q][N] same dtype as q (f32 or f16).  Codes >= K are skipped. */
+int lap_aq_lut_direct(const void* q, const void* codebooks, int dtype,
+                      const void* codes, int codes_dtype,
+                      int Q, int N, int M, int K, int D,
+                      void* out, lap_stream_t stream);
+
+/* ======================================================================= *
+ * A3  Top-k selection                                                      *
+ * Replaces: torch.topk(scores[..., cand_start:cand_end], k, sorted=False)
+ *   at laprune/llm/modifiers/aq_evaluation.py:198-201.
+ * Rows r = 0..R-1 select over columns [cand_start, cand_end) of
+ *   key(r, t) = max over g < group of score[(r*group + g), t]   (fp16)
+ * mapped through key_mode.  The k largest keys are kept; among equal keys
+ * the lowest column wins.  Output: column indices (t, absolute, i.e.
+ * including cand_start) in ascending order, out[r][0..k_eff), with
+ * k_eff = min(k, cand_end - cand_start); entries past k_eff are not written.
+ *   scores   fp16 [R*group][T] with row stride score_row_stride
+ *   out_idx  [R][k] int32 or int64 (out_dtype)
+ * ======================================================================= */
+int lap_topk_workspace_size(int R, int cand_len, size_t* bytes);
+int lap_topk_select(const void* scores, int64_t score_row_stride,
+                    int R, int group, int T, int cand_start, int cand_end,
+                    int k, int key_mode, void* out_idx, int out_dtype,
+                    void* workspace, size_t workspace_bytes,
+                    lap_stream_t stream);
+
+/* Fused score + select for one decode step (A1 output -> A2 -> A3).
+ * lut is LAP_LUT_GMKG fp16 for G = 4, M = 32, K = 256.  Per KV row r the
+ * group key is max_g fp16(score); selection as lap_topk_select.  Optional
+ * per-head fp16 scores are written when scores_out != NULL ([Hkv*4][T]).
+ * R = B*Hkv rows; codes row r = (b, hkv) at codes + b*cs_b + hkv*cs_h. */
+int lap_retrieve_workspace_size(int R, int T, size_t* bytes);
+int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
+                      int64_t codes_stride_b, int64_t codes_stride_h,
+                      int64_t codes_stride_t, int B, int Hkv, int T,
+                      int cand_start, int cand_end, int k, int key_mode,
+                      void* scores_out, void* out_idx, int out_dtype,
+                      void* workspace, size_t workspace_bytes,
+                      lap_stream_t stream);
+
+/* ======================================================================= *
+ * A4  Native-GQA K/V gather                                                *
+ * Replaces: gqa_gather_kv and gqa_gather_kv_with_tail,
+ *   aq_kernels/aq_lut_gqa.cu:536-604 and :606-664 (kernels :222-323).
+ *   keys, vals  [B][Hkv][T][D] with strides (sb, sh, st, 1), f16 or bf16
+ *   indices     int64 [B][Hq][explicit_N] contiguous
+ *   out_k/out_v [B][Hq][N][D] contiguous, N = explicit_N + tail_count;
+ *   row n < explicit_N copies token indices[b,hq,n]; row explicit_N + j
+ *   copies token tail_start + j.  Rows whose token is outside [0,T) are
+ *   left unwritten.  tail_start < 0 means no tail (tail_count must be 0).
+ * ======================================================================= */
+int lap_gqa_gather_kv(const void* keys, const void* vals, int dtype,
+                      int B, int Hkv, int T, int D,
+                      int64_t k_sb, int64_t k_sh, int64_t k_st,
+                      int64_t v_sb, int64_t v_sh, int64_t v_st,
+                      const int64_t* indices, int Hq, int explicit_N,
+                      int tail_start, int tail_count,
+                      void* out_k, void* out_v, lap_stream_t stream);
+
+/* ======================================================================= *
+ * A5  Sparse-attention decode with the gather fused in                    *
+ * Replaces: the gather at aq_evaluation.py:243-247 plus
+ *   F.scaled_dot_product_attention(Q_rope, K_sel, V_sel) at :251; native
+ *   model aq_kernels/aq_lut.cu:195-324 (sparse_attn_q1_kernel).
+ * For each batch b and query head h, over the keep list
+ *   L(b,h) = indices[b, row(h), 0..n_idx) ++ [0, sink_count)
+ *            ++ [tail_start, tail_start + tail_count)
+ * with row(h) = h / (Hq / H_idx) (H_idx = Hq: per-head lists, H_idx = Hkv:
+ * one list per KV group):
+ *   o[b,h] = sum_j softmax_j(scale * q[b,h].K[b,h/G,L_j]) V[b,h/G,L_j]
+ * in fp32, written in the q dtype.  Indices outside [0,T) are skipped.
+ *   q     [B][Hq][D] with row strides (q_sb, q_sh), f16/bf16
+ *   K/V   [B][Hkv][T][D] strides (sb, sh, st, 1), same dtype as q
+ *   indices int32 or int64 [B][H_idx][n_idx] contiguous (may be NULL if
+ *           n_idx == 0)
+ *   out   [B][Hq][D] contiguous, q dtype
+ * ======================================================================= */
+int lap_attn_decode_workspace_size(int B, int Hq, int D, int max_keys, size_t* bytes);
+int lap_sparse_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
+                           const void* keys, const void* vals, int dtype,
+                           int B, int Hq, int Hkv, int T, int D,
+                           int64_t k_sb, int64_t k_sh, int64_t k_st,
+                           int64_t v_sb, int64_t v_sh, int64_t v_st,
+                           const void* indices, int idx_dtype, int H_idx,
+                           int n_idx, int sink_count,
+                           int tail_start, int tail_count, float scale,
+                           void* out, void* workspace, size_t workspace_bytes,
+                           lap_stream_t stream);
+
+/* Dense single-query decode over all T tokens (flash-decode, split-K).
+ * Replaces: laprune/attention.py:62-65 (SDPA with num_queries == 1, native
+ * GQA).  Same argument meaning as lap_sparse_attn_decode with the keep list
+ * [0, T). */
+int lap_dense_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
+                          const void* keys, const void* vals, int dtype,
+                          int B, int Hq, int Hkv, int T, int D,
+                          int64_t k_sb, int64_t k_sh, int64_t k_st,
+                          int64_t v_sb, int64_t v_sh, int64_t v_st,
+                          float scale, void* out,
+                          void* workspace, size_t workspace_bytes,
+                          lap_stream_t stream);
+
+/* ======================================================================= *
+ * A6  Greedy AQ encode                                                     *
+ * Replaces: fused_linear_encode_forward, aq_kernels/fused_linear_encode.cu:
+ *   168-234 (kernel :34-102), called from laprune/llm/aq_kv.py:44-75; the
+ *   contract followed is the fp32 greedy path of laprune/quantizer.py:
+ *   346-355 (_batch_icm_lut, iters = 0):
+ *     r = x; for m: dist_k = (rn + cn[m,k]) - 2*dot(r, C[m,k]);
+ *     code_m = lowest k with minimal dist; r = r - C[m,code_m]
+ *   with dot/rn/cn all computed by dot16: 16 fmaf chains over consecutive
+ *   blocks (chain j sums d = j*L .. j*L+L-1 in order, L = D/16, from 0),
+ *   folded pairwise s[j] += s[j+w] for w = 8, 4, 2, 1.  Requires
+ *   D % 16 == 0, K <= 256.
+ * lap_encode_prepare fills prep (size lap_encode_prep_size) from the
+ * codebooks once; lap_encode_greedy then encodes N rows.
+ *   x          [N][D] fp32 with row stride x_row_stride
+ *   codebooks  [M][K][D] fp32 contiguous
+ *   codes_out  u8 [N][M] with row stride codes_row_stride
+ *   resid_norm fp32 [N] (sqrtf(rn_final)), may be NULL
+ * ======================================================================= */
+int lap_encode_prep_size(int M, int K, int D, size_t* bytes);
+int lap_encode_prepare(const float* codebooks, int M, int K, int D,
+                       void* prep, size_t prep_bytes, lap_stream_t stream);
+int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, int D,
+                      const float* codebooks, int M, int K,
+                      const void* prep, size_t prep_bytes,
+                      uint8_t* codes_out, int64_t codes_row_stride,
+                      float* resid_norm, lap_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LAPRUNE_HIP_H */

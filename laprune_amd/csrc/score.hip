@@ -1,0 +1,475 @@
+// score.hip — A2: AQ LUT scoring of cached keys.
+//
+// Accumulation contract shared by every scorer here and by the reference
+// kernels (aq_kernels/aq_lut_gqa.cu:69-74, :134-147, :195-210):
+//     acc = 0.0f;  for m ascending: acc += (float)lut_fp16[h, m, code_m];
+//     score = fp16_rne(acc)
+//
+// Fast path (G = 4, M = 32, K = 256; Llama-3.1 GQA): one KV group's table
+// [M][K][G] fp16 = 64 KiB sits in LDS, so the four query heads of a code are
+// one 8-byte LDS read.  Each 32-byte code row arrives as two 16-byte loads.
+// The per-head add is one v_fma_mix_f32 (exact fp16->fp32 widening fused
+// with the fp32 add).  The grid is 1-D with the KV row in the low bits of the
+// block id: workgroups are dealt round-robin to the 8 XCDs, so with 8 KV rows
+// each XCD scores one KV group and its 64 KiB table stays in that XCD's L2.
+// Optionally the kernel also emits the group-max selection key (the max of
+// the four fp16 head scores, as an orderable 16-bit key) and a per-workgroup
+// 256-bin histogram of the key's high byte over the candidate window, which
+// is the first radix level of the top-k (topk.hip).
+#include "common.h"
+
+namespace lap {
+
+// Tunables of the fast scorer (read once from the environment; documented in
+// the design notes):  LAPRUNE_SCORE_WG_PER_CU  (default 2 workgroups per CU).
+static int score_wg_per_cu() {
+  static int v = [] {
+    const char* e = getenv("LAPRUNE_SCORE_WG_PER_CU");
+    int x = e ? atoi(e) : 2;
+    return x > 0 && x <= 16 ? x : 2;
+  }();
+  return v;
+}
+
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kG = 4, kM = 32, kK = 256;
+constexpr int kLutBytes = kG * kM * kK * 2;  // 65536
+
+struct ScoreOut {
+  uint16_t* heads;   // [R*4][T] fp16 or null
+  uint16_t* keys;    // [R][T] u16 or null
+  uint32_t* hist;    // [R][nchunk][256] or null
+  int key_mode;
+  int cand_start, cand_end;
+};
+
+// Accumulate one token's 32 lookups into four fp32 head sums.
+__device__ __forceinline__ void score_token(const char* __restrict__ lds, const uint4 c0,
+                                            const uint4 c1, _Float16 one, float& a0,
+                                            float& a1, float& a2, float& a3) {
+  const uint32_t w[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+  for (int m = 0; m < kM; ++m) {
+    const uint32_t off = ((w[m >> 2] >> ((m & 3) * 8)) & 0xffu) << 3;
+    const half4_t v = *reinterpret_cast<const half4_t*>(lds + m * (kK * kG * 2) + off);
+    a0 = acc_f16(a0, v.x, one);
+    a1 = acc_f16(a1, v.y, one);
+    a2 = acc_f16(a2, v.z, one);
+    a3 = acc_f16(a3, v.w, one);
+  }
+}
+
+template <int THREADS, bool LUT_IL>
+__global__ __launch_bounds__(THREADS) void score_g4_kernel(
+    const uint16_t* __restrict__ lut, const uint8_t* __restrict__ codes, int64_t cs_b,
+    int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, int chunk_tokens, ScoreOut so,
+    _Float16 one) {
+  __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
+  __shared__ uint32_t s_hist[256];
+
+  const int r = blockIdx.x % R;
+  const int chunk = blockIdx.x / R;
+  const int tid = threadIdx.x;
+  const int b = r / Hkv, hkv = r - b * Hkv;
+
+  // Fill the [M][K][G] table.
+  if (LUT_IL) {
+    const uint4* src = reinterpret_cast<const uint4*>(lut + (int64_t)r * (kG * kM * kK));
+#pragma unroll 4
+    for (int i = tid; i < kLutBytes / 16; i += THREADS) s_lut[i] = src[i];
+  } else {
+    // Reference layout [R*4][M][K]: gather the four heads of each (m,k).
+    const uint16_t* src = lut + (int64_t)r * (kG * kM * kK);
+    uint2* dst = reinterpret_cast<uint2*>(s_lut);
+    for (int mk = tid; mk < kM * kK; mk += THREADS) {
+      const uint32_t h0 = src[mk], h1 = src[kM * kK + mk];
+      const uint32_t h2 = src[2 * kM * kK + mk], h3 = src[3 * kM * kK + mk];
+      dst[mk] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+    }
+  }
+  if (so.hist) {
+    for (int i = tid; i < 256; i += THREADS) s_hist[i] = 0;
+  }
+  __syncthreads();
+
+  const char* lds = reinterpret_cast<const char*>(s_lut);
+  const uint8_t* crow = codes + (int64_t)b * cs_b + (int64_t)hkv * cs_h;
+  const int t0 = chunk * chunk_tokens;
+  const int t1 = min(T, t0 + chunk_tokens);
+
+  for (int base = t0; base < t1; base += 2 * THREADS) {
+    const int ta = base + tid, tb = base + THREADS + tid;
+    const bool va = ta < t1, vb = tb < t1;
+    uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0, b0 = a0, b1 = a0;
+    if (va) {
+      const uint4* p = reinterpret_cast<const uint4*>(crow + (int64_t)ta * cs_t);
+      a0 = p[0];
+      a1 = p[1];
+    }
+    if (vb) {
+      const uint4* p = reinterpret_cast<const uint4*>(crow + (int64_t)tb * cs_t);
+      b0 = p[0];
+      b1 = p[1];
+    }
+    float x0 = 0.f, x1 = 0.f, x2 = 0.f, x3 = 0.f;
+    float y0 = 0.f, y1 = 0.f, y2 = 0.f, y3 = 0.f;
+    score_token(lds, a0, a1, one, x0, x1, x2, x3);
+    score_token(lds, b0, b1, one, y0, y1, y2, y3);
+
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const bool v = s == 0 ? va : vb;
+      if (!v) continue;
+      const int t = s == 0 ? ta : tb;
+      const float e0 = s == 0 ? x0 : y0, e1 = s == 0 ? x1 : y1;
+      const float e2 = s == 0 ? x2 : y2, e3 = s == 0 ? x3 : y3;
+      if (so.heads) {
+        uint16_t* hp = so.heads + (int64_t)(r * kG) * T + t;
+        hp[0] = f2h(e0);
+        hp[(int64_t)T] = f2h(e1);
+        hp[2 * (int64_t)T] = f2h(e2);
+        hp[3 * (int64_t)T] = f2h(e3);
+      }
+      if (so.keys || so.hist) {
+        // fp16 rounding is monotone, so fp16(max) == max of the fp16 scores.
+        const uint16_t hm = f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
+        const uint32_t key = so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(hm) : f16_key(hm);
+        if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
+        if (so.hist && t >= so.cand_start && t < so.cand_end) atomicAdd(&s_hist[key >> 8], 1u);
+      }
+    }
+  }
+
+  if (so.hist) {
+    __syncthreads();
+    const int nchunk = gridDim.x / R;
+    uint32_t* dst = so.hist + ((int64_t)r * nchunk + chunk) * 256;
+    for (int i = tid; i < 256; i += THREADS) dst[i] = s_hist[i];
+  }
+}
+
+// Generic grouped scorer: G <= 4, any M, K.  Table [G][M][K] fp16 in LDS.
+__global__ __launch_bounds__(256) void score_grouped_generic_kernel(
+    const uint16_t* __restrict__ lut, int lut_layout, const uint8_t* __restrict__ codes,
+    int64_t cs_h, int64_t cs_t, int G, int T, int M, int K, uint16_t* __restrict__ out,
+    _Float16 one) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_tab[];  // [G][M][K]
+  const int hkv = blockIdx.x;
+  const int MK = M * K;
+  for (int i = threadIdx.x; i < G * MK; i += blockDim.x) {
+    uint16_t v;
+    if (lut_layout == LAP_LUT_HMK) {
+      v = lut[(int64_t)hkv * G * MK + i];
+    } else {  // [Hkv][M][K][G] -> [G][M][K]
+      const int g = i / MK, mk = i - g * MK;
+      v = lut[((int64_t)hkv * MK + mk) * G + g];
+    }
+    s_tab[i] = v;
+  }
+  __syncthreads();
+  const uint8_t* crow = codes + (int64_t)hkv * cs_h;
+  for (int t = blockIdx.y * blockDim.x + threadIdx.x; t < T; t += gridDim.y * blockDim.x) {
+    const uint8_t* cp = crow + (int64_t)t * cs_t;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < M; ++m) {
+      const int code = cp[m];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        if (g < G) acc[g] = acc_f16(acc[g], __builtin_bit_cast(_Float16, s_tab[(g * M + m) * K + code]), one);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      if (g < G) out[((int64_t)hkv * G + g) * T + t] = f2h(acc[g]);
+  }
+}
+
+// Per-query-head scorer over an M sub-range, dense or over an index list
+// (reference aq_kernels/aq_lut_gqa.cu:20-76).
+__global__ __launch_bounds__(256) void score_gqa_kernel(
+    const uint16_t* __restrict__ lut, const uint8_t* __restrict__ codes, int64_t cs_h,
+    int64_t cs_t, int G, int T, int N, int M_start, int M_range, int M_stride, int K,
+    const int64_t* __restrict__ indices, uint16_t* __restrict__ out, _Float16 one) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_tab[];  // [M_range][K]
+  const int h = blockIdx.x;
+  const int hkv = h / G;
+  const uint16_t* src = lut + ((int64_t)h * M_stride + M_start) * K;
+  for (int i = threadIdx.x; i < M_range * K; i += blockDim.x) s_tab[i] = src[i];
+  __syncthreads();
+  for (int n = blockIdx.y * blockDim.x + threadIdx.x; n < N; n += gridDim.y * blockDim.x) {
+    int64_t t = n;
+    if (indices) {
+      t = indices[(int64_t)h * N + n];
+      if (t < 0 || t >= T) {
+        out[(int64_t)h * N + n] = 0;
+        continue;
+      }
+    }
+    const uint8_t* cp = codes + (int64_t)hkv * cs_h + t * cs_t + M_start;
+    float acc = 0.f;
+    for (int m = 0; m < M_range; ++m)
+      acc = acc_f16(acc, __builtin_bit_cast(_Float16, s_tab[m * K + cp[m]]), one);
+    out[(int64_t)h * N + n] = f2h(acc);
+  }
+}
+
+template <typename CT>
+__device__ __forceinline__ int code_index(CT v, int K) {
+  int c = (int)(uint8_t)(v);  // low 8 bits as an unsigned code
+  return c >= K ? K - 1 : c;  // c >= 0 by construction
+}
+
+// Non-GQA scorer (reference aq_kernels/aq_lut.cu:581-639).
+template <typename CT, bool F32>
+__global__ __launch_bounds__(256) void score_mha_kernel(const void* __restrict__ lut,
+                                                        const CT* __restrict__ codes, int Q,
+                                                        int N, int M, int K,
+                                                        void* __restrict__ out, _Float16 one) {
+  const int q = blockIdx.x;
+  const int n = blockIdx.y * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const CT* cp = codes + ((int64_t)q * N + n) * M;
+  const int64_t lrow = (int64_t)q * M * K;
+  float acc = 0.f;
+  if (F32) {
+    const float* L = static_cast<const float*>(lut) + lrow;
+    for (int m = 0; m < M; ++m) acc = acc + L[m * K + code_index(cp[m], K)];
+    static_cast<float*>(out)[(int64_t)q * N + n] = acc;
+  } else {
+    const uint16_t* L = static_cast<const uint16_t*>(lut) + lrow;
+    for (int m = 0; m < M; ++m)
+      acc = acc_f16(acc, __builtin_bit_cast(_Float16, L[m * K + code_index(cp[m], K)]), one);
+    static_cast<uint16_t*>(out)[(int64_t)q * N + n] = f2h(acc);
+  }
+}
+
+// Direct scorer without a table (reference aq_kernels/aq_lut.cu:37-149).
+template <typename CT, bool F32>
+__global__ __launch_bounds__(256) void aq_direct_kernel(const void* __restrict__ qv,
+                                                        const void* __restrict__ cbv,
+                                                        const CT* __restrict__ codes, int Q,
+                                                        int N, int M, int K, int D,
+                                                        void* __restrict__ out) {
+  const int q = blockIdx.x;
+  const int n = blockIdx.y * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const CT* cp = codes + ((int64_t)q * N + n) * M;
+  float acc = 0.f;
+  if (F32) {
+    const float* qq = static_cast<const float*>(qv) + (int64_t)q * D;
+    const float* cb = static_cast<const float*>(cbv);
+    for (int m = 0; m < M; ++m) {
+      const int c = (int)(uint8_t)cp[m];
+      if (c >= K) continue;
+      const float* row = cb + ((int64_t)m * K + c) * D;
+      for (int i = 0; i < D; ++i) acc = __builtin_fmaf(qq[i], row[i], acc);
+    }
+    static_cast<float*>(out)[(int64_t)q * N + n] = acc;
+  } else {
+    const _Float16* qq = static_cast<const _Float16*>(qv) + (int64_t)q * D;
+    const _Float16* cb = static_cast<const _Float16*>(cbv);
+    for (int m = 0; m < M; ++m) {
+      const int c = (int)(uint8_t)cp[m];
+      if (c >= K) continue;
+      const _Float16* row = cb + ((int64_t)m * K + c) * D;
+      int i = 0;
+      for (; i + 1 < D; i += 2) {
+        const float p0 = (float)(_Float16)(qq[i] * row[i]);
+        const float p1 = (float)(_Float16)(qq[i + 1] * row[i + 1]);
+        acc = acc + (p0 + p1);
+      }
+      for (; i < D; ++i) acc = acc + (float)qq[i] * (float)row[i];
+    }
+    static_cast<uint16_t*>(out)[(int64_t)q * N + n] = f2h(acc);
+  }
+}
+
+inline _Float16 f16_one() { return (_Float16)1.0f; }
+
+}  // namespace
+
+// Launch the fast G=4 scorer.  Exposed to the fused retrieval entry point.
+int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int64_t cs_b,
+                    int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, uint16_t* heads,
+                    uint16_t* keys, uint32_t* hist, int key_mode, int cand_start,
+                    int cand_end, int* nchunk_out, hipStream_t st) {
+  DevInfo di;
+  int s = device_info(&di);
+  if (s != LAP_OK) return s;
+  const int R = B * Hkv;
+  constexpr int THREADS = 512;
+  const int target_wgs = di.cu_count * score_wg_per_cu();
+  int nchunk = (target_wgs + R - 1) / R;
+  // Tokens per workgroup rounded up to whole passes of the token loop.
+  int chunk_tokens = (T + nchunk - 1) / nchunk;
+  chunk_tokens = (chunk_tokens + 2 * THREADS - 1) / (2 * THREADS) * (2 * THREADS);
+  if (chunk_tokens < 2 * THREADS) chunk_tokens = 2 * THREADS;
+  nchunk = (T + chunk_tokens - 1) / chunk_tokens;
+  if (nchunk < 1) nchunk = 1;
+  ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end};
+  dim3 grid((unsigned)(R * nchunk));
+  if (lut_il)
+    hipLaunchKernelGGL((score_g4_kernel<THREADS, true>), grid, dim3(THREADS), 0, st, lut,
+                       codes, cs_b, cs_h, cs_t, Hkv, R, T, chunk_tokens, so, f16_one());
+  else
+    hipLaunchKernelGGL((score_g4_kernel<THREADS, false>), grid, dim3(THREADS), 0, st, lut,
+                       codes, cs_b, cs_h, cs_t, Hkv, R, T, chunk_tokens, so, f16_one());
+  LAP_LAUNCH_CHECK("score_g4_kernel");
+  if (nchunk_out) *nchunk_out = nchunk;
+  return LAP_OK;
+}
+
+// Number of workgroup chunks launch_score_g4 will use for T tokens, R rows.
+int score_g4_nchunk(int R, int T) {
+  DevInfo di;
+  if (device_info(&di) != LAP_OK) return -1;
+  constexpr int THREADS = 512;
+  const int target_wgs = di.cu_count * score_wg_per_cu();
+  int nchunk = (target_wgs + R - 1) / R;
+  int chunk_tokens = (T + nchunk - 1) / nchunk;
+  chunk_tokens = (chunk_tokens + 2 * THREADS - 1) / (2 * THREADS) * (2 * THREADS);
+  if (chunk_tokens < 2 * THREADS) chunk_tokens = 2 * THREADS;
+  nchunk = (T + chunk_tokens - 1) / chunk_tokens;
+  return nchunk < 1 ? 1 : nchunk;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool score_g4_supported(const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t) {
+  return aligned16(codes) && cs_t % 16 == 0 && cs_h % 16 == 0 && cs_b % 16 == 0;
+}
+
+}  // namespace lap
+
+using namespace lap;
+
+extern "C" int lap_lut_score_grouped(const void* lut, int lut_layout, const uint8_t* codes,
+                                     int64_t codes_stride_h, int64_t codes_stride_t, int Hkv,
+                                     int G, int T, int M, int K, void* out,
+                                     lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(lut && codes && out, "lap_lut_score_grouped: null pointer");
+  LAP_CHECK(lut_layout == LAP_LUT_HMK || lut_layout == LAP_LUT_GMKG,
+            "lap_lut_score_grouped: bad lut layout");
+  LAP_CHECK(G > 0 && G <= 4, "grouped kernel supports G<=4");
+  LAP_CHECK(Hkv > 0 && T >= 0 && M > 0 && K > 0 && K <= 256,
+            "lap_lut_score_grouped: bad sizes Hkv=%d T=%d M=%d K=%d", Hkv, T, M, K);
+  LAP_CHECK(codes_stride_t >= M && codes_stride_h >= 0,
+            "lap_lut_score_grouped: codes strides must cover M");
+  if (T == 0) return LAP_OK;
+  hipStream_t st = as_stream(stream);
+  const uint16_t* L = static_cast<const uint16_t*>(lut);
+  if (G == 4 && M == kM && K == kK && score_g4_supported(codes, 0, codes_stride_h, codes_stride_t)) {
+    return launch_score_g4(L, lut_layout == LAP_LUT_GMKG, codes, 0, codes_stride_h,
+                           codes_stride_t, 1, Hkv, T, static_cast<uint16_t*>(out), nullptr,
+                           nullptr, LAP_KEY_F16, 0, 0, nullptr, st);
+  }
+  DevInfo di;
+  int s = device_info(&di);
+  if (s != LAP_OK) return s;
+  const size_t smem = (size_t)G * M * K * 2;
+  LAP_CHECK_CODE(smem <= (size_t)di.lds_per_block, LAP_ERR_UNSUPPORTED,
+                 "grouped LUT shared-memory request is too large (%zu > %d bytes)", smem,
+                 di.lds_per_block);
+  const int gy = std::min((T + 255) / 256, std::max(1, di.cu_count * 2 / Hkv));
+  hipLaunchKernelGGL(score_grouped_generic_kernel, dim3(Hkv, gy), dim3(256), smem, st, L,
+                     lut_layout, codes, codes_stride_h, codes_stride_t, G, T, M, K,
+                     static_cast<uint16_t*>(out), f16_one());
+  LAP_LAUNCH_CHECK("score_grouped_generic_kernel");
+  return LAP_OK;
+}
+
+extern "C" int lap_lut_score_gqa(const void* lut, const uint8_t* codes, int64_t codes_stride_h,
+                                 int64_t codes_stride_t, int Hkv, int G, int T, int M_stride,
+                                 int K, int M_start, int M_end, const int64_t* indices, int N,
+                                 void* out, lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(lut && codes && out, "lap_lut_score_gqa: null pointer");
+  LAP_CHECK(G > 0 && Hkv > 0, "H must equal Hkv * G");
+  LAP_CHECK(M_end <= M_stride && M_start >= 0 && M_end - M_start > 0,
+            "lap_lut_score_gqa: bad M range [%d,%d) of %d", M_start, M_end, M_stride);
+  LAP_CHECK(K > 0 && K <= 256, "lap_lut_score_gqa: K=%d out of range", K);
+  LAP_CHECK(T >= 0 && N >= 0, "lap_lut_score_gqa: negative size");
+  if (!indices) LAP_CHECK(N == T, "lap_lut_score_gqa: dense mode needs N == T");
+  if (N == 0) return LAP_OK;
+  DevInfo di;
+  int s = device_info(&di);
+  if (s != LAP_OK) return s;
+  const int M_range = M_end - M_start;
+  const size_t smem = (size_t)M_range * K * 2;
+  LAP_CHECK_CODE(smem <= (size_t)di.lds_per_block, LAP_ERR_UNSUPPORTED,
+                 "lap_lut_score_gqa: table of %zu bytes exceeds LDS", smem);
+  const int H = Hkv * G;
+  const int gy = std::min((N + 255) / 256, std::max(1, di.cu_count * 4 / H));
+  hipLaunchKernelGGL(score_gqa_kernel, dim3(H, gy), dim3(256), smem, as_stream(stream),
+                     static_cast<const uint16_t*>(lut), codes, codes_stride_h, codes_stride_t, G,
+                     T, N, M_start, M_range, M_stride, K, indices,
+                     static_cast<uint16_t*>(out), f16_one());
+  LAP_LAUNCH_CHECK("score_gqa_kernel");
+  return LAP_OK;
+}
+
+extern "C" int lap_lut_score_mha(const void* lut, int lut_dtype, const void* codes,
+                                 int codes_dtype, int Q, int N, int M, int K, void* out,
+                                 lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(lut && codes && out, "lap_lut_score_mha: null pointer");
+  LAP_CHECK(lut_dtype == LAP_DTYPE_F16 || lut_dtype == LAP_DTYPE_F32, "lut must be fp16 or fp32");
+  LAP_CHECK(codes_dtype == LAP_DTYPE_U8 || codes_dtype == LAP_DTYPE_I8 ||
+                codes_dtype == LAP_DTYPE_I64,
+            "codes must be int64 (Long) or uint8 (Byte) or int8 (Char)");
+  LAP_CHECK(Q > 0 && M > 0 && K > 0 && N >= 0, "lap_lut_score_mha: bad sizes");
+  if (N == 0) return LAP_OK;
+  dim3 grid(Q, (N + 255) / 256);
+  hipStream_t st = as_stream(stream);
+  const bool f32 = lut_dtype == LAP_DTYPE_F32;
+#define LAP_MHA(CT)                                                                          \
+  do {                                                                                       \
+    if (f32)                                                                                 \
+      hipLaunchKernelGGL((score_mha_kernel<CT, true>), grid, dim3(256), 0, st, lut,          \
+                         static_cast<const CT*>(codes), Q, N, M, K, out, f16_one());         \
+    else                                                                                     \
+      hipLaunchKernelGGL((score_mha_kernel<CT, false>), grid, dim3(256), 0, st, lut,         \
+                         static_cast<const CT*>(codes), Q, N, M, K, out, f16_one());         \
+  } while (0)
+  if (codes_dtype == LAP_DTYPE_U8) LAP_MHA(uint8_t);
+  else if (codes_dtype == LAP_DTYPE_I8) LAP_MHA(int8_t);
+  else LAP_MHA(int64_t);
+#undef LAP_MHA
+  LAP_LAUNCH_CHECK("score_mha_kernel");
+  return LAP_OK;
+}
+
+extern "C" int lap_aq_lut_direct(const void* q, const void* codebooks, int dtype,
+                                 const void* codes, int codes_dtype, int Q, int N, int M, int K,
+                                 int D, void* out, lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(q && codebooks && codes && out, "lap_aq_lut_direct: null pointer");
+  LAP_CHECK(dtype == LAP_DTYPE_F32 || dtype == LAP_DTYPE_F16,
+            "lap_aq_lut_direct: dtype must be fp32 or fp16");
+  LAP_CHECK(codes_dtype == LAP_DTYPE_U8 || codes_dtype == LAP_DTYPE_I8 ||
+                codes_dtype == LAP_DTYPE_I64,
+            "codes must be int64 (Long) or uint8 (Byte) or int8 (Char)");
+  LAP_CHECK(Q > 0 && M > 0 && K > 0 && D > 0 && N >= 0, "lap_aq_lut_direct: bad sizes");
+  if (N == 0) return LAP_OK;
+  dim3 grid(Q, (N + 255) / 256);
+  hipStream_t st = as_stream(stream);
+  const bool f32 = dtype == LAP_DTYPE_F32;
+#define LAP_DIRECT(CT)                                                                       \
+  do {                                                                                       \
+    if (f32)                                                                                 \
+      hipLaunchKernelGGL((aq_direct_kernel<CT, true>), grid, dim3(256), 0, st, q, codebooks, \
+                         static_cast<const CT*>(codes), Q, N, M, K, D, out);                 \
+    else                                                                                     \
+      hipLaunchKernelGGL((aq_direct_kernel<CT, false>), grid, dim3(256), 0, st, q,           \
+                         codebooks, static_cast<const CT*>(codes), Q, N, M, K, D, out);      \
+  } while (0)
+  if (codes_dtype == LAP_DTYPE_U8) LAP_DIRECT(uint8_t);
+  else if (codes_dtype == LAP_DTYPE_I8) LAP_DIRECT(int8_t);
+  else LAP_DIRECT(int64_t);
+#undef LAP_DIRECT
+  LAP_LAUNCH_CHECK("aq_direct_kernel");
+  return LAP_OK;
+}

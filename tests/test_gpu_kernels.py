@@ -1,0 +1,309 @@
+"""GPU parity of every kernel against the CPU oracle (bit-exact unless stated).
+
+All calls go through the C ABI (via the torch-facing wrappers of
+laprune_amd.aq_kernels, which only marshal pointers).  Inputs are seeded.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _np_u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def K(dev):
+    from laprune_amd import aq_kernels as K
+    for name in K.REFERENCE_NAMES:
+        assert getattr(K, name) is not None, name
+    return K
+
+
+# ------------------------------------------------------------------ A1 LUT
+
+@pytest.mark.parametrize("qdt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("layout", ["hmk", "gmkg"])
+def test_lut_build_bit_exact(dev, K, orc, qdt, layout):
+    g = _gen(1)
+    q = torch.randn(32, 128, generator=g).to(qdt)
+    cb = torch.randn(32, 256, 128, generator=g) * 0.02
+    lut = K.aq_lut_build(q.to(dev), cb.to(dev), G=4, layout=layout)
+    torch.cuda.synchronize()
+    want = orc.lut_build(q.float().numpy(), cb.numpy())
+    if layout == "gmkg":
+        want = orc.lut_to_gmkg(want, 4)
+    got = _np_u16(lut)
+    assert got.shape == want.shape
+    assert np.array_equal(got, want)
+
+
+def test_lut_build_odd_shapes(dev, K, orc):
+    g = _gen(2)
+    q = torch.randn(5, 64, generator=g)
+    cb = torch.randn(3, 37, 64, generator=g) * 0.1
+    lut = K.aq_lut_build(q.to(dev), cb.to(dev))
+    assert np.array_equal(_np_u16(lut), orc.lut_build(q.numpy(), cb.numpy()))
+
+
+# --------------------------------------------------------------- A2 scores
+
+def _codes_view(g, Hkv, T, M=32, cap=0):
+    buf = torch.randint(0, 256, (Hkv, T + cap, M), generator=g, dtype=torch.uint8)
+    return buf, buf[:, :T, :]
+
+
+@pytest.mark.parametrize("T,cap", [(1, 0), (1000, 0), (8192, 128), (20000, 64)])
+@pytest.mark.parametrize("layout", ["hmk", "gmkg"])
+def test_score_grouped_fast_path(dev, K, orc, T, cap, layout):
+    from laprune_amd import _native as N
+    g = _gen(3 + T)
+    lut16 = (torch.randn(32, 32, 256, generator=g) * 0.3).half()
+    buf, view = _codes_view(g, 8, T, cap=cap)
+    dbuf = buf.to(dev)
+    dview = dbuf[:, :T, :]
+    if layout == "hmk":
+        out = K.aq_lut_gather_grouped(lut16.to(dev), dview, 4)
+    else:
+        lut_il = lut16.view(8, 4, 32, 256).permute(0, 2, 3, 1).contiguous().to(dev)
+        out = torch.empty(32, T, dtype=torch.float16, device=dev)
+        N.call("lap_lut_score_grouped", N.ptr(lut_il), N.LUT_GMKG, N.ptr(dview), dview.stride(0),
+               dview.stride(1), 8, 4, T, 32, 256, N.ptr(out), N.stream_of(out))
+    torch.cuda.synchronize()
+    want = orc.score_grouped(_np_u16(lut16), view.numpy(), 4)
+    assert np.array_equal(_np_u16(out), want)
+
+
+@pytest.mark.parametrize("G,M,Kc", [(2, 32, 256), (3, 16, 128), (4, 24, 256), (1, 8, 64)])
+def test_score_grouped_generic(dev, K, orc, G, M, Kc):
+    g = _gen(10 + G)
+    Hkv, T = 3, 777
+    lut16 = (torch.randn(Hkv * G, M, Kc, generator=g) * 0.3).half()
+    codes = torch.randint(0, Kc, (Hkv, T, M), generator=g, dtype=torch.uint8)
+    out = K.aq_lut_gather_grouped(lut16.to(dev), codes.to(dev), G)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np_u16(out), orc.score_grouped(_np_u16(lut16), codes.numpy(), G))
+
+
+@pytest.mark.parametrize("with_idx", [False, True])
+@pytest.mark.parametrize("mrange", [(0, 32), (8, 24)])
+def test_score_gqa(dev, K, orc, with_idx, mrange):
+    g = _gen(20)
+    Hkv, G, T = 2, 4, 3000
+    lut16 = (torch.randn(Hkv * G, 32, 256, generator=g) * 0.3).half()
+    buf, view = _codes_view(g, Hkv, T, cap=50)
+    idx = None
+    if with_idx:
+        idx = torch.randint(-5, T + 5, (Hkv * G, 300), generator=g, dtype=torch.int64)
+    out = K.aq_lut_gather_gqa(lut16.to(dev), buf.to(dev)[:, :T, :], G, mrange[0], mrange[1],
+                              None if idx is None else idx.to(dev))
+    torch.cuda.synchronize()
+    want = orc.score_gqa(_np_u16(lut16), view.numpy(), G, mrange[0], mrange[1],
+                         None if idx is None else idx.numpy())
+    assert np.array_equal(_np_u16(out), want)
+
+
+@pytest.mark.parametrize("lut_dt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("code_dt", [torch.uint8, torch.int8, torch.int64])
+def test_score_mha(dev, K, orc, lut_dt, code_dt):
+    g = _gen(30)
+    Q, n, M, Kc = 5, 999, 32, 200
+    lut = (torch.randn(Q, M * Kc, generator=g) * 0.3).to(lut_dt)
+    if code_dt == torch.int64:
+        codes = torch.randint(-300, 600, (Q, n, M), generator=g, dtype=torch.int64)
+    else:
+        codes = torch.randint(-128 if code_dt == torch.int8 else 0,
+                              128 if code_dt == torch.int8 else 256, (Q, n, M), generator=g,
+                              dtype=torch.int64).to(code_dt)
+    out = K.aq_lut_gather_forward(lut.to(dev), codes.to(dev))
+    torch.cuda.synchronize()
+    f32 = lut_dt == torch.float32
+    want = orc.score_mha(lut.numpy() if f32 else _np_u16(lut), codes.numpy(), f32)
+    got = out.cpu().numpy() if f32 else _np_u16(out)
+    assert np.array_equal(got.view(np.uint32) if f32 else got, want.view(np.uint32) if f32 else want)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_aq_lut_direct(dev, K, orc, dt):
+    g = _gen(40)
+    Q, n, M, Kc, D = 3, 300, 8, 64, 128
+    q = torch.randn(Q, D, generator=g).to(dt)
+    cb = (torch.randn(M, Kc, D, generator=g) * 0.05).to(dt)
+    codes = torch.randint(0, 80, (Q, n, M), generator=g, dtype=torch.int64)
+    out = K.aq_lut_forward(q.to(dev), cb.to(dev), codes.to(dev))
+    torch.cuda.synchronize()
+    if dt == torch.float32:
+        want = orc.aq_direct(q.numpy(), cb.numpy(), codes.numpy(), False)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    else:
+        want = orc.aq_direct(_np_u16(q), _np_u16(cb), codes.numpy(), True)
+        assert np.array_equal(_np_u16(out), want)
+
+
+# ---------------------------------------------------------------- A3 top-k
+
+@pytest.mark.parametrize("group,key_dt", [(1, torch.float16), (4, torch.float16),
+                                          (4, torch.bfloat16), (1, torch.bfloat16)])
+@pytest.mark.parametrize("T,cs,ce,k", [(8192, 0, 8128, 163), (8192, 4, 8128, 2048),
+                                       (5000, 10, 4990, 5000), (70000, 0, 70000, 1),
+                                       (3000, 0, 3000, 2999)])
+def test_topk(dev, K, orc, group, key_dt, T, cs, ce, k):
+    g = _gen(50 + T + k)
+    R = 3
+    # coarse values to force many ties
+    s = (torch.randn(R * group, T, generator=g) * 4).round().half() / 4
+    idx = K.aq_topk(s.to(dev), k, group=group, cand_start=cs, cand_end=ce, key_dtype=key_dt)
+    torch.cuda.synchronize()
+    bits = _np_u16(s)
+    want = orc.topk(bits, k, group, cs, ce, key_bf16=key_dt == torch.bfloat16)
+    want2 = orc.topk_numpy(bits, k, group, cs, ce, key_bf16=key_dt == torch.bfloat16)
+    assert np.array_equal(want, want2)
+    assert np.array_equal(idx.cpu().numpy(), want)
+
+
+def test_topk_all_equal_and_int32(dev, K, orc):
+    s = torch.zeros(2, 4096, dtype=torch.float16)
+    s[1] = -0.0
+    idx = K.aq_topk(s.to(dev), 100, cand_start=7, cand_end=4000, index_dtype=torch.int32)
+    torch.cuda.synchronize()
+    assert idx.dtype == torch.int32
+    assert np.array_equal(idx.cpu().numpy(), np.tile(np.arange(7, 107), (2, 1)))
+
+
+@pytest.mark.parametrize("T,k,key_dt", [(8192, 2048, torch.float16), (131072, 2048, torch.float16),
+                                        (131072, 2621, torch.bfloat16), (4096, 5000, torch.float16)])
+def test_retrieve_topk_fused(dev, K, orc, T, k, key_dt):
+    g = _gen(60 + T)
+    Hkv, cap = 8, 128
+    q = torch.randn(32, 128, generator=g).bfloat16()
+    cb = torch.randn(32, 256, 128, generator=g) * 0.02
+    buf = torch.randint(0, 256, (1, Hkv, T + cap, 32), generator=g, dtype=torch.uint8)
+    dbuf = buf.to(dev)
+    codes = dbuf[:, :, :T, :]
+    lut = K.aq_lut_build(q.to(dev), cb.to(dev), G=4, layout="gmkg")
+    cs, ce = orc.candidate_window(T, T, 4, 64)
+    idx, scores = K.aq_retrieve_topk(lut, codes, k, cs, ce, key_dtype=key_dt, return_scores=True)
+    torch.cuda.synchronize()
+    lut_hmk = orc.lut_build(q.float().numpy(), cb.numpy())
+    want_s = orc.score_grouped(lut_hmk, buf[0, :, :T, :].numpy(), 4)
+    assert np.array_equal(_np_u16(scores[0]), want_s)
+    want_i = orc.topk(want_s, k, group=4, cand_start=cs, cand_end=ce,
+                      key_bf16=key_dt == torch.bfloat16)
+    assert np.array_equal(idx[0].cpu().numpy().astype(np.int64), want_i)
+
+
+# --------------------------------------------------------------- A4 gather
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("tail", [None, (40, 24)])
+def test_gqa_gather_kv(dev, K, orc, dt, tail):
+    g = _gen(70)
+    B, Hkv, T, D, G, n = 2, 2, 100, 128, 4, 17
+    buf_k = torch.randn(B, Hkv, T + 28, D, generator=g).to(dt)
+    buf_v = torch.randn(B, Hkv, T + 28, D, generator=g).to(dt)
+    idx = torch.randint(0, T, (B, Hkv * G, n), generator=g, dtype=torch.int64)
+    dk, dv = buf_k.to(dev)[:, :, :T], buf_v.to(dev)[:, :, :T]
+    if tail is None:
+        ok, ov = K.gqa_gather_kv(dk, dv, idx.to(dev), G)
+        full = idx.numpy()
+    else:
+        ok, ov = K.gqa_gather_kv_with_tail(dk, dv, idx.to(dev), G, tail[0], tail[1])
+        t_idx = np.broadcast_to(np.arange(tail[0], tail[0] + tail[1]), (B, Hkv * G, tail[1]))
+        full = np.concatenate([idx.numpy(), t_idx], axis=2)
+    torch.cuda.synchronize()
+    want_k = orc.gather_rows(buf_k[:, :, :T].float().numpy(), full, G)
+    want_v = orc.gather_rows(buf_v[:, :, :T].float().numpy(), full, G)
+    assert np.array_equal(ok.float().cpu().numpy(), want_k)
+    assert np.array_equal(ov.float().cpu().numpy(), want_v)
+
+
+def test_gqa_gather_out_of_range_rows_untouched(dev, K):
+    B, Hkv, T, D = 1, 1, 10, 64
+    k = torch.randn(B, Hkv, T, D, device=dev, dtype=torch.float16)
+    idx = torch.tensor([[[0, -1, 10, 3]]], dtype=torch.int64, device=dev)
+    ok, ov = K.gqa_gather_kv(k, k, idx, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(ok[0, 0, 0], k[0, 0, 0]) and torch.equal(ok[0, 0, 3], k[0, 0, 3])
+
+
+# ---------------------------------------------------------- A5 attention
+
+def _rel(a, b):
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-6))
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("per_head", [False, True])
+@pytest.mark.parametrize("D", [128, 64])
+def test_sparse_attn_decode(dev, K, orc, dt, per_head, D):
+    g = _gen(80 + D)
+    B, Hq, Hkv, T, n = 2, 8, 2, 3000, 300
+    q = torch.randn(B, Hq, 1, D, generator=g).to(dt)
+    kk = torch.randn(B, Hkv, T + 16, D, generator=g).to(dt)
+    vv = torch.randn(B, Hkv, T + 16, D, generator=g).to(dt)
+    H_idx = Hq if per_head else Hkv
+    idx = torch.randint(4, T - 64, (B, H_idx, n), generator=g, dtype=torch.int64)
+    out = K.sparse_attn_decode(q.to(dev), kk.to(dev)[:, :, :T], vv.to(dev)[:, :, :T],
+                               idx.to(dev), sink=4, tail_start=T - 64, tail_count=64)
+    torch.cuda.synchronize()
+    G = Hq // Hkv
+
+    def keep(b, h):
+        row = h if per_head else h // G
+        return np.concatenate([idx[b, row].numpy(), np.arange(4), np.arange(T - 64, T)])
+
+    want = orc.attn_decode_f64(q[:, :, 0].double().numpy(), kk[:, :, :T].double().numpy(),
+                               vv[:, :, :T].double().numpy(), keep)
+    assert _rel(out[:, :, 0].double().cpu().numpy(), want) < 1e-2
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 5000, 131072])
+def test_dense_attn_decode(dev, K, orc, T):
+    g = _gen(90 + T)
+    B, Hq, Hkv, D = 1, 32, 8, 128
+    q = torch.randn(B, Hq, 1, D, generator=g).bfloat16()
+    kk = torch.randn(B, Hkv, T, D, generator=g).bfloat16()
+    vv = torch.randn(B, Hkv, T, D, generator=g).bfloat16()
+    out = K.dense_attn_decode(q.to(dev), kk.to(dev), vv.to(dev))
+    torch.cuda.synchronize()
+    want = orc.attn_decode_f64(q[:, :, 0].double().numpy(), kk.double().numpy(),
+                               vv.double().numpy(), lambda b, h: np.arange(T))
+    assert _rel(out[:, :, 0].double().cpu().numpy(), want) < 1e-2
+
+
+# --------------------------------------------------------------- A6 encode
+
+@pytest.mark.parametrize("N,D", [(512, 128), (37, 64), (3, 256)])
+def test_encode_bit_exact(dev, K, orc, N, D):
+    g = _gen(100 + N)
+    M, Kc = 32, 256
+    x = torch.randn(N, D, generator=g) * (torch.rand(D, generator=g) * 3.5 + 0.5)
+    cb = torch.randn(M, Kc, D, generator=g) * 0.02
+    codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
+    torch.cuda.synchronize()
+    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
+    assert np.array_equal(codes.cpu().numpy(), want_c)
+    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+
+
+def test_fused_linear_encode_dropin(dev, K, orc):
+    g = _gen(110)
+    M, Kc, D, N = 32, 256, 128, 64
+    cb = torch.randn(M, Kc, D, generator=g) * 0.02
+    x = torch.randn(N, D, generator=g)
+    cbh = cb.half()
+    weight_t = cbh.transpose(1, 2).contiguous()
+    bias = (-0.5 * cbh.float().pow(2).sum(-1)).half()
+    codes = K.fused_linear_encode_forward(x.half().to(dev), weight_t.to(dev), bias.to(dev),
+                                          cbh.to(dev), True, 0)
+    torch.cuda.synchronize()
+    want, _ = orc.encode(x.half().float().numpy(), cbh.float().numpy())
+    assert codes.dtype == torch.uint8 and np.array_equal(codes.cpu().numpy(), want)
