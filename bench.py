@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode-time retrieval path on one MI355X.
+
+Metric: "GQA LUT-score GB/s (%HBM peak) @128k ctx; sparse
+decode step us vs dense".  Workload = configs[1] (C2): one layer of
+Llama-3.1-8B geometry (32 query / 8 KV heads, head_dim 128), batch 1,
+131072-token context, AQ codes uint8 uniform [8, 131072, 32] (strided views
+of a [.., 131072 + 128, 32] capacity buffer, as the reference's decode cache),
+codebooks fp32 N(0, 0.02) [32, 256, 128], query bf16 N(0, 1), K/V bf16 N(0, 1);
+selection = top-2048 per KV group on the max of its 4 query-head scores,
+plus 4 sink and 64 local tokens.
+
+One step = LUT build -> fused score (+ level-1 histogram) -> radix top-k ->
+sparse attention over the kept rows read in place from the cache, captured
+in a HIP graph.  Twelve code/query sets and four K/V sets (~2.5 GB) rotate
+so that the 256 MB Infinity Cache cannot serve the step from cache.
+
+``value``        code bytes / average duration of the fused scorer kernel,
+                 timed with HIP events around graph replays on the launch
+                 stream (inside the timed region's second half).
+``ms_per_step``  wall time of one full sparse decode step.
+``dense_step_us`` the same GPU's split-K flash-decode over all 131072 tokens.
+``cpu_baseline`` the reference's fp32 PyTorch scoring + bf16 cast + top-k
+                 path (restated in oracle/ref_path.py) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "GQA LUT-score GB/s (%HBM peak) @128k ctx; sparse decode step µs vs dense"
+HBM_PEAK_GBS = 8000.0
+T, HQ, HKV, D, M, K = 131072, 32, 8, 128, 32, 256
+CAP = 128            # extra capacity rows, as the reference's decode cache
+TOPK, SINK, LOCAL = 2048, 4, 64
+N_CODE_SETS, N_KV_SETS = 12, 4
+CODE_BYTES = HKV * T * M  # 33,554,432 algorithmic bytes per scorer launch
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="budget for the CPU baseline sample")
+    ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    return ap.parse_args()
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Time the reference's fp32 CPU path (restated) at T = 131072, top-2048."""
+    import torch
+    from oracle import ref_path
+    ncpu = os.cpu_count() or 1
+    torch.set_num_threads(ncpu)
+    g = torch.Generator().manual_seed(123)
+    q = torch.randn(HQ, D, generator=g).bfloat16().float()
+    cb = torch.randn(M, K, D, generator=g) * 0.02
+    codes = torch.randint(0, 256, (HKV, T, M), generator=g, dtype=torch.uint8)
+
+    def one():
+        s = ref_path.scores_fp32(q, cb, codes, HQ // HKV)
+        return ref_path.select_topk(s, torch.bfloat16, T, sink=SINK, local=LOCAL, k=TOPK)
+
+    for _ in range(3):
+        one()
+    ts = []
+    t_end = time.perf_counter() + seconds
+    while len(ts) < 10 or (time.perf_counter() < t_end and len(ts) < 30):
+        t0 = time.perf_counter()
+        one()
+        ts.append(time.perf_counter() - t0)
+    med = sorted(ts)[len(ts) // 2]
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(CODE_BYTES / med / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"3 warm-up + {len(ts)} timed calls (median {med * 1e3:.1f} ms) of the "
+                   "reference fp32 PyTorch path restated in oracle/ref_path.py: einsum LUT, "
+                   "int64 gather + sum over 32 codebooks for 32 q heads x 131072 tokens, "
+                   f"bf16 cast, top-{TOPK} per head; host CPU: {model or 'unknown'}"),
+    }
+
+
+def traffic_from_profile() -> dict | None:
+    p = ROOT / "profiles" / "score_g4_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: the retrieval path has no cross-GPU exchange "
+              f"in this build (asked for --gpus {args.gpus}, WORLD_SIZE={world}).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from laprune_amd import _native as N
+    from laprune_amd.retrieval import DenseDecoder, RetrievalConfig, SparseDecoder
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    N.lib()
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    log("allocating inputs")
+    codes_sets = [torch.randint(0, 256, (1, HKV, T + CAP, M), generator=g,
+                                dtype=torch.uint8).to(dev) for _ in range(N_CODE_SETS)]
+    q_sets = [torch.randn(1, HQ, 1, D, generator=g).bfloat16().to(dev)
+              for _ in range(N_CODE_SETS)]
+    kv_sets = []
+    for _ in range(N_KV_SETS):
+        kk = torch.randn(1, HKV, T + CAP, D, dtype=torch.bfloat16, device=dev)
+        vv = torch.randn(1, HKV, T + CAP, D, dtype=torch.bfloat16, device=dev)
+        kv_sets.append((kk, vv))
+    cb = (torch.randn(M, K, D, generator=g) * 0.02).to(dev)
+
+    cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=TOPK, select="group",
+                          score_dtype=torch.bfloat16)
+    dec = SparseDecoder(cb, 1, HQ, HKV, D, T, cfg)
+    dense = DenseDecoder(1, HQ, HKV, D, T, dev)
+
+    def sparse_step(i):
+        kk, vv = kv_sets[i % N_KV_SETS]
+        c = codes_sets[i % N_CODE_SETS]
+        return dec.step(q_sets[i % N_CODE_SETS], c[:, :, :T], kk[:, :, :T], vv[:, :, :T])
+
+    def dense_step(i):
+        kk, vv = kv_sets[i % N_KV_SETS]
+        return dense.step(q_sets[i % N_CODE_SETS], kk[:, :, :T], vv[:, :, :T])
+
+    plan = dec.plan(T, T)
+    ws = dec.ws_sel
+
+    def score_only(i):
+        c = codes_sets[i % N_CODE_SETS][:, :, :T]
+        N.call("lap_retrieve_score", N.ptr(dec.lut), N.ptr(c), c.stride(0), c.stride(1),
+               c.stride(2), 1, HKV, T, plan["cand_start"], plan["cand_end"], N.KEY_BF16, None,
+               N.ptr(ws), ws.numel(), N.stream_of(c))
+
+    log("warm-up")
+    for i in range(max(args.warmup, 2)):
+        sparse_step(i)
+        dense_step(i)
+    torch.cuda.synchronize()
+
+    # Capture: one graph per input set (the sets rotate step by step).
+    n_sets = N_CODE_SETS
+    if args.eager:
+        run_sparse = sparse_step
+        run_dense = dense_step
+    else:
+        log("capturing graphs")
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(2):
+                sparse_step(i)
+                dense_step(i)
+                score_only(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        sg, dg = [], []
+        for j in range(n_sets):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                sparse_step(j)
+            sg.append(gph)
+        for j in range(N_KV_SETS):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                dense_step(j)
+            dg.append(gph)
+        run_sparse = lambda i: sg[i % n_sets].replay()  # noqa: E731
+        run_dense = lambda i: dg[i % N_KV_SETS].replay()  # noqa: E731
+    for i in range(args.warmup):
+        run_sparse(i)
+        run_dense(i)
+    torch.cuda.synchronize()
+
+    # ---- timed region 1: K full sparse decode steps
+    log(f"timing {args.steps} sparse steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run_sparse(i)
+    torch.cuda.synchronize()
+    sparse_s = (time.perf_counter() - t0) / args.steps
+
+    # ---- timed region 2: K dense decode steps on the same GPU
+    log(f"timing {args.steps} dense steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run_dense(i)
+    torch.cuda.synchronize()
+    dense_s = (time.perf_counter() - t0) / args.steps
+
+    # ---- scorer kernel duration: HIP events on the launch stream around a
+    # graph of back-to-back scorer launches over the rotating code sets.
+    log("timing the scorer kernel")
+    reps = max(1, args.steps // n_sets)
+    stream = torch.cuda.current_stream()
+    if args.eager:
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for i in range(reps * n_sets):
+            score_only(i)
+        ev1.record(stream)
+    else:
+        gsc = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gsc):
+            for j in range(n_sets):
+                score_only(j)
+        gsc.replay()
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(reps):
+            gsc.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    score_us = ev0.elapsed_time(ev1) * 1e3 / (reps * n_sets)
+    score_gbs = CODE_BYTES / (score_us * 1e-6) / 1e9
+
+    # correctness guard: the selected index sets are valid and the right size
+    sparse_step(0)
+    torch.cuda.synchronize()
+    sel = dec.selected()
+    ok = bool(sel.shape[-1] == TOPK and int(sel.min()) >= plan["cand_start"]
+              and int(sel.max()) < plan["cand_end"])
+
+    traffic = traffic_from_profile()
+    result = {
+        "metric": METRIC,
+        "value": round(score_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sparse_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": ("C2: 1 layer, Llama-3.1-8B attention geometry (32 q / 8 kv heads, "
+                         "head_dim 128), batch 1, 131072-token context; u8 AQ codes "
+                         "[8,131072,32], 32x256 fp32 codebooks, fp16 LUT, fp32 accumulate; "
+                         "top-2048 per KV group (group max) + 4 sink + 64 local; bf16 K/V"),
+            "context": T, "batch": 1, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
+            "codebooks": M, "entries": K, "topk": TOPK, "sink": SINK, "local": LOCAL,
+            "graphs": not args.eager,
+        },
+        "hbm_frac": round(score_gbs / HBM_PEAK_GBS, 4),
+        "sparse_step_us": round(sparse_s * 1e6, 2),
+        "dense_step_us": round(dense_s * 1e6, 2),
+        "speedup_vs_dense": round(dense_s / sparse_s, 3),
+        "dense_hbm_gbs": round(2 * HKV * T * D * 2 / dense_s / 1e9, 1),
+        "score_kernel_us": round(score_us, 3),
+        "selection_check": ok,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(score_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(score_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -158,6 +158,19 @@ int lap_topk_select(const void* scores, int64_t score_row_stride,
  * per-head fp16 scores are written when scores_out != NULL ([Hkv*4][T]).
  * R = B*Hkv rows; codes row r = (b, hkv) at codes + b*cs_b + hkv*cs_h. */
 int lap_retrieve_workspace_size(int R, int T, size_t* bytes);
+/* The two halves of lap_retrieve_topk, for callers that time or overlap them:
+ * lap_retrieve_score runs the scorer and leaves group keys and level-1
+ * histograms in the workspace; lap_retrieve_select (same workspace, same
+ * B/Hkv/T/window, on the same stream afterwards) emits the indices. */
+int lap_retrieve_score(const void* lut_gmkg, const uint8_t* codes,
+                       int64_t codes_stride_b, int64_t codes_stride_h,
+                       int64_t codes_stride_t, int B, int Hkv, int T,
+                       int cand_start, int cand_end, int key_mode,
+                       void* scores_out, void* workspace, size_t workspace_bytes,
+                       lap_stream_t stream);
+int lap_retrieve_select(int B, int Hkv, int T, int cand_start, int cand_end, int k,
+                        void* out_idx, int out_dtype, void* workspace,
+                        size_t workspace_bytes, lap_stream_t stream);
 int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
                       int64_t codes_stride_b, int64_t codes_stride_h,
                       int64_t codes_stride_t, int B, int Hkv, int T,

@@ -57,6 +57,8 @@ SIGNATURES = {
     "lap_retrieve_workspace_size": [i32, i32, psz],
     "lap_retrieve_topk": [vp, vp, i64, i64, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp,
                           i32, vp, sz, vp],
+    "lap_retrieve_score": [vp, vp, i64, i64, i64, i32, i32, i32, i32, i32, i32, vp, vp, sz, vp],
+    "lap_retrieve_select": [i32, i32, i32, i32, i32, i32, vp, i32, vp, sz, vp],
     "lap_gqa_gather_kv": [vp, vp, i32, i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, vp,
                           i32, i32, i32, i32, vp, vp, vp],
     "lap_attn_decode_workspace_size": [i32, i32, i32, i32, psz],

@@ -247,26 +247,54 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 }
 
 // Merge split partials: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// One workgroup per (b, h).  Split weights are formed once in LDS; each
+// output dim is then summed by 256/D threads over interleaved splits with
+// independent loads, and the partial sums are folded through LDS.
 template <int DT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part,
                                                            int nsplit, int D,
                                                            uint16_t* __restrict__ out) {
+  __shared__ float s_w[1024];
+  __shared__ float s_red[8];
+  __shared__ float s_acc[256];
   const int bh = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* pp = part + (int64_t)bh * nsplit * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pp[s * (D + 2)]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float l = 0.f, acc = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < nsplit; ++s) {
-        const float ms = pp[s * (D + 2)];
-        if (ms == -INFINITY) continue;
-        const float w = exp2f(ms - M);
-        l += pp[s * (D + 2) + 1] * w;
-        acc += pp[s * (D + 2) + 2 + d] * w;
-      }
-    }
-    out[(int64_t)bh * D + d] = st16<DT>(l > 0.f ? acc / l : 0.f);
+  // block max of m_s
+  float mx = -INFINITY;
+  for (int s = tid; s < nsplit; s += 256) mx = fmaxf(mx, pp[(int64_t)s * (D + 2)]);
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+  if (lane == 0) s_red[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  float lsum = 0.f;
+  for (int s = tid; s < nsplit; s += 256) {
+    const float ms = pp[(int64_t)s * (D + 2)];
+    const float w = (ms == -INFINITY || M == -INFINITY) ? 0.f : exp2f(ms - M);
+    s_w[s] = w;
+    lsum += pp[(int64_t)s * (D + 2) + 1] * w;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) lsum += __shfl_xor(lsum, d, 64);
+  __syncthreads();
+  if (lane == 0) s_red[4 + wave] = lsum;
+  __syncthreads();
+  const float l = s_red[4] + s_red[5] + s_red[6] + s_red[7];
+  const int P = 256 / D;  // threads per output dim
+  const int d = tid % D, part_id = tid / D;
+  float acc = 0.f;
+  if (part_id < P) {
+#pragma unroll 8
+    for (int s = part_id; s < nsplit; s += P)
+      acc = __builtin_fmaf(pp[(int64_t)s * (D + 2) + 2 + d], s_w[s], acc);
+  }
+  s_acc[tid] = acc;
+  __syncthreads();
+  if (tid < D) {
+    float sum = 0.f;
+    for (int p2 = 0; p2 < P; ++p2) sum += s_acc[p2 * D + tid];
+    out[(int64_t)bh * D + tid] = st16<DT>(l > 0.f ? sum / l : 0.f);
   }
 }
 
@@ -274,7 +302,7 @@ int choose_nsplit(int rows, int L) {
   DevInfo di;
   if (device_info(&di) != LAP_OK) return -1;
   const int max_split = (L + kTile - 1) / kTile;
-  int ns = (di.cu_count * 4 + rows - 1) / rows;
+  int ns = (di.cu_count * 2 + rows - 1) / rows;
   if (ns > max_split) ns = max_split;
   if (ns > 1024) ns = 1024;
   return ns < 1 ? 1 : ns;
@@ -327,10 +355,10 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
   LAP_HIP(e, "attn_decode_kernel launch");
   if (a.nsplit > 1) {
     if (dtype == LAP_DTYPE_F16)
-      hipLaunchKernelGGL(attn_combine_kernel<LAP_DTYPE_F16>, dim3(a.B * a.Hq), dim3(D), 0, st,
+      hipLaunchKernelGGL(attn_combine_kernel<LAP_DTYPE_F16>, dim3(a.B * a.Hq), dim3(256), 0, st,
                          a.part, a.nsplit, D, a.out);
     else
-      hipLaunchKernelGGL(attn_combine_kernel<LAP_DTYPE_BF16>, dim3(a.B * a.Hq), dim3(D), 0, st,
+      hipLaunchKernelGGL(attn_combine_kernel<LAP_DTYPE_BF16>, dim3(a.B * a.Hq), dim3(256), 0, st,
                          a.part, a.nsplit, D, a.out);
     LAP_LAUNCH_CHECK("attn_combine_kernel");
   }

@@ -6,8 +6,8 @@
 // (the order the CPU oracle restates).  The reference forms this LUT with a
 // vendor GEMM (laprune/llm/aq_kv.py:681-682) or an fp32 einsum (:620).
 //
-// Work shape: a 256-thread workgroup owns a tile of 64 codebook rows
-// (row = m*K + k) x 32 query heads; each thread produces 2 rows x 4 heads.
+// Work shape: a 256-thread workgroup owns a tile of 32 codebook rows
+// (row = m*K + k) x 32 query heads; each thread produces 1 row x 4 heads.
 // The codebook tile and the query tile are staged in LDS as fp32 with padded
 // rows so that the eight row-pairs (and eight head-quads) read by one wave
 // fall in distinct banks.  The interleaved layout [Hq/G][M][K][G] is written
@@ -17,112 +17,118 @@
 namespace lap {
 namespace {
 
-constexpr int kRowsPerTile = 64;
+constexpr int kRowsPerTile = 32;
 constexpr int kHeadsPerTile = 32;
 constexpr int kThreads = 256;
 
+// Load 4 consecutive elements of dtype DT at element offset i as fp32.
+template <int DT>
+__device__ __forceinline__ float4 load4(const void* p, int64_t i) {
+  if (DT == LAP_DTYPE_F32) return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+  const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+  if (DT == LAP_DTYPE_F16)
+    return make_float4(h2f(w.x & 0xffffu), h2f(w.x >> 16), h2f(w.y & 0xffffu), h2f(w.y >> 16));
+  return make_float4(bf2f(w.x & 0xffffu), bf2f(w.x >> 16), bf2f(w.y & 0xffffu), bf2f(w.y >> 16));
+}
+
+// LDS layout (floats):
+//   s_cb [32 rows][D + 4]                 rows padded by 4 banks
+//   s_q  [8 quads][4 heads][D] + 4 per quad  quads padded by 4 banks
+// so the 8 row reads and the 8 head-quad reads of one wave hit distinct banks.
 template <int QDT, int CDT>
 __global__ __launch_bounds__(kThreads) void lut_build_kernel(
     const void* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ cb, int Hq, int D, int MK, int G, int layout,
     uint16_t* __restrict__ out) {
-  extern __shared__ float smem[];
-  const int ld = D + 4;  // padded row length (floats)
-  float* s_cb = smem;                        // [64][ld]
-  float* s_q = smem + kRowsPerTile * ld;     // [32][ld]
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int ldc = D + 4;
+  const int ldq = 4 * D + 4;
+  float* s_cb = smem;                         // [32][ldc]
+  float* s_q = smem + kRowsPerTile * ldc;     // [8][ldq]
 
   const int row0 = blockIdx.x * kRowsPerTile;
   const int head0 = blockIdx.y * kHeadsPerTile;
   const int tid = threadIdx.x;
+  const int D4 = D / 4;
 
-  // Stage the codebook tile (fp32) and the query tile (fp32).
-  for (int i = tid; i < kRowsPerTile * D; i += kThreads) {
-    const int r = i / D, d = i - r * D;
-    const int row = row0 + r;
-    float v = 0.f;
-    if (row < MK) v = load_as_f32(cb, (int64_t)row * D + d, CDT);
-    s_cb[r * ld + d] = v;
-  }
-  for (int i = tid; i < kHeadsPerTile * D; i += kThreads) {
-    const int h = i / D, d = i - h * D;
-    const int head = head0 + h;
-    float v = 0.f;
-    if (head < Hq) v = load_as_f32(q, (int64_t)head * q_row_stride + d, QDT);
-    s_q[h * ld + d] = v;
+  // Stage both tiles with all loads issued before the LDS stores.
+  {
+    constexpr int kMaxIt = (kRowsPerTile * 256 / 4 + kThreads - 1) / kThreads;  // D <= 256
+    float4 cv[kMaxIt], qv[kMaxIt];
+    const int n4 = kRowsPerTile * D4;  // float4 slots per tile (same for q: 32 heads)
+#pragma unroll
+    for (int it = 0; it < kMaxIt; ++it) {
+      const int i = tid + it * kThreads;
+      cv[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+      qv[it] = cv[it];
+      if (i < n4) {
+        const int r = i / D4, d = (i - r * D4) * 4;
+        if (row0 + r < MK) cv[it] = load4<CDT>(cb, (int64_t)(row0 + r) * D + d);
+        if (head0 + r < Hq) qv[it] = load4<QDT>(q, (int64_t)(head0 + r) * q_row_stride + d);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < kMaxIt; ++it) {
+      const int i = tid + it * kThreads;
+      if (i < n4) {
+        const int r = i / D4, d = (i - r * D4) * 4;
+        *reinterpret_cast<float4*>(s_cb + r * ldc + d) = cv[it];
+        *reinterpret_cast<float4*>(s_q + (r >> 2) * ldq + (r & 3) * D + d) = qv[it];
+      }
+    }
   }
   __syncthreads();
 
-  const int hq4 = tid & 7;    // heads 4*hq4 .. 4*hq4+3 of the tile
-  const int rp = tid >> 3;    // rows 2*rp, 2*rp+1 of the tile
-  const float* c0 = s_cb + (2 * rp) * ld;
-  const float* c1 = c0 + ld;
-  const float* qa = s_q + (4 * hq4) * ld;
+  const int hq4 = tid & 7;   // heads 4*hq4 .. 4*hq4+3 of the tile
+  const int rr = tid >> 3;   // row rr of the tile
+  const float* c0 = s_cb + rr * ldc;
+  const float* qa = s_q + hq4 * ldq;
 
-  float acc[2][4];
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int h = 0; h < 4; ++h) acc[r][h] = 0.f;
-
-  // Sequential fmaf chain over d for each of the 8 outputs.
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  // One fmaf chain over d per output, d ascending.
   for (int d = 0; d < D; d += 4) {
-    const float4 x0 = *reinterpret_cast<const float4*>(c0 + d);
-    const float4 x1 = *reinterpret_cast<const float4*>(c1 + d);
-    float4 qv[4];
-#pragma unroll
-    for (int h = 0; h < 4; ++h) qv[h] = *reinterpret_cast<const float4*>(qa + h * ld + d);
+    const float4 x = *reinterpret_cast<const float4*>(c0 + d);
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      acc[0][h] = __builtin_fmaf(qv[h].x, x0.x, acc[0][h]);
-      acc[0][h] = __builtin_fmaf(qv[h].y, x0.y, acc[0][h]);
-      acc[0][h] = __builtin_fmaf(qv[h].z, x0.z, acc[0][h]);
-      acc[0][h] = __builtin_fmaf(qv[h].w, x0.w, acc[0][h]);
-      acc[1][h] = __builtin_fmaf(qv[h].x, x1.x, acc[1][h]);
-      acc[1][h] = __builtin_fmaf(qv[h].y, x1.y, acc[1][h]);
-      acc[1][h] = __builtin_fmaf(qv[h].z, x1.z, acc[1][h]);
-      acc[1][h] = __builtin_fmaf(qv[h].w, x1.w, acc[1][h]);
+      const float4 qv = *reinterpret_cast<const float4*>(qa + h * D + d);
+      acc[h] = __builtin_fmaf(qv.x, x.x, acc[h]);
+      acc[h] = __builtin_fmaf(qv.y, x.y, acc[h]);
+      acc[h] = __builtin_fmaf(qv.z, x.z, acc[h]);
+      acc[h] = __builtin_fmaf(qv.w, x.w, acc[h]);
     }
   }
 
-  const int rowA = row0 + 2 * rp;
+  const int row = row0 + rr;
   const int headA = head0 + 4 * hq4;
-  if (layout == LAP_LUT_GMKG && G == 4 && headA + 3 < Hq && (headA & 3) == 0 &&
-      rowA + 1 < MK) {
-    // Four heads of one KV group for two consecutive rows: 16 contiguous bytes.
+  if (row >= MK) return;
+  if (layout == LAP_LUT_GMKG && G == 4 && headA + 3 < Hq) {
+    // Four heads of one KV group for one row: 8 contiguous bytes.
     const int hkv = headA >> 2;
-    uint32_t w[4];
-    w[0] = (uint32_t)f2h(acc[0][0]) | ((uint32_t)f2h(acc[0][1]) << 16);
-    w[1] = (uint32_t)f2h(acc[0][2]) | ((uint32_t)f2h(acc[0][3]) << 16);
-    w[2] = (uint32_t)f2h(acc[1][0]) | ((uint32_t)f2h(acc[1][1]) << 16);
-    w[3] = (uint32_t)f2h(acc[1][2]) | ((uint32_t)f2h(acc[1][3]) << 16);
-    uint4* dst = reinterpret_cast<uint4*>(out + ((int64_t)hkv * MK + rowA) * 4);
-    *dst = make_uint4(w[0], w[1], w[2], w[3]);
+    const uint32_t w0 = (uint32_t)f2h(acc[0]) | ((uint32_t)f2h(acc[1]) << 16);
+    const uint32_t w1 = (uint32_t)f2h(acc[2]) | ((uint32_t)f2h(acc[3]) << 16);
+    *reinterpret_cast<uint2*>(out + ((int64_t)hkv * MK + row) * 4) = make_uint2(w0, w1);
     return;
   }
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = rowA + r;
-    if (row >= MK) continue;
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int head = headA + h;
-      if (head >= Hq) continue;
-      int64_t idx;
-      if (layout == LAP_LUT_HMK) {
-        idx = (int64_t)head * MK + row;
-      } else {
-        idx = ((int64_t)(head / G) * MK + row) * G + (head % G);
-      }
-      out[idx] = f2h(acc[r][h]);
-    }
+  for (int h = 0; h < 4; ++h) {
+    const int head = headA + h;
+    if (head >= Hq) continue;
+    int64_t idx;
+    if (layout == LAP_LUT_HMK) idx = (int64_t)head * MK + row;
+    else idx = ((int64_t)(head / G) * MK + row) * G + (head % G);
+    out[idx] = f2h(acc[h]);
   }
+}
+
+size_t lut_smem_bytes(int D) {
+  return ((size_t)kRowsPerTile * (D + 4) + (size_t)8 * (4 * D + 4)) * sizeof(float);
 }
 
 template <int QDT>
 hipError_t launch_lut(const void* q, int64_t qs, const void* cb, int cb_dtype, int Hq,
                       int D, int MK, int G, int layout, uint16_t* out, hipStream_t st) {
   dim3 grid((MK + kRowsPerTile - 1) / kRowsPerTile, (Hq + kHeadsPerTile - 1) / kHeadsPerTile);
-  const size_t smem = (size_t)(kRowsPerTile + kHeadsPerTile) * (D + 4) * sizeof(float);
+  const size_t smem = lut_smem_bytes(D);
   if (cb_dtype == LAP_DTYPE_F32) {
     hipLaunchKernelGGL((lut_build_kernel<QDT, LAP_DTYPE_F32>), grid, dim3(kThreads), smem, st,
                        q, qs, cb, Hq, D, MK, G, layout, out);
@@ -157,7 +163,7 @@ extern "C" int lap_lut_build(const void* q, int q_dtype, int64_t q_row_stride,
   DevInfo di;
   int ds = device_info(&di);
   if (ds != LAP_OK) return ds;
-  const size_t smem = (size_t)(kRowsPerTile + kHeadsPerTile) * (D + 4) * sizeof(float);
+  const size_t smem = lut_smem_bytes(D);
   LAP_CHECK_CODE(smem <= (size_t)di.lds_per_block, LAP_ERR_UNSUPPORTED,
                  "lap_lut_build: D=%d needs %zu bytes of LDS", D, smem);
   hipError_t e;

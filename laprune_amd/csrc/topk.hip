@@ -25,6 +25,7 @@ int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int6
                     uint16_t* keys, uint32_t* hist, int key_mode, int cand_start, int cand_end,
                     int* nchunk_out, hipStream_t st);
 bool score_g4_supported(const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t);
+int score_g4_nchunk(int R, int T);
 
 namespace {
 
@@ -73,6 +74,7 @@ __global__ __launch_bounds__(kThreads) void topk_prep_kernel(
   s_h[threadIdx.x] = 0;
   __syncthreads();
   const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
+#pragma unroll 8
   for (int e = e0 + threadIdx.x; e < e1; e += kThreads) {
     uint32_t key = 0;
     for (int g = 0; g < group; ++g) {
@@ -100,6 +102,7 @@ __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
   const int tid = threadIdx.x;
   uint32_t tot = 0;
   const uint32_t* h1 = hist1 + (int64_t)r * C1 * 256 + tid;
+#pragma unroll 16
   for (int cc = 0; cc < C1; ++cc) tot += h1[(int64_t)cc * 256];
   s_h[tid] = tot;
   s_h2[tid] = 0;
@@ -114,10 +117,17 @@ __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
   const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
   uint32_t gt = 0;
   const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
-  for (int e = e0 + tid; e < e1; e += kThreads) {
-    const uint32_t key = kr[e];
-    const uint32_t hi = key >> 8;
-    if (hi == b1) atomicAdd(&s_h2[key & 255u], 1u);
+  uint32_t kv[kChunk / kThreads];
+#pragma unroll
+  for (int i = 0; i < kChunk / kThreads; ++i) {
+    const int e = e0 + i * kThreads + tid;
+    kv[i] = e < e1 ? (uint32_t)kr[e] : 0xffffffffu;
+  }
+#pragma unroll
+  for (int i = 0; i < kChunk / kThreads; ++i) {
+    if (kv[i] == 0xffffffffu) continue;
+    const uint32_t hi = kv[i] >> 8;
+    if (hi == b1) atomicAdd(&s_h2[kv[i] & 255u], 1u);
     gt += hi > b1;
   }
   if (gt) atomicAdd(&s_gt, gt);
@@ -139,10 +149,11 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
 
   uint32_t tot = 0, pre = 0;
   const uint32_t* h2 = hist2 + (int64_t)r * C * 256 + tid;
+#pragma unroll 16
   for (int cc = 0; cc < C; ++cc) {
     const uint32_t v = h2[(int64_t)cc * 256];
     tot += v;
-    if (cc < c) pre += v;
+    pre += cc < c ? v : 0u;
   }
   s_tot[tid] = tot;
   s_pre[tid] = pre;
@@ -170,11 +181,19 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
   const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
   OUT_T* orow = out + (int64_t)r * out_stride;
   uint32_t sel_run = base, tie_run = ties_before;
-  for (int e0r = e0; e0r < e1; e0r += kThreads) {
+  uint32_t kv[kChunk / kThreads];
+#pragma unroll
+  for (int i = 0; i < kChunk / kThreads; ++i) {
+    const int e = e0 + i * kThreads + tid;
+    kv[i] = e < e1 ? (uint32_t)kr[e] : 0u;
+  }
+#pragma unroll
+  for (int i = 0; i < kChunk / kThreads; ++i) {
+    const int e0r = e0 + i * kThreads;
+    if (e0r >= e1) break;
     const int e = e0r + tid;
-    uint32_t key = 0;
     const bool valid = e < e1;
-    if (valid) key = kr[e];
+    const uint32_t key = kv[i];
     const bool is_gt = valid && key > tau;
     const bool is_tie = valid && key == tau;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -308,6 +327,74 @@ extern "C" int lap_retrieve_workspace_size(int R, int T, size_t* bytes) {
   return LAP_OK;
 }
 
+static int retrieve_checks(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b,
+                           int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, int cand_start,
+                           int cand_end, int k, int key_mode) {
+  LAP_CHECK(lut_gmkg && codes, "lap_retrieve: null pointer");
+  LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "lap_retrieve: bad sizes");
+  LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
+            "lap_retrieve: candidate window [%d,%d) outside [0,%d)", cand_start, cand_end, T);
+  LAP_CHECK(k >= 0, "lap_retrieve: k must be non-negative");
+  LAP_CHECK(key_mode == LAP_KEY_F16 || key_mode == LAP_KEY_BF16, "lap_retrieve: bad key mode");
+  LAP_CHECK(cs_t >= 32, "lap_retrieve: codes token stride < M=32");
+  LAP_CHECK_CODE(score_g4_supported(codes, cs_b, cs_h, cs_t), LAP_ERR_UNSUPPORTED,
+                 "lap_retrieve: codes base and strides must be 16-byte aligned");
+  return LAP_OK;
+}
+
+extern "C" int lap_retrieve_score(const void* lut_gmkg, const uint8_t* codes,
+                                  int64_t codes_stride_b, int64_t codes_stride_h,
+                                  int64_t codes_stride_t, int B, int Hkv, int T, int cand_start,
+                                  int cand_end, int key_mode, void* scores_out,
+                                  void* workspace, size_t workspace_bytes,
+                                  lap_stream_t stream) {
+  clear_error();
+  int s = retrieve_checks(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
+                          Hkv, T, cand_start, cand_end, 0, key_mode);
+  if (s != LAP_OK) return s;
+  const int R = B * Hkv;
+  const int C2 = (T + kChunk - 1) / kChunk;
+  Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
+  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
+                 "lap_retrieve_score: workspace of %zu bytes needed", w.bytes);
+  int C1 = 0;
+  s = launch_score_g4(static_cast<const uint16_t*>(lut_gmkg), true, codes, codes_stride_b,
+                      codes_stride_h, codes_stride_t, B, Hkv, T,
+                      static_cast<uint16_t*>(scores_out), w.keys, w.hist1, key_mode,
+                      cand_start, cand_end, &C1, as_stream(stream));
+  if (s != LAP_OK) return s;
+  LAP_CHECK_CODE(C1 <= retrieve_chunk_bound(T), LAP_ERR_INVALID,
+                 "lap_retrieve_score: internal chunk bound exceeded");
+  return LAP_OK;
+}
+
+extern "C" int lap_retrieve_select(int B, int Hkv, int T, int cand_start, int cand_end, int k,
+                                   void* out_idx, int out_dtype, void* workspace,
+                                   size_t workspace_bytes, lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(out_idx, "lap_retrieve_select: null output");
+  LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "lap_retrieve_select: bad sizes");
+  LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
+            "lap_retrieve_select: candidate window [%d,%d) outside [0,%d)", cand_start, cand_end,
+            T);
+  LAP_CHECK(k >= 0, "lap_retrieve_select: k must be non-negative");
+  LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
+            "lap_retrieve_select: out dtype must be int32/int64");
+  const int R = B * Hkv;
+  const int n = cand_end - cand_start;
+  const int ke = std::min(k, n);
+  if (ke == 0) return LAP_OK;
+  const int C2 = (T + kChunk - 1) / kChunk;
+  Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
+  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
+                 "lap_retrieve_select: workspace of %zu bytes needed", w.bytes);
+  const int C1 = score_g4_nchunk(R, T);
+  LAP_CHECK_CODE(C1 > 0 && C1 <= retrieve_chunk_bound(T), LAP_ERR_HIP,
+                 "lap_retrieve_select: device query failed");
+  KeySrc ks{w.keys, T, cand_start};
+  return run_levels(w, ks, R, n, ke, C1, cand_start, out_idx, out_dtype, k, as_stream(stream));
+}
+
 extern "C" int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
                                  int64_t codes_stride_b, int64_t codes_stride_h,
                                  int64_t codes_stride_t, int B, int Hkv, int T, int cand_start,
@@ -315,36 +402,11 @@ extern "C" int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
                                  void* out_idx, int out_dtype, void* workspace,
                                  size_t workspace_bytes, lap_stream_t stream) {
   clear_error();
-  LAP_CHECK(lut_gmkg && codes && out_idx, "lap_retrieve_topk: null pointer");
-  LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "lap_retrieve_topk: bad sizes");
-  LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
-            "lap_retrieve_topk: candidate window [%d,%d) outside [0,%d)", cand_start, cand_end,
-            T);
-  LAP_CHECK(k >= 0, "lap_retrieve_topk: k must be non-negative");
-  LAP_CHECK(key_mode == LAP_KEY_F16 || key_mode == LAP_KEY_BF16, "lap_retrieve_topk: bad key mode");
-  LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
-            "lap_retrieve_topk: out dtype must be int32/int64");
-  LAP_CHECK(codes_stride_t >= 32, "lap_retrieve_topk: codes token stride < M=32");
-  LAP_CHECK_CODE(score_g4_supported(codes, codes_stride_b, codes_stride_h, codes_stride_t),
-                 LAP_ERR_UNSUPPORTED,
-                 "lap_retrieve_topk: codes base and strides must be 16-byte aligned");
-  const int R = B * Hkv;
-  const int n = cand_end - cand_start;
-  const int ke = std::min(k, n);
-  const int C2 = (T + kChunk - 1) / kChunk;
-  Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
-  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
-                 "lap_retrieve_topk: workspace of %zu bytes needed", w.bytes);
-  hipStream_t st = as_stream(stream);
-  int C1 = 0;
-  int s = launch_score_g4(static_cast<const uint16_t*>(lut_gmkg), true, codes, codes_stride_b,
-                          codes_stride_h, codes_stride_t, B, Hkv, T,
-                          static_cast<uint16_t*>(scores_out), w.keys, ke > 0 ? w.hist1 : nullptr,
-                          key_mode, cand_start, cand_end, &C1, st);
+  LAP_CHECK(out_idx || k == 0, "lap_retrieve_topk: null output");
+  int s = lap_retrieve_score(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
+                             Hkv, T, cand_start, cand_end, key_mode, scores_out, workspace,
+                             workspace_bytes, stream);
   if (s != LAP_OK) return s;
-  if (ke == 0) return LAP_OK;
-  LAP_CHECK_CODE(C1 <= retrieve_chunk_bound(T), LAP_ERR_INVALID,
-                 "lap_retrieve_topk: internal chunk bound exceeded");
-  KeySrc ks{w.keys, T, cand_start};
-  return run_levels(w, ks, R, n, ke, C1, cand_start, out_idx, out_dtype, k, st);
+  return lap_retrieve_select(B, Hkv, T, cand_start, cand_end, k, out_idx, out_dtype, workspace,
+                             workspace_bytes, stream);
 }
