@@ -1,0 +1,101 @@
+"""The C ABI library loads, exports every symbol include/laprune_hip.h declares,
+and rejects invalid arguments with a status and a message — all without a GPU
+(argument checks run before any device call)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "laprune_hip.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(lap_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from laprune_amd import _native as N
+    return N.lib()
+
+
+def test_header_declares_the_abi():
+    names = declared()
+    assert "lap_last_error" in names and "lap_retrieve_topk" in names
+    assert len(names) >= 20
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    from laprune_amd import _native as N
+    for name in declared():
+        assert hasattr(lib, name), f"{name} not exported"
+        if name != "lap_last_error":
+            assert name in N.SIGNATURES, f"{name} not bound in _native.SIGNATURES"
+
+
+def test_abi_version(lib):
+    assert lib.lap_abi_version() == 1
+
+
+def _err(lib):
+    return lib.lap_last_error().decode()
+
+
+def test_invalid_arguments_return_status_and_message(lib):
+    from laprune_amd import _native as N
+    st = lib.lap_lut_build(None, N.BF16, 128, None, N.F32, 32, 128, 32, 256, 4, N.LUT_GMKG, None, None)
+    assert st == N.LAP_ERR_INVALID and "null pointer" in _err(lib)
+    one = C.c_void_p(16)  # never dereferenced: validation fails first
+    st = lib.lap_lut_score_grouped(one, N.LUT_HMK, one, 0, 32, 8, 5, 100, 32, 256, one, None)
+    assert st == N.LAP_ERR_INVALID and "G<=4" in _err(lib)
+    st = lib.lap_lut_score_mha(one, N.BF16, one, N.U8, 1, 1, 1, 1, one, None)
+    assert st == N.LAP_ERR_INVALID and "fp16 or fp32" in _err(lib)
+    st = lib.lap_topk_select(one, 10, 1, 1, 10, 5, 20, 3, N.KEY_F16, one, N.I32, None, 0, None)
+    assert st == N.LAP_ERR_INVALID and "candidate window" in _err(lib)
+    st = lib.lap_gqa_gather_kv(one, one, N.F32, 1, 1, 10, 128, 0, 0, 128, 0, 0, 128, one, 4, 1,
+                               -1, 0, one, one, None)
+    assert st == N.LAP_ERR_INVALID and "fp16/bf16" in _err(lib)
+    st = lib.lap_encode_greedy(one, 128, 4, 128, one, 32, 300, one, 1 << 30, one, 32, None, None)
+    assert st == N.LAP_ERR_INVALID and "exceeds 256" in _err(lib)
+    st = lib.lap_sparse_attn_decode(one, 0, 128, one, one, N.BF16, 1, 32, 8, 100, 128, 0, 0, 128,
+                                    0, 0, 128, one, N.I32, 5, 10, 0, -1, 0, 1.0, one, None, 0, None)
+    assert st == N.LAP_ERR_INVALID and "H_idx" in _err(lib)
+
+
+def test_workspace_size_queries(lib):
+    from laprune_amd import _native as N
+    assert N.size_query("lap_topk_workspace_size", 8, 131008) > 8 * 131008 * 2
+    assert N.size_query("lap_retrieve_workspace_size", 8, 131072) > 8 * 131072 * 2
+    assert N.size_query("lap_attn_decode_workspace_size", 1, 32, 128, 2116) > 0
+    assert N.size_query("lap_encode_prep_size", 32, 256, 128) >= 32 * 256 * 128 * 4
+
+
+def test_aq_kernels_exports_reference_names():
+    from laprune_amd import aq_kernels as K
+    for name in K.REFERENCE_NAMES:
+        assert hasattr(K, name)
+    import inspect
+    sig = inspect.signature(K._impl.gqa_gather_kv_with_tail)
+    assert list(sig.parameters) == ["keys", "vals", "indices", "G", "tail_start", "tail_count",
+                                    "threads", "vector_width"]
+    assert sig.parameters["threads"].default == 256 and sig.parameters["vector_width"].default == 8
+    sig = inspect.signature(K._impl.aq_lut_gather)
+    assert list(sig.parameters) == ["lut", "codes", "G", "M_start", "M_end", "indices"]
+    sig = inspect.signature(K._impl.fused_linear_encode_forward)
+    assert list(sig.parameters) == ["x", "weight_t", "bias", "codebooks", "fp32_residual", "tile_n"]
+    sig = inspect.signature(K._impl.aq_lut_gather_grouped)
+    assert sig.parameters["grid_y_cap"].default == 48
+
+
+def test_cpu_tensors_are_rejected_loudly():
+    import torch
+    from laprune_amd.aq_kernels import _impl
+    with pytest.raises(RuntimeError, match="CUDA"):
+        _impl.aq_lut_gather_grouped(torch.zeros(4, 32, 256, dtype=torch.float16),
+                                    torch.zeros(1, 10, 32, dtype=torch.uint8), 4)
+    with pytest.raises(RuntimeError):
+        _impl.aq_lut_build(torch.zeros(4, 128), torch.zeros(32, 256, 128))
