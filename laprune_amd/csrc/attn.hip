@@ -338,6 +338,10 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
   a.per_split = (a.per_split + kTile - 1) / kTile * kTile;
   if (a.per_split < kTile) a.per_split = kTile;
   a.nsplit = L > 0 ? (L + a.per_split - 1) / a.per_split : 1;
+  // Workspace: split partials [B][Hq][nsplit][D + 2], merged by a combine
+  // kernel.  (An in-kernel merge by the last-arriving workgroup needs a
+  // device-scope release per workgroup, which on the multi-XCD part writes
+  // back the XCD's L2 and costs far more than the second launch.)
   if (a.nsplit > 1) {
     const size_t need = (size_t)a.B * a.Hq * a.nsplit * (D + 2) * sizeof(float);
     LAP_CHECK_CODE(workspace && ws_bytes >= need, LAP_ERR_WORKSPACE,
@@ -396,7 +400,7 @@ extern "C" int lap_attn_decode_workspace_size(int B, int Hq, int D, int max_keys
   int ns = (max_keys + kTile - 1) / kTile;
   if (ns > 1024) ns = 1024;
   if (ns < 1) ns = 1;
-  *bytes = (size_t)B * Hq * ns * (D + 2) * sizeof(float);
+  *bytes = (size_t)B * Hq * ns * (D + 2) * sizeof(float);  // split partials
   return LAP_OK;
 }
 

@@ -134,4 +134,16 @@ __device__ __forceinline__ float acc_f16(float acc, _Float16 h, _Float16 one) {
 // ---------------------------------------------------------- wave helpers
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() is a fence over
+// all address spaces, which on gfx9 waits for every outstanding global load
+// (vmcnt(0)) before the barrier and so cancels any prefetch in flight; this
+// barrier waits only for the LDS counter, letting global loads stay in
+// flight across it.  Use it only where no global-memory ordering between the
+// threads of the workgroup is needed.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace lap

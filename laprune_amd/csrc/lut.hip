@@ -6,19 +6,17 @@
 // (the order the CPU oracle restates).  The reference forms this LUT with a
 // vendor GEMM (laprune/llm/aq_kv.py:681-682) or an fp32 einsum (:620).
 //
-// Work shape: a 256-thread workgroup owns a tile of 32 codebook rows
-// (row = m*K + k) x 32 query heads; each thread produces 1 row x 4 heads.
-// The codebook tile and the query tile are staged in LDS as fp32 with padded
-// rows so that the eight row-pairs (and eight head-quads) read by one wave
-// fall in distinct banks.  The interleaved layout [Hq/G][M][K][G] is written
-// directly so the scorer can fill its LDS table with a linear copy.
+// Work shape: one lane per codebook row (row = m*K + k), four query heads per
+// wave, 64 rows x 16 heads per workgroup (1024 waves at Hq = 32, M*K = 8192).
+// The interleaved layout [Hq/G][M][K][G] is written directly so the scorer can
+// fill its LDS table with a linear copy.
 #include "common.h"
 
 namespace lap {
 namespace {
 
-constexpr int kRowsPerTile = 32;
-constexpr int kHeadsPerTile = 32;
+constexpr int kRows = 64;        // codebook rows per workgroup (one per lane)
+constexpr int kHeadsPerWG = 16;  // query heads per workgroup (4 per wave)
 constexpr int kThreads = 256;
 
 // Load 4 consecutive elements of dtype DT at element offset i as fp32.
@@ -31,82 +29,67 @@ __device__ __forceinline__ float4 load4(const void* p, int64_t i) {
   return make_float4(bf2f(w.x & 0xffffu), bf2f(w.x >> 16), bf2f(w.y & 0xffffu), bf2f(w.y >> 16));
 }
 
-// LDS layout (floats):
-//   s_cb [32 rows][D + 4]                 rows padded by 4 banks
-//   s_q  [8 quads][4 heads][D] + 4 per quad  quads padded by 4 banks
-// so the 8 row reads and the 8 head-quad reads of one wave hit distinct banks.
+// Workgroup = 64 codebook rows x 16 query heads; wave w owns heads
+// head0 + 4w .. head0 + 4w + 3 and lane l owns row row0 + l, so each lane runs
+// four independent fmaf chains over d.  The query slice is staged once in LDS
+// as fp32 and read as wave-wide broadcasts (one address per instruction, no
+// bank conflicts); the codebook row is read straight from L1/L2.
 template <int QDT, int CDT>
 __global__ __launch_bounds__(kThreads) void lut_build_kernel(
     const void* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ cb, int Hq, int D, int MK, int G, int layout,
     uint16_t* __restrict__ out) {
-  extern __shared__ __attribute__((aligned(16))) float smem[];
-  const int ldc = D + 4;
-  const int ldq = 4 * D + 4;
-  float* s_cb = smem;                         // [32][ldc]
-  float* s_q = smem + kRowsPerTile * ldc;     // [8][ldq]
-
-  const int row0 = blockIdx.x * kRowsPerTile;
-  const int head0 = blockIdx.y * kHeadsPerTile;
-  const int tid = threadIdx.x;
+  extern __shared__ __attribute__((aligned(16))) float s_q[];  // [16][D]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * kRows;
+  const int head0 = blockIdx.y * kHeadsPerWG;
   const int D4 = D / 4;
 
-  // Stage both tiles with all loads issued before the LDS stores.
-  {
-    constexpr int kMaxIt = (kRowsPerTile * 256 / 4 + kThreads - 1) / kThreads;  // D <= 256
-    float4 cv[kMaxIt], qv[kMaxIt];
-    const int n4 = kRowsPerTile * D4;  // float4 slots per tile (same for q: 32 heads)
-#pragma unroll
-    for (int it = 0; it < kMaxIt; ++it) {
-      const int i = tid + it * kThreads;
-      cv[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-      qv[it] = cv[it];
-      if (i < n4) {
-        const int r = i / D4, d = (i - r * D4) * 4;
-        if (row0 + r < MK) cv[it] = load4<CDT>(cb, (int64_t)(row0 + r) * D + d);
-        if (head0 + r < Hq) qv[it] = load4<QDT>(q, (int64_t)(head0 + r) * q_row_stride + d);
-      }
-    }
-#pragma unroll
-    for (int it = 0; it < kMaxIt; ++it) {
-      const int i = tid + it * kThreads;
-      if (i < n4) {
-        const int r = i / D4, d = (i - r * D4) * 4;
-        *reinterpret_cast<float4*>(s_cb + r * ldc + d) = cv[it];
-        *reinterpret_cast<float4*>(s_q + (r >> 2) * ldq + (r & 3) * D + d) = qv[it];
-      }
-    }
+  for (int i = tid; i < kHeadsPerWG * D4; i += kThreads) {
+    const int h = i / D4, d = (i - h * D4) * 4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (head0 + h < Hq) v = load4<QDT>(q, (int64_t)(head0 + h) * q_row_stride + d);
+    *reinterpret_cast<float4*>(s_q + h * D + d) = v;
   }
   __syncthreads();
 
-  const int hq4 = tid & 7;   // heads 4*hq4 .. 4*hq4+3 of the tile
-  const int rr = tid >> 3;   // row rr of the tile
-  const float* c0 = s_cb + rr * ldc;
-  const float* qa = s_q + hq4 * ldq;
-
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  // One fmaf chain over d per output, d ascending.
+  const int row = row0 + lane;
+  const int rowc = row < MK ? row : MK - 1;  // clamped for the loads
+  const float* qw = s_q + (4 * wave) * D;
+  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+#pragma unroll 4
   for (int d = 0; d < D; d += 4) {
-    const float4 x = *reinterpret_cast<const float4*>(c0 + d);
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const float4 qv = *reinterpret_cast<const float4*>(qa + h * D + d);
-      acc[h] = __builtin_fmaf(qv.x, x.x, acc[h]);
-      acc[h] = __builtin_fmaf(qv.y, x.y, acc[h]);
-      acc[h] = __builtin_fmaf(qv.z, x.z, acc[h]);
-      acc[h] = __builtin_fmaf(qv.w, x.w, acc[h]);
-    }
+    const float4 c = load4<CDT>(cb, (int64_t)rowc * D + d);
+    const float4 q0 = *reinterpret_cast<const float4*>(qw + d);
+    const float4 q1 = *reinterpret_cast<const float4*>(qw + D + d);
+    const float4 q2 = *reinterpret_cast<const float4*>(qw + 2 * D + d);
+    const float4 q3 = *reinterpret_cast<const float4*>(qw + 3 * D + d);
+    acc0 = __builtin_fmaf(q0.x, c.x, acc0);
+    acc1 = __builtin_fmaf(q1.x, c.x, acc1);
+    acc2 = __builtin_fmaf(q2.x, c.x, acc2);
+    acc3 = __builtin_fmaf(q3.x, c.x, acc3);
+    acc0 = __builtin_fmaf(q0.y, c.y, acc0);
+    acc1 = __builtin_fmaf(q1.y, c.y, acc1);
+    acc2 = __builtin_fmaf(q2.y, c.y, acc2);
+    acc3 = __builtin_fmaf(q3.y, c.y, acc3);
+    acc0 = __builtin_fmaf(q0.z, c.z, acc0);
+    acc1 = __builtin_fmaf(q1.z, c.z, acc1);
+    acc2 = __builtin_fmaf(q2.z, c.z, acc2);
+    acc3 = __builtin_fmaf(q3.z, c.z, acc3);
+    acc0 = __builtin_fmaf(q0.w, c.w, acc0);
+    acc1 = __builtin_fmaf(q1.w, c.w, acc1);
+    acc2 = __builtin_fmaf(q2.w, c.w, acc2);
+    acc3 = __builtin_fmaf(q3.w, c.w, acc3);
   }
-
-  const int row = row0 + rr;
-  const int headA = head0 + 4 * hq4;
   if (row >= MK) return;
+  const int headA = head0 + 4 * wave;
+  const float acc[4] = {acc0, acc1, acc2, acc3};
   if (layout == LAP_LUT_GMKG && G == 4 && headA + 3 < Hq) {
-    // Four heads of one KV group for one row: 8 contiguous bytes.
-    const int hkv = headA >> 2;
-    const uint32_t w0 = (uint32_t)f2h(acc[0]) | ((uint32_t)f2h(acc[1]) << 16);
-    const uint32_t w1 = (uint32_t)f2h(acc[2]) | ((uint32_t)f2h(acc[3]) << 16);
-    *reinterpret_cast<uint2*>(out + ((int64_t)hkv * MK + row) * 4) = make_uint2(w0, w1);
+    // The four heads of one KV group for this row: 8 contiguous bytes; a
+    // wave writes 512 contiguous bytes.
+    const uint32_t w0 = (uint32_t)f2h(acc0) | ((uint32_t)f2h(acc1) << 16);
+    const uint32_t w1 = (uint32_t)f2h(acc2) | ((uint32_t)f2h(acc3) << 16);
+    *reinterpret_cast<uint2*>(out + ((int64_t)(headA >> 2) * MK + row) * 4) = make_uint2(w0, w1);
     return;
   }
 #pragma unroll
@@ -120,14 +103,12 @@ __global__ __launch_bounds__(kThreads) void lut_build_kernel(
   }
 }
 
-size_t lut_smem_bytes(int D) {
-  return ((size_t)kRowsPerTile * (D + 4) + (size_t)8 * (4 * D + 4)) * sizeof(float);
-}
+size_t lut_smem_bytes(int D) { return (size_t)kHeadsPerWG * D * sizeof(float); }
 
 template <int QDT>
 hipError_t launch_lut(const void* q, int64_t qs, const void* cb, int cb_dtype, int Hq,
                       int D, int MK, int G, int layout, uint16_t* out, hipStream_t st) {
-  dim3 grid((MK + kRowsPerTile - 1) / kRowsPerTile, (Hq + kHeadsPerTile - 1) / kHeadsPerTile);
+  dim3 grid((MK + kRows - 1) / kRows, (Hq + kHeadsPerWG - 1) / kHeadsPerWG);
   const size_t smem = lut_smem_bytes(D);
   if (cb_dtype == LAP_DTYPE_F32) {
     hipLaunchKernelGGL((lut_build_kernel<QDT, LAP_DTYPE_F32>), grid, dim3(kThreads), smem, st,

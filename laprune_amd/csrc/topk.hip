@@ -94,16 +94,75 @@ struct KeySrc {
   int off;         // column of candidate 0
 };
 
+// Sum of n values p[0], p[stride], ... with 32 independent loads in flight
+// (the chunk histograms live in L2; latency, not bandwidth, is the cost).
+__device__ __forceinline__ void sum_strided2(const uint32_t* __restrict__ p, int n,
+                                             int64_t stride, int split, uint32_t& tot,
+                                             uint32_t& pre) {
+  tot = 0;
+  pre = 0;
+  int i = 0;
+  for (; i + 32 <= n; i += 32) {
+    uint32_t v[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) v[u] = p[(int64_t)(i + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      tot += v[u];
+      pre += (i + u) < split ? v[u] : 0u;
+    }
+  }
+  for (; i < n; ++i) {
+    const uint32_t v = p[(int64_t)i * stride];
+    tot += v;
+    pre += i < split ? v : 0u;
+  }
+}
+
+// Exclusive prefix sum over the 256 threads of the block; returns the
+// thread's prefix and writes the block total to *total.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t x, uint32_t* s_wsum,
+                                                         uint32_t* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t inc = x;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += y;
+  }
+  if (lane == 63) s_wsum[wave] = inc;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t v = s_wsum[w];
+    before += w < wave ? v : 0u;
+    all += v;
+  }
+  __syncthreads();
+  *total = all;
+  return before + inc - x;
+}
+
+constexpr int kPer = kChunk / kThreads;  // keys per thread, contiguous
+
 __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
     KeySrc ks, int R, int n, int k, const uint32_t* __restrict__ hist1, int C1, int C,
     uint32_t* __restrict__ hist2, uint32_t* __restrict__ gtc, uint32_t* __restrict__ info) {
   __shared__ uint32_t s_h[256], s_h2[256], s_wsum[kWaves], s_res[2], s_gt;
   const int r = blockIdx.x % R, c = blockIdx.x / R;
   const int tid = threadIdx.x;
-  uint32_t tot = 0;
-  const uint32_t* h1 = hist1 + (int64_t)r * C1 * 256 + tid;
-#pragma unroll 16
-  for (int cc = 0; cc < C1; ++cc) tot += h1[(int64_t)cc * 256];
+  // this thread's keys first, so their latency overlaps the histogram sum
+  const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
+  const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
+  uint32_t kv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = e0 + tid * kPer + i;
+    kv[i] = e < e1 ? (uint32_t)kr[e] : 0xffffffffu;
+  }
+  uint32_t tot, unused;
+  sum_strided2(hist1 + (int64_t)r * C1 * 256 + tid, C1, 256, 0, tot, unused);
   s_h[tid] = tot;
   s_h2[tid] = 0;
   if (tid == 0) s_gt = 0;
@@ -114,17 +173,9 @@ __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
     info[r * 4 + 0] = b1;
     info[r * 4 + 1] = s_res[1];
   }
-  const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
   uint32_t gt = 0;
-  const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
-  uint32_t kv[kChunk / kThreads];
 #pragma unroll
-  for (int i = 0; i < kChunk / kThreads; ++i) {
-    const int e = e0 + i * kThreads + tid;
-    kv[i] = e < e1 ? (uint32_t)kr[e] : 0xffffffffu;
-  }
-#pragma unroll
-  for (int i = 0; i < kChunk / kThreads; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     if (kv[i] == 0xffffffffu) continue;
     const uint32_t hi = kv[i] >> 8;
     if (hi == b1) atomicAdd(&s_h2[kv[i] & 255u], 1u);
@@ -141,20 +192,20 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
     KeySrc ks, int R, int n, int k, int C, const uint32_t* __restrict__ hist2,
     const uint32_t* __restrict__ gtc, const uint32_t* __restrict__ info, int cand_start,
     OUT_T* __restrict__ out, int64_t out_stride) {
-  __shared__ uint32_t s_tot[256], s_pre[256], s_wsum[kWaves], s_res[2];
-  __shared__ uint32_t s_wsel[kWaves], s_wtie[kWaves], s_red[kWaves];
+  __shared__ uint32_t s_tot[256], s_pre[256], s_wsum[kWaves], s_res[2], s_red[kWaves];
   const int r = blockIdx.x % R, c = blockIdx.x / R;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t b1 = info[r * 4 + 0], gt1 = info[r * 4 + 1];
-
-  uint32_t tot = 0, pre = 0;
-  const uint32_t* h2 = hist2 + (int64_t)r * C * 256 + tid;
-#pragma unroll 16
-  for (int cc = 0; cc < C; ++cc) {
-    const uint32_t v = h2[(int64_t)cc * 256];
-    tot += v;
-    pre += cc < c ? v : 0u;
+  const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
+  const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
+  uint32_t kv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = e0 + tid * kPer + i;
+    kv[i] = e < e1 ? (uint32_t)kr[e] : 0u;
   }
+  const uint32_t b1 = info[r * 4 + 0], gt1 = info[r * 4 + 1];
+  uint32_t tot, pre;
+  sum_strided2(hist2 + (int64_t)r * C * 256 + tid, C, 256, c, tot, pre);
   s_tot[tid] = tot;
   s_pre[tid] = pre;
   // Selected-above-threshold count of earlier chunks: gtc prefix.
@@ -177,47 +228,32 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
   for (int w = 0; w < kWaves; ++w) base += s_red[w];
   base += min(need, ties_before);
 
-  const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
-  const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
-  OUT_T* orow = out + (int64_t)r * out_stride;
-  uint32_t sel_run = base, tie_run = ties_before;
-  uint32_t kv[kChunk / kThreads];
+  // Ordered compaction: each thread owns kPer consecutive candidates.
+  uint32_t ntie = 0, ngt = 0;
 #pragma unroll
-  for (int i = 0; i < kChunk / kThreads; ++i) {
-    const int e = e0 + i * kThreads + tid;
-    kv[i] = e < e1 ? (uint32_t)kr[e] : 0u;
+  for (int i = 0; i < kPer; ++i) {
+    const bool valid = e0 + tid * kPer + i < e1;
+    ntie += (valid && kv[i] == tau) ? 1u : 0u;
+    ngt += (valid && kv[i] > tau) ? 1u : 0u;
   }
+  uint32_t all_ties;
+  const uint32_t tie_rank0 = ties_before + block_exclusive_scan(ntie, s_wsum, &all_ties);
+  // ties this thread may take: ranks [tie_rank0, tie_rank0 + ntie) below need
+  const uint32_t take = tie_rank0 >= need ? 0u : min(ntie, need - tie_rank0);
+  uint32_t all_sel;
+  uint32_t pos = base + block_exclusive_scan(ngt + take, s_wsum, &all_sel);
+  OUT_T* orow = out + (int64_t)r * out_stride;
+  uint32_t taken = 0;
 #pragma unroll
-  for (int i = 0; i < kChunk / kThreads; ++i) {
-    const int e0r = e0 + i * kThreads;
-    if (e0r >= e1) break;
-    const int e = e0r + tid;
-    const bool valid = e < e1;
-    const uint32_t key = kv[i];
-    const bool is_gt = valid && key > tau;
-    const bool is_tie = valid && key == tau;
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    const uint64_t mtie = __ballot(is_tie);
-    if (lane == 0) s_wtie[wave] = (uint32_t)__popcll(mtie);
-    __syncthreads();
-    uint32_t tie_off = tie_run;
-    for (int w = 0; w < wave; ++w) tie_off += s_wtie[w];
-    const uint32_t my_tie_rank = tie_off + (uint32_t)__popcll(mtie & below);
-    const bool sel = is_gt || (is_tie && my_tie_rank < need);
-    const uint64_t msel = __ballot(sel);
-    if (lane == 0) s_wsel[wave] = (uint32_t)__popcll(msel);
-    __syncthreads();
-    uint32_t sel_off = sel_run;
-    uint32_t round_sel = 0, round_tie = 0;
-    for (int w = 0; w < kWaves; ++w) {
-      if (w < wave) sel_off += s_wsel[w];
-      round_sel += s_wsel[w];
-      round_tie += s_wtie[w];
+  for (int i = 0; i < kPer; ++i) {
+    const int e = e0 + tid * kPer + i;
+    if (e >= e1) continue;
+    bool sel = kv[i] > tau;
+    if (kv[i] == tau && taken < take) {
+      sel = true;
+      ++taken;
     }
-    if (sel) orow[sel_off + (uint32_t)__popcll(msel & below)] = (OUT_T)(cand_start + e);
-    sel_run += round_sel;
-    tie_run += round_tie;
-    __syncthreads();
+    if (sel) orow[pos++] = (OUT_T)(cand_start + e);
   }
 }
 
@@ -268,7 +304,9 @@ int run_levels(const Ws& w, KeySrc ks, int R, int n, int k, int C1, int cand_sta
   return LAP_OK;
 }
 
-int retrieve_chunk_bound(int T) { return (T + 1023) / 1024; }
+// Upper bound on the scorer's workgroup chunks per row: a chunk holds at
+// least one pass of the smallest launch shape (256 threads x 1 token).
+int retrieve_chunk_bound(int T) { return (T + 255) / 256; }
 
 }  // namespace
 }  // namespace lap
