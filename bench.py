@@ -43,6 +43,7 @@ CAP = 128            # extra capacity rows, as the reference's decode cache
 TOPK, SINK, LOCAL = 2048, 4, 64
 N_CODE_SETS, N_KV_SETS = 12, 4
 CODE_BYTES = HKV * T * M  # 33,554,432 algorithmic bytes per scorer launch
+CALIB_BYTES = 256 << 20   # copy-like calibration kernel: bytes read (= bytes written)
 
 
 def log(*a):
@@ -58,6 +59,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget for the CPU baseline sample")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    ap.add_argument("--counters", action="store_true",
+                    help="counter-collection pass: eager scorer launches over the rotating "
+                         "code sets, then a 256 MiB copy-like kernel (fp32 negate) that "
+                         "calibrates the HBM byte counters; prints one line, no JSON")
     return ap.parse_args()
 
 
@@ -168,6 +173,20 @@ def main():
         N.call("lap_retrieve_score", N.ptr(dec.lut), N.ptr(c), c.stride(0), c.stride(1),
                c.stride(2), 1, HKV, T, plan["cand_start"], plan["cand_end"], N.KEY_BF16, None,
                N.ptr(ws), ws.numel(), N.stream_of(c))
+
+    if args.counters:
+        # one LUT per set is enough: the scorer's traffic does not depend on it
+        sparse_step(0)
+        for i in range(2 * N_CODE_SETS):
+            score_only(i)
+        a = torch.randn(CALIB_BYTES // 4, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        print(f"counters pass: {2 * N_CODE_SETS} scorer launches of {CODE_BYTES} code bytes, "
+              f"3 fp32 negate launches of {CALIB_BYTES} bytes read + written", flush=True)
+        return
 
     log("warm-up")
     for i in range(max(args.warmup, 2)):
