@@ -18,6 +18,9 @@
 // is the first radix level of the top-k (topk.hip).
 #include "common.h"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace lap {
 
 // Tunables of the fast scorer (read once from the environment; documented in
@@ -140,6 +143,143 @@ __global__ __launch_bounds__(THREADS) void score_g4_kernel(
         if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
         if (so.hist && t >= so.cand_start && t < so.cand_end) atomicAdd(&s_hist[key >> 8], 1u);
       }
+    }
+  }
+
+  if (so.hist) {
+    __syncthreads();
+    const int nchunk = gridDim.x / R;
+    uint32_t* dst = so.hist + ((int64_t)r * nchunk + chunk) * 256;
+    for (int i = tid; i < 256; i += THREADS) dst[i] = s_hist[i];
+  }
+}
+
+// Pipelined fused scorer (GMKG table only).  A workgroup owns THREADS * TOK
+// consecutive tokens of one KV row; thread tid scores tokens
+// t0 + j * THREADS + tid, j < TOK, as TOK stages.  Every CU of the chip
+// starts at once, so requesting all code rows up front lets the memory
+// system share bandwidth evenly and complete every wave's rows near the end
+// of the whole stream, after which all CUs compute with HBM idle.  Instead a
+// thread keeps PREF stages in flight: it requests stage j + PREF only when
+// stage j has arrived, so early stages complete early and the lookups of
+// stage j overlap the stream of the later ones.  The table slice is
+// requested first; vector-memory loads return in issue order (vmcnt), so the
+// table is written to LDS while code rows are still in flight, and the
+// barrier after the fill orders LDS only.
+//
+// The loads are issued from inline asm because their order is the point and
+// the compiler may reorder independent loads; every loaded value is tied to
+// the s_waitcnt that covers it, so no instruction reads it early.  A wait
+// for n outstanding operations is safe with stores in flight too: stores
+// only add to the count, which makes the wait longer, never shorter.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 gload16_ordered(const void* p) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void vmw1(u32x4& a) {
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(a) : "n"(N));
+}
+template <int N>
+__device__ __forceinline__ void vmw2(u32x4& a, u32x4& b) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
+}
+// Wait until at most n vector-memory operations are outstanding; n is a
+// compile-time constant after unrolling, so the switch folds away.
+__device__ __forceinline__ void vm_wait(int n, u32x4& a) {
+  switch (n) {
+#define LAP_VW(N) case N: vmw1<N>(a); break;
+    LAP_VW(0) LAP_VW(1) LAP_VW(2) LAP_VW(3) LAP_VW(4) LAP_VW(5) LAP_VW(6) LAP_VW(7)
+    LAP_VW(8) LAP_VW(9) LAP_VW(10) LAP_VW(11) LAP_VW(12) LAP_VW(13) LAP_VW(14) LAP_VW(15)
+    LAP_VW(16) LAP_VW(17) LAP_VW(18) LAP_VW(19) LAP_VW(20) LAP_VW(21) LAP_VW(22) LAP_VW(23)
+#undef LAP_VW
+    default: vmw1<0>(a);
+  }
+}
+__device__ __forceinline__ void vm_wait(int n, u32x4& a, u32x4& b) {
+  switch (n) {
+#define LAP_VW(N) case N: vmw2<N>(a, b); break;
+    LAP_VW(0) LAP_VW(2) LAP_VW(4) LAP_VW(6) LAP_VW(8) LAP_VW(10) LAP_VW(12) LAP_VW(14)
+    LAP_VW(16)
+#undef LAP_VW
+    default: vmw2<0>(a, b);
+  }
+}
+
+__device__ __forceinline__ uint4 as_uint4(const u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
+template <int THREADS, int TOK, int PREF>
+__global__ __launch_bounds__(THREADS) void score_g4p_kernel(
+    const uint16_t* __restrict__ lut, const uint8_t* __restrict__ codes, int64_t cs_b,
+    int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, ScoreOut so, _Float16 one) {
+  constexpr int kFill = kLutBytes / 16 / THREADS;  // table uint4s per thread
+  constexpr int kAhead = PREF < TOK ? PREF : TOK;  // stages requested up front
+  static_assert(kFill * THREADS * 16 == kLutBytes && THREADS >= 256, "bad THREADS");
+  static_assert(kFill + 2 * kAhead <= 23 && 2 * kAhead <= 16, "vmcnt range");
+  __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
+  __shared__ uint32_t s_hist[256];
+
+  const int r = blockIdx.x % R;
+  const int chunk = blockIdx.x / R;
+  const int tid = threadIdx.x;
+  const int b = r / Hkv, hkv = r - b * Hkv;
+  const int t0 = chunk * (THREADS * TOK);
+  const int t1 = min(T, t0 + THREADS * TOK);  // t1 > t0 by the grid
+
+  const uint4* src = reinterpret_cast<const uint4*>(lut + (int64_t)r * (kG * kM * kK));
+  u32x4 f[kFill];
+#pragma unroll
+  for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * THREADS + tid);
+
+  // Rows past the chunk end load the chunk's last row (always in bounds) and
+  // are discarded after scoring.
+  const uint8_t* crow = codes + (int64_t)b * cs_b + (int64_t)hkv * cs_h;
+  u32x4 c[TOK][2];
+  auto request = [&](int j) {
+    const int t = min(t0 + j * THREADS + tid, t1 - 1);
+    const uint8_t* p = crow + (int64_t)t * cs_t;
+    c[j][0] = gload16_ordered(p);
+    c[j][1] = gload16_ordered(p + 16);
+  };
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) request(j);
+
+#pragma unroll
+  for (int i = 0; i < kFill; ++i) {
+    vm_wait(kFill - 1 - i + 2 * kAhead, f[i]);
+    s_lut[i * THREADS + tid] = as_uint4(f[i]);
+  }
+  if (tid < 256) s_hist[tid] = 0;
+  lds_barrier();
+
+  const char* lds = reinterpret_cast<const char*>(s_lut);
+#pragma unroll
+  for (int j = 0; j < TOK; ++j) {
+    // Stages requested after stage j so far: j+1 .. min(j+kAhead-1, TOK-1).
+    const int later = (j + kAhead - 1 < TOK - 1 ? j + kAhead - 1 : TOK - 1) - j;
+    vm_wait(2 * later, c[j][0], c[j][1]);
+    if (j + kAhead < TOK) request(j + kAhead);
+    float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
+    score_token(lds, as_uint4(c[j][0]), as_uint4(c[j][1]), one, e0, e1, e2, e3);
+    const int t = t0 + j * THREADS + tid;
+    if (t >= t1) continue;
+    if (so.heads) {
+      uint16_t* hp = so.heads + (int64_t)(r * kG) * T + t;
+      hp[0] = f2h(e0);
+      hp[(int64_t)T] = f2h(e1);
+      hp[2 * (int64_t)T] = f2h(e2);
+      hp[3 * (int64_t)T] = f2h(e3);
+    }
+    if (so.keys || so.hist) {
+      // fp16 rounding is monotone, so fp16(max) == max of the fp16 scores.
+      const uint16_t hm = f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
+      const uint32_t key = so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(hm) : f16_key(hm);
+      if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
+      if (so.hist && t >= so.cand_start && t < so.cand_end) atomicAdd(&s_hist[key >> 8], 1u);
     }
   }
 
@@ -290,49 +430,133 @@ inline _Float16 f16_one() { return (_Float16)1.0f; }
 
 }  // namespace
 
+// Launch plan of the fast G=4 scorer.  kind 0: score_g4_kernel (any table
+// layout); kind 1: the pipelined score_g4p_kernel<threads, tok> (GMKG table).
+struct G4Plan {
+  int kind, threads, tok, pref, chunk_tokens, nchunk;
+};
+
+// LAPRUNE_SCORE_CFG overrides the choice for measurements: "legacy" or
+// "<threads>x<tok>p<pref>" (threads in {256, 512, 1024}, tok in {1, 2, 4, 8},
+// pref in {1, 2, tok}).
+static bool score_cfg_override(int* threads, int* tok, int* pref, bool* legacy) {
+  static const char* e = getenv("LAPRUNE_SCORE_CFG");
+  if (!e || !*e) return false;
+  if (strcmp(e, "legacy") == 0) {
+    *legacy = true;
+    return true;
+  }
+  int th = 0, tk = 0, pf = 0;
+  if (sscanf(e, "%dx%dp%d", &th, &tk, &pf) != 3) return false;
+  if (!(th == 256 || th == 512 || th == 1024) || !(tk == 1 || tk == 2 || tk == 4 || tk == 8))
+    return false;
+  if (!(pf == 1 || pf == 2 || pf == tk)) return false;
+  *threads = th;
+  *tok = tk;
+  *pref = pf;
+  *legacy = false;
+  return true;
+}
+
+static int g4_plan(int R, int T, bool lut_il, G4Plan* p) {
+  DevInfo di;
+  int s = device_info(&di);
+  if (s != LAP_OK) return s;
+  int th = 0, tk = 0, pf = 1;
+  bool legacy = !lut_il;
+  const bool forced = score_cfg_override(&th, &tk, &pf, &legacy);
+  if (legacy || !lut_il) {
+    constexpr int THREADS = 512;
+    const int target_wgs = di.cu_count * score_wg_per_cu();
+    int nchunk = (target_wgs + R - 1) / R;
+    // Tokens per workgroup rounded up to whole passes of the token loop.
+    int chunk_tokens = (T + nchunk - 1) / nchunk;
+    chunk_tokens = (chunk_tokens + 2 * THREADS - 1) / (2 * THREADS) * (2 * THREADS);
+    if (chunk_tokens < 2 * THREADS) chunk_tokens = 2 * THREADS;
+    nchunk = (T + chunk_tokens - 1) / chunk_tokens;
+    *p = G4Plan{0, THREADS, 0, 0, chunk_tokens, nchunk < 1 ? 1 : nchunk};
+    return LAP_OK;
+  }
+  if (!forced) {
+    // Largest chunk that still gives every CU a workgroup; the smallest
+    // shape when even that cannot.
+    static const int kShapes[][3] = {{1024, 4, 1}, {512, 4, 1}, {512, 2, 1}, {256, 2, 1},
+                                     {256, 1, 1}};
+    th = 256;
+    tk = 1;
+    pf = 1;
+    for (const auto& sh : kShapes) {
+      const int ct = sh[0] * sh[1];
+      if ((int64_t)R * ((T + ct - 1) / ct) >= di.cu_count) {
+        th = sh[0];
+        tk = sh[1];
+        pf = sh[2];
+        break;
+      }
+    }
+  }
+  const int ct = th * tk;
+  *p = G4Plan{1, th, tk, pf, ct, (T + ct - 1) / ct};
+  return LAP_OK;
+}
+
+template <int TH, int TK, int PF>
+static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, const uint8_t* codes,
+                       int64_t cs_b, int64_t cs_h, int64_t cs_t, int Hkv, int R, int T,
+                       const ScoreOut& so) {
+  hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF>), grid, dim3(TH), 0, st, lut, codes, cs_b,
+                     cs_h, cs_t, Hkv, R, T, so, f16_one());
+}
+
 // Launch the fast G=4 scorer.  Exposed to the fused retrieval entry point.
 int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int64_t cs_b,
                     int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, uint16_t* heads,
                     uint16_t* keys, uint32_t* hist, int key_mode, int cand_start,
                     int cand_end, int* nchunk_out, hipStream_t st) {
-  DevInfo di;
-  int s = device_info(&di);
-  if (s != LAP_OK) return s;
   const int R = B * Hkv;
-  constexpr int THREADS = 512;
-  const int target_wgs = di.cu_count * score_wg_per_cu();
-  int nchunk = (target_wgs + R - 1) / R;
-  // Tokens per workgroup rounded up to whole passes of the token loop.
-  int chunk_tokens = (T + nchunk - 1) / nchunk;
-  chunk_tokens = (chunk_tokens + 2 * THREADS - 1) / (2 * THREADS) * (2 * THREADS);
-  if (chunk_tokens < 2 * THREADS) chunk_tokens = 2 * THREADS;
-  nchunk = (T + chunk_tokens - 1) / chunk_tokens;
-  if (nchunk < 1) nchunk = 1;
+  G4Plan pl;
+  int s = g4_plan(R, T, lut_il, &pl);
+  if (s != LAP_OK) return s;
   ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end};
-  dim3 grid((unsigned)(R * nchunk));
-  if (lut_il)
-    hipLaunchKernelGGL((score_g4_kernel<THREADS, true>), grid, dim3(THREADS), 0, st, lut,
-                       codes, cs_b, cs_h, cs_t, Hkv, R, T, chunk_tokens, so, f16_one());
-  else
-    hipLaunchKernelGGL((score_g4_kernel<THREADS, false>), grid, dim3(THREADS), 0, st, lut,
-                       codes, cs_b, cs_h, cs_t, Hkv, R, T, chunk_tokens, so, f16_one());
+  dim3 grid((unsigned)(R * pl.nchunk));
+  if (pl.kind == 0) {
+    if (lut_il)
+      hipLaunchKernelGGL((score_g4_kernel<512, true>), grid, dim3(512), 0, st, lut, codes, cs_b,
+                         cs_h, cs_t, Hkv, R, T, pl.chunk_tokens, so, f16_one());
+    else
+      hipLaunchKernelGGL((score_g4_kernel<512, false>), grid, dim3(512), 0, st, lut, codes, cs_b,
+                         cs_h, cs_t, Hkv, R, T, pl.chunk_tokens, so, f16_one());
+  } else {
+    const int key = (pl.threads * 16 + pl.tok) * 16 + pl.pref;
+    switch (key) {
+#define LAP_G4P(TH, TK, PF)                                                               \
+  case (TH * 16 + TK) * 16 + PF:                                                          \
+    launch_g4p<TH, TK, PF>(grid, st, lut, codes, cs_b, cs_h, cs_t, Hkv, R, T, so);        \
+    break;
+      LAP_G4P(1024, 4, 1) LAP_G4P(1024, 4, 2) LAP_G4P(1024, 4, 4)
+      LAP_G4P(1024, 2, 1) LAP_G4P(1024, 2, 2) LAP_G4P(1024, 8, 1) LAP_G4P(1024, 8, 2)
+      LAP_G4P(512, 8, 1) LAP_G4P(512, 8, 2) LAP_G4P(512, 4, 1) LAP_G4P(512, 4, 2)
+      LAP_G4P(512, 4, 4) LAP_G4P(512, 2, 1) LAP_G4P(512, 2, 2)
+      LAP_G4P(256, 8, 1) LAP_G4P(256, 8, 2) LAP_G4P(256, 4, 1) LAP_G4P(256, 2, 1)
+      LAP_G4P(256, 1, 1)
+#undef LAP_G4P
+      default:
+        set_error("score_g4: no kernel for %d threads x %d tokens (prefetch %d)", pl.threads,
+                  pl.tok, pl.pref);
+        return LAP_ERR_INVALID;
+    }
+  }
   LAP_LAUNCH_CHECK("score_g4_kernel");
-  if (nchunk_out) *nchunk_out = nchunk;
+  if (nchunk_out) *nchunk_out = pl.nchunk;
   return LAP_OK;
 }
 
-// Number of workgroup chunks launch_score_g4 will use for T tokens, R rows.
+// Number of workgroup chunks launch_score_g4 uses for the GMKG table with T
+// tokens and R rows (the level-1 histogram count of the fused top-k).
 int score_g4_nchunk(int R, int T) {
-  DevInfo di;
-  if (device_info(&di) != LAP_OK) return -1;
-  constexpr int THREADS = 512;
-  const int target_wgs = di.cu_count * score_wg_per_cu();
-  int nchunk = (target_wgs + R - 1) / R;
-  int chunk_tokens = (T + nchunk - 1) / nchunk;
-  chunk_tokens = (chunk_tokens + 2 * THREADS - 1) / (2 * THREADS) * (2 * THREADS);
-  if (chunk_tokens < 2 * THREADS) chunk_tokens = 2 * THREADS;
-  nchunk = (T + chunk_tokens - 1) / chunk_tokens;
-  return nchunk < 1 ? 1 : nchunk;
+  G4Plan pl;
+  if (g4_plan(R, T, true, &pl) != LAP_OK) return -1;
+  return pl.nchunk;
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
