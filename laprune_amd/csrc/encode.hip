@@ -23,12 +23,17 @@
 // residual lives in LDS and is read as a broadcast.
 #include "common.h"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace lap {
 namespace {
 
 struct Prep {
-  float* ct;  // [M][D][K]
-  float* cn;  // [M][K]
+  float* ct;       // [M][D][K]
+  float* cn;       // [M][K]
+  float* scn;      // [M][K] sqrtf(cn)
+  uint16_t* frag;  // bf16 MFMA B fragments [M][K/16][D/16][64 lanes][4] (K % 16 == 0)
   size_t bytes;
 };
 
@@ -40,6 +45,10 @@ Prep carve_prep(void* base, int M, int K, int D) {
   off = align_up(off + (size_t)M * D * K * 4, 256);
   p.cn = reinterpret_cast<float*>(b ? b + off : nullptr);
   off = align_up(off + (size_t)M * K * 4, 256);
+  p.scn = reinterpret_cast<float*>(b ? b + off : nullptr);
+  off = align_up(off + (size_t)M * K * 4, 256);
+  p.frag = reinterpret_cast<uint16_t*>(b ? b + off : nullptr);
+  if (K % 16 == 0) off = align_up(off + (size_t)M * K * D * 2, 256);
   p.bytes = off;
   return p;
 }
@@ -72,7 +81,8 @@ __global__ __launch_bounds__(256) void encode_prep_transpose(const float* __rest
 }
 
 __global__ __launch_bounds__(256) void encode_prep_norms(const float* __restrict__ cb, int M,
-                                                         int K, int D, float* __restrict__ cn) {
+                                                         int K, int D, float* __restrict__ cn,
+                                                         float* __restrict__ scn) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= M * K) return;
   const float* row = cb + (int64_t)i * D;
@@ -85,6 +95,7 @@ __global__ __launch_bounds__(256) void encode_prep_norms(const float* __restrict
     s[j] = a;
   }
   cn[i] = fold16(s);
+  scn[i] = sqrtf(cn[i]);
 }
 
 // dot16(r, r) over a row held in LDS: lanes 0..15 each run one chain, the
@@ -174,10 +185,397 @@ __global__ __launch_bounds__(256) void encode_greedy_kernel(
   if (live && lane == 0 && rnorm) rnorm[row] = sqrtf(rn);
 }
 
+// ------------------------------------------------------------------ MFMA path
+// The same greedy recurrence with the distance search split in two:
+//   coarse: G_k = (rn + cn_k) - 2 * Dm_k, where Dm_k = r . C_k from
+//           v_mfma_f32_16x16x16_bf16 on bf16-rounded inputs;
+//   exact:  E_k = (rn + cn_k) - 2 * dot16(r, C_k) (the contract) for every k
+//           that the coarse pass cannot rule out.
+// Error bound.  With S_k = sum_d |r_d C_k,d| <= sqrt(rn * cn_k) (up to the
+// relative error of the fp32 norms), bf16 rounding of both inputs moves each
+// product by at most 2^-8 (1 + 2^-10) |r_d C_d|, fp32 accumulation of the 128
+// exact products adds at most 128 * 2^-24 S_k, and dot16 differs from the
+// exact dot by at most 12 * 2^-24 S_k; so |Dm_k - dot16_k| < 1.02 * 2^-8 S_k
+// and |G_k - E_k| < 2^-7 * 1.03 * S_k + 2u (|A_k| + 2 |Dm_k|) (u = 2^-24, the
+// two roundings of the final subtraction).  eps_k doubles both terms and adds
+// an absolute term for flushed subnormals.  Entry k is ruled out only when
+//   fl(G_k - eps_k) > U,  U = min_j fl(G_j + eps_j),
+// which implies E_k > E_j for the entry j attaining U, so the exact minimum
+// and all its ties survive; written as !(G_k - eps_k > U), non-finite
+// values are never ruled out (NaN rows fall back to a full exact scan).
+// The exact pass keeps the contract's lowest-index tie rule; NaN and +inf
+// never win, as in the strict-< scan, and a row with no finite distance gets
+// code 0.
+//
+// A workgroup owns 16 rows and runs all M stages; wave w covers N-tiles
+// w, w + WAVES, ...  Stage m + 1's B fragments and norms are loaded while
+// stage m runs.
+typedef short bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int D>
+struct EncCfg {
+  static constexpr int KS = D / 16;             // MFMA k-steps per tile
+  static constexpr int TPW = D == 256 ? 2 : 4;  // N-tiles per wave
+  static constexpr int WAVES = 16 / TPW;        // covers K <= 256 (16 tiles)
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int L = D / 16;              // dot16 chain length
+  static constexpr int CAP = D == 256 ? 2 : 4;  // exact rechecks loaded per batch
+};
+
+__global__ __launch_bounds__(256) void encode_prep_frag(const float* __restrict__ cb, int M,
+                                                        int K, int D,
+                                                        uint16_t* __restrict__ frag) {
+  // One thread per (m, tile, ks, lane): four bf16 of C[m][tile*16 + l%16][ks*16 + 4*(l/16) ..].
+  const int KS = D / 16, NT = K / 16;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)M * NT * KS * 64;
+  if (i >= total) return;
+  const int l = (int)(i % 64);
+  int64_t q = i / 64;
+  const int ks = (int)(q % KS);
+  q /= KS;
+  const int tile = (int)(q % NT);
+  const int m = (int)(q / NT);
+  const int k = tile * 16 + (l & 15);
+  const int d = ks * 16 + 4 * (l >> 4);
+  const float* src = cb + ((int64_t)m * K + k) * D + d;
+  uint16_t* dst = frag + i * 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[e] = f2bf(src[e]);
+}
+
+// Cross-lane moves within a row of 16 lanes (DPP, no LDS round trip).
+// row_shl:n gives lane i the value of lane i + n of its row (0 past the end).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+// dot16 fold of the 16 chain sums held by the lanes of a row, leaving s_0 in
+// every lane.  Step w adds the value rotated by w within the row.  After the
+// steps for 8, ..., 2w the row's values repeat with period 2w, so the lane at
+// rotation distance w holds the value of lane j ^ w: lanes j < w compute
+// s_j + s_{j+w} (the contract's pairing) and every other lane a copy of one
+// of those sums (fp32 addition is commutative).
+__device__ __forceinline__ float row_fold16(float a) {
+  a = a + dpp_f<0x128>(a);  // row_ror:8
+  a = a + dpp_f<0x124>(a);  // row_ror:4
+  a = a + dpp_f<0x122>(a);  // row_ror:2
+  a = a + dpp_f<0x121>(a);  // row_ror:1
+  return a;
+}
+// Minimum over the 16 lanes of a row, in every lane (row_ror rotations).
+__device__ __forceinline__ float row_min16(float a) {
+  a = fminf(a, dpp_f<0x128>(a));  // row_ror:8
+  a = fminf(a, dpp_f<0x124>(a));  // row_ror:4
+  a = fminf(a, dpp_f<0x122>(a));  // row_ror:2
+  a = fminf(a, dpp_f<0x121>(a));  // row_ror:1
+  return a;
+}
+
+template <int D>
+struct EncStage {
+  uint2 b[EncCfg<D>::TPW][EncCfg<D>::KS];
+  float cn[EncCfg<D>::TPW];
+  float scn[EncCfg<D>::TPW];
+};
+
+// Stage m's fragments and norms for this wave's tiles.  Tiles past K load
+// tile NT - 1 (in bounds, results ignored), so the loads are branch-free and
+// the compiler's wait counts stay exact.
+template <int D>
+__device__ __forceinline__ void enc_load_stage(EncStage<D>& st, const uint2* __restrict__ frag,
+                                               const float* __restrict__ cn,
+                                               const float* __restrict__ scn, int m, int NT,
+                                               int K, int wave, int lane) {
+  using C = EncCfg<D>;
+#pragma unroll
+  for (int i = 0; i < C::TPW; ++i) {
+    const int tile = min(wave + i * C::WAVES, NT - 1);
+    const uint2* f = frag + (((int64_t)m * NT + tile) * C::KS) * 64 + lane;
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) st.b[i][ks] = f[ks * 64];
+    const int64_t ci = (int64_t)m * K + tile * 16 + (lane & 15);
+    st.cn[i] = cn[ci];
+    st.scn[i] = scn[ci];
+  }
+}
+
+// Four fp32 -> bf16 (round to nearest even; v_cvt_pk_bf16_f32) packed in 8 bytes.
+__device__ __forceinline__ uint2 bf16x4_bits(const float4 v) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t lo = {(__bf16)v.x, (__bf16)v.y};
+  const bf16x2_t hi = {(__bf16)v.z, (__bf16)v.w};
+  return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+}
+
+template <int D>
+struct EncShared {
+  float r[16][D];
+  uint16_t rb[16][D];  // bf16(r): the MFMA A operand
+  float rn[16];
+  float u[EncCfg<D>::WAVES][16];
+  uint32_t cnt[16];       // survivors of the coarse pass per row
+  uint8_t list[16][256];  // their entries, in no particular order
+};
+
+// Pull this workgroup's quarter of codebook m (fp32) into L2 ahead of the
+// exact recheck: one dword per 128-byte line.  Workgroups are dealt
+// round-robin to the 8 XCDs, so the four workgroups b, b + 8, b + 16, b + 24
+// share an L2 and each takes a different quarter.  The value is consumed a
+// stage later (folded into a sink the kernel keeps alive), so the compiler
+// waits for it only then.
+template <int D>
+__device__ __forceinline__ uint32_t enc_prefetch_l2(const float* __restrict__ cb, int m, int K,
+                                                    int wave, int lane) {
+  using C = EncCfg<D>;
+  const int64_t words = (int64_t)K * D;     // fp32 words of codebook m
+  const int64_t q = words / 4;              // this workgroup's quarter
+  const int64_t lo = ((blockIdx.x >> 3) & 3) * q;
+  int64_t w = lo + ((int64_t)lane * C::WAVES + wave) * 32;  // one word per 128-byte line
+  w = w < words - 1 ? w : words - 1;
+  return __builtin_bit_cast(uint32_t, cb[(int64_t)m * words + w]);
+}
+
+// One greedy stage for the workgroup's 16 rows.  On entry s.r holds the
+// residuals and s.rn their dot16 norms; on exit both are updated and codes
+// for stage m are written.  The barriers order LDS only, so the next stage's
+// fragment loads stay in flight across them.
+template <int D>
+__device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st,
+                                          const float* __restrict__ cb,
+                                          const float* __restrict__ cn, int m, int K, int NT,
+                                          int row0, int N, uint8_t* __restrict__ codes,
+                                          int64_t c_rs, int wave, int lane, int tid) {
+  using C = EncCfg<D>;
+  // A fragments: row l%16, d = ks*16 + 4*(l/16) + e, from the bf16 copy.
+  bf16x4_t a[C::KS];
+  {
+    const uint16_t* rr = s.rb[lane & 15] + 4 * (lane >> 4);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks)
+      a[ks] = __builtin_bit_cast(bf16x4_t, *reinterpret_cast<const uint2*>(rr + ks * 16));
+  }
+  f32x4_t acc[C::TPW];
+#pragma unroll
+  for (int i = 0; i < C::TPW; ++i) {
+    acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks)
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+          a[ks], __builtin_bit_cast(bf16x4_t, st.b[i][ks]), acc[i], 0, 0, 0);
+  }
+  // acc[i][e]: row 4*(lane/16) + e, entry k = (wave + i*WAVES)*16 + lane%16.
+  float g_lo[C::TPW][4], g_hi[C::TPW][4];
+  float umin[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = 4 * (lane >> 4) + e;
+    const float rn = s.rn[row];
+    // v_sqrt_f32 (within an ulp or so): the 1.0078 factor of the first eps
+    // term absorbs the rounding of both square roots and their product.
+    const float srn = __builtin_amdgcn_sqrtf(rn);
+#pragma unroll
+    for (int i = 0; i < C::TPW; ++i) {
+      const float cnk = st.cn[i];
+      const float A = rn + cnk;
+      const float dm = acc[i][e];
+      const float g = A - 2.0f * dm;
+      const float eps = 0x1.02p-6f * (srn * st.scn[i]) + 0x1p-21f * (fabsf(A) + 2.0f * fabsf(dm)) +
+                        0x1p-116f * (1.0f + srn + st.scn[i]);
+      const bool live = wave + i * C::WAVES < NT;
+      g_lo[i][e] = live ? g - eps : INFINITY;
+      g_hi[i][e] = live ? g + eps : INFINITY;
+      umin[e] = fminf(umin[e], g_hi[i][e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) umin[e] = row_min16(umin[e]);
+  if ((lane & 15) == 0)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s.u[wave][4 * (lane >> 4) + e] = umin[e];
+  lds_barrier();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = 4 * (lane >> 4) + e;
+    float U = s.u[0][row];
+#pragma unroll
+    for (int w = 1; w < C::WAVES; ++w) U = fminf(U, s.u[w][row]);
+    uint32_t keep = 0;
+#pragma unroll
+    for (int i = 0; i < C::TPW; ++i)
+      keep |= (uint32_t)(wave + i * C::WAVES < NT && !(g_lo[i][e] > U)) << i;
+    // Only lanes holding survivors (about 1.7 per row) reserve list slots.
+    if (keep) {
+      uint32_t slot = atomicAdd(&s.cnt[row], (uint32_t)__builtin_popcount(keep));
+#pragma unroll
+      for (int i = 0; i < C::TPW; ++i)
+        if (keep & (1u << i)) s.list[row][slot++] = (uint8_t)((wave + i * C::WAVES) * 16 + (lane & 15));
+    }
+  }
+  lds_barrier();
+  // Group g < 16 (16 lanes) owns row g: it rechecks the row's survivors with
+  // the exact dot16 (lane j runs chain j), keeps the winner's fp32 chunk in
+  // registers, and updates its residual chunk and norm without another
+  // barrier.  Ties go to the lowest entry; NaN and +inf never win; no finite
+  // distance leaves code 0.
+  const int grp = wave * 4 + (lane >> 4), j = lane & 15;
+  if (grp < 16) {
+    const int row = grp;
+    float rc[C::L];
+#pragma unroll
+    for (int t = 0; t < C::L; t += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&s.r[row][j * C::L + t]);
+      rc[t] = v.x;
+      rc[t + 1] = v.y;
+      rc[t + 2] = v.z;
+      rc[t + 3] = v.w;
+    }
+    const float rn = s.rn[row];
+    const uint32_t n = s.cnt[row];
+    if (j == 0) s.cnt[row] = 0;  // ready for the next stage (read above by the whole group)
+    float bc[C::L];
+#pragma unroll
+    for (int t = 0; t < C::L; ++t) bc[t] = 0.f;
+    float best = 0.f;
+    int bk = -1;
+    // Batches of CAP survivors: all their loads are issued before any
+    // is used, so a batch costs one memory latency.
+    for (uint32_t base = 0; base < n; base += C::CAP) {
+      const uint32_t word = C::CAP == 4 ? *reinterpret_cast<const uint32_t*>(&s.list[row][base])
+                                        : *reinterpret_cast<const uint16_t*>(&s.list[row][base]);
+      int kq[C::CAP];
+      float c[C::CAP][C::L], cnk[C::CAP];
+#pragma unroll
+      for (int q = 0; q < C::CAP; ++q) {
+        // entries past n repeat the batch's first (in bounds; not evaluated)
+        kq[q] = base + q < n ? (int)((word >> (8 * q)) & 0xffu) : (int)(word & 0xffu);
+        const float* cr = cb + ((int64_t)m * K + kq[q]) * D + j * C::L;
+#pragma unroll
+        for (int t = 0; t < C::L; t += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(cr + t);
+          c[q][t] = v.x;
+          c[q][t + 1] = v.y;
+          c[q][t + 2] = v.z;
+          c[q][t + 3] = v.w;
+        }
+        cnk[q] = cn[(int64_t)m * K + kq[q]];
+      }
+#pragma unroll
+      for (int q = 0; q < C::CAP; ++q) {
+        float dot = 0.f;
+#pragma unroll
+        for (int t = 0; t < C::L; ++t) dot = __builtin_fmaf(rc[t], c[q][t], dot);
+        dot = row_fold16(dot);
+        const float E = (rn + cnk[q]) - 2.0f * dot;
+        const int k = kq[q];
+        if (base + q < n && !(E != E) && E != INFINITY &&
+            (bk < 0 || E < best || (E == best && k < bk))) {
+          best = E;
+          bk = k;
+#pragma unroll
+          for (int t = 0; t < C::L; ++t) bc[t] = c[q][t];
+        }
+      }
+    }
+    const int code = bk < 0 ? 0 : bk;
+    if (bk < 0) {
+      const float* cr = cb + (int64_t)m * K * D + j * C::L;
+#pragma unroll
+      for (int t = 0; t < C::L; ++t) bc[t] = cr[t];
+    }
+    float a2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < C::L; t += 4) {
+      float4 r4;
+      r4.x = rc[t] - bc[t];
+      r4.y = rc[t + 1] - bc[t + 1];
+      r4.z = rc[t + 2] - bc[t + 2];
+      r4.w = rc[t + 3] - bc[t + 3];
+      *reinterpret_cast<float4*>(&s.r[row][j * C::L + t]) = r4;
+      *reinterpret_cast<uint2*>(&s.rb[row][j * C::L + t]) = bf16x4_bits(r4);
+      a2 = __builtin_fmaf(r4.x, r4.x, a2);
+      a2 = __builtin_fmaf(r4.y, r4.y, a2);
+      a2 = __builtin_fmaf(r4.z, r4.z, a2);
+      a2 = __builtin_fmaf(r4.w, r4.w, a2);
+    }
+    a2 = row_fold16(a2);
+    if (j == 0) {
+      s.rn[row] = a2;
+      if (row0 + row < N) codes[(int64_t)(row0 + row) * c_rs + m] = (uint8_t)code;
+    }
+  }
+  lds_barrier();
+}
+
+template <int D>
+__global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
+    const float* __restrict__ x, int64_t x_rs, int N, const float* __restrict__ cb, int M,
+    int K, const uint2* __restrict__ frag, const float* __restrict__ cn,
+    const float* __restrict__ scn, uint8_t* __restrict__ codes, int64_t c_rs,
+    float* __restrict__ rnorm) {
+  using C = EncCfg<D>;
+  __shared__ __attribute__((aligned(16))) EncShared<D> s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * 16;
+  const int NT = K / 16;
+  for (int i = tid; i < 16 * D; i += C::THREADS) {
+    const int r = i / D, d = i - r * D;
+    const float v = row0 + r < N ? x[(int64_t)(row0 + r) * x_rs + d] : 0.f;
+    s.r[r][d] = v;
+    s.rb[r][d] = __builtin_bit_cast(uint16_t, (__bf16)v);
+  }
+  if (tid < 16) s.cnt[tid] = 0;
+  __syncthreads();
+  const int grp = wave * 4 + (lane >> 4), j = lane & 15;
+  if (grp < 16) {
+    const float* rr = s.r[grp] + j * C::L;
+    float a2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < C::L; ++t) a2 = __builtin_fmaf(rr[t], rr[t], a2);
+    a2 = row_fold16(a2);
+    if (j == 0) s.rn[grp] = a2;
+  }
+  __syncthreads();
+
+  // Stage m + 1's fragments are requested before stage m runs.  The request
+  // is unconditional (the last stage re-requests itself) so that no branch
+  // joins paths with different numbers of loads in flight, which would force
+  // the compiler to wait for all of them before the first MFMA.
+  EncStage<D> st0, st1;
+  enc_load_stage<D>(st0, frag, cn, scn, 0, NT, K, wave, lane);
+  uint32_t sink = 0, pfa = 0, pfb = 0;
+  for (int m = 0; m < M; m += 2) {
+    enc_load_stage<D>(st1, frag, cn, scn, min(m + 1, M - 1), NT, K, wave, lane);
+    pfb = enc_prefetch_l2<D>(cb, min(m + 1, M - 1), K, wave, lane);
+    enc_stage<D>(s, st0, cb, cn, m, K, NT, row0, N, codes, c_rs, wave, lane, tid);
+    sink ^= pfa;
+    if (m + 1 >= M) break;
+    enc_load_stage<D>(st0, frag, cn, scn, min(m + 2, M - 1), NT, K, wave, lane);
+    pfa = enc_prefetch_l2<D>(cb, min(m + 2, M - 1), K, wave, lane);
+    enc_stage<D>(s, st1, cb, cn, m + 1, K, NT, row0, N, codes, c_rs, wave, lane, tid);
+    sink ^= pfb;
+  }
+  sink ^= pfa ^ pfb;
+  if (sink == 0x9e3779b9u && N < 0) codes[0] = 0;  // never true: keeps the prefetch loads
+  if (tid < 16 && rnorm && row0 + tid < N) rnorm[row0 + tid] = sqrtf(s.rn[tid]);
+}
+
 }  // namespace
 }  // namespace lap
 
 using namespace lap;
+
+// LAPRUNE_ENCODE_IMPL=valu selects the all-VALU search (measurements and
+// cross-checks); the MFMA search is the default wherever K % 16 == 0.
+static bool encode_impl_mfma() {
+  static const bool v = [] {
+    const char* e = getenv("LAPRUNE_ENCODE_IMPL");
+    return !(e && strcmp(e, "valu") == 0);
+  }();
+  return v;
+}
 
 extern "C" int lap_encode_prep_size(int M, int K, int D, size_t* bytes) {
   clear_error();
@@ -201,8 +599,14 @@ extern "C" int lap_encode_prepare(const float* codebooks, int M, int K, int D, v
                      st, codebooks, M, K, D, p.ct);
   LAP_LAUNCH_CHECK("encode_prep_transpose");
   hipLaunchKernelGGL(encode_prep_norms, dim3((M * K + 255) / 256), dim3(256), 0, st, codebooks,
-                     M, K, D, p.cn);
+                     M, K, D, p.cn, p.scn);
   LAP_LAUNCH_CHECK("encode_prep_norms");
+  if (K % 16 == 0) {
+    const int64_t n = (int64_t)M * (K / 16) * (D / 16) * 64;
+    hipLaunchKernelGGL(encode_prep_frag, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       codebooks, M, K, D, p.frag);
+    LAP_LAUNCH_CHECK("encode_prep_frag");
+  }
   return LAP_OK;
 }
 
@@ -224,6 +628,21 @@ extern "C" int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, in
   LAP_CHECK((reinterpret_cast<uintptr_t>(p.ct) & 15) == 0, "lap_encode_greedy: prep misaligned");
   if (N == 0) return LAP_OK;
   hipStream_t st = as_stream(stream);
+  if (K % 16 == 0 && encode_impl_mfma()) {
+    dim3 g16((N + 15) / 16);
+    const uint2* fr = reinterpret_cast<const uint2*>(p.frag);
+#define LAP_ENCM(D_)                                                                         \
+  hipLaunchKernelGGL(encode_mfma_kernel<D_>, g16, dim3(EncCfg<D_>::THREADS), 0, st, x,       \
+                     x_row_stride, N, codebooks, M, K, fr, p.cn, p.scn, codes_out,          \
+                     codes_row_stride,                                                         \
+                     resid_norm)
+    if (D == 64) LAP_ENCM(64);
+    else if (D == 128) LAP_ENCM(128);
+    else LAP_ENCM(256);
+#undef LAP_ENCM
+    LAP_LAUNCH_CHECK("encode_mfma_kernel");
+    return LAP_OK;
+  }
   dim3 grid((N + 3) / 4);
 #define LAP_ENC(D_)                                                                          \
   hipLaunchKernelGGL(encode_greedy_kernel<D_>, grid, dim3(256), 0, st, x, x_row_stride, N,   \

@@ -294,6 +294,66 @@ def test_encode_bit_exact(dev, K, orc, N, D):
     assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
 
 
+@pytest.mark.parametrize("Kc,D", [(60, 64), (48, 128), (16, 64), (240, 128)])
+def test_encode_bit_exact_entry_counts(dev, K, orc, Kc, D):
+    """K % 16 != 0 takes the all-VALU search, the rest the MFMA search with
+    fewer entry tiles than waves."""
+    g = _gen(120 + Kc)
+    M, N = 8, 45
+    x = torch.randn(N, D, generator=g) * 2.0
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
+    torch.cuda.synchronize()
+    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
+    assert np.array_equal(codes.cpu().numpy(), want_c)
+    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+
+
+def test_encode_ties_and_near_ties(dev, K, orc):
+    """Duplicate entries (exact ties: the lowest index must win) and entries a
+    few ulps apart, far inside the bf16 coarse error, so the exact recheck
+    decides."""
+    g = _gen(130)
+    M, Kc, D, N = 6, 64, 128, 80
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    cb[:, 40] = cb[:, 7]                       # exact duplicate of an earlier entry
+    cb[:, 41] = cb[:, 7] * (1 + 2 ** -20)      # a hair away from it
+    cb[:, 63] = cb[:, 12].clone()
+    cb[:, 63, 0] = torch.nextafter(cb[:, 12, 0], torch.tensor(1.0))
+    # rows built from the duplicated entries so that they are the likely winners
+    x = torch.zeros(N, D)
+    for i in range(N):
+        k = [7, 40, 41, 12, 63][i % 5]
+        x[i] = sum(cb[m, k] for m in range(M)) + torch.randn(D, generator=g) * 1e-3
+    codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
+    torch.cuda.synchronize()
+    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
+    assert np.array_equal(codes.cpu().numpy(), want_c)
+    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+    assert 40 not in set(codes.cpu().numpy().ravel().tolist())  # ties go to entry 7
+
+
+def test_encode_non_finite_rows(dev, K, orc):
+    """Rows whose norms overflow or hold NaN take the full exact scan and
+    follow the contract (NaN and +inf distances never win; no finite
+    distance gives code 0)."""
+    g = _gen(140)
+    M, Kc, D, N = 4, 32, 64, 20
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    x = torch.randn(N, D, generator=g)
+    x[3, 5] = float("nan")
+    x[7] = 3e19            # rn overflows to +inf
+    x[11, 0] = float("inf")
+    codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
+    torch.cuda.synchronize()
+    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
+    assert np.array_equal(codes.cpu().numpy(), want_c)
+    got_r = rn.cpu().numpy()
+    assert np.array_equal(np.isnan(got_r), np.isnan(want_r))
+    fin = ~np.isnan(want_r)
+    assert np.array_equal(got_r[fin].view(np.uint32), want_r[fin].view(np.uint32))
+
+
 def test_fused_linear_encode_dropin(dev, K, orc):
     g = _gen(110)
     M, Kc, D, N = 32, 256, 128, 64
