@@ -22,6 +22,10 @@ so that the 256 MB Infinity Cache cannot serve the step from cache.
 ``dense_step_us`` the same GPU's split-K flash-decode over all 131072 tokens.
 ``cpu_baseline`` the reference's fp32 PyTorch scoring + bf16 cast + top-k
                  path (restated in oracle/ref_path.py) on the host cores.
+``encode``       configs[2] (C3): greedy AQ encode of one 64-token flush of
+                 post-RoPE keys (8 KV heads x 64 tokens = 512 rows, 32x256
+                 codebooks), MFMA coarse search + exact recheck, next to the
+                 reference's fp32 greedy path on the host cores.
 """
 from __future__ import annotations
 
@@ -44,6 +48,8 @@ TOPK, SINK, LOCAL = 2048, 4, 64
 N_CODE_SETS, N_KV_SETS = 12, 4
 CODE_BYTES = HKV * T * M  # 33,554,432 algorithmic bytes per scorer launch
 CALIB_BYTES = 256 << 20   # copy-like calibration kernel: bytes read (= bytes written)
+ENC_TOKENS, ENC_POS0, ROPE_THETA = 64, 131008, 500000.0
+ENC_FLOP = 2 * HKV * ENC_TOKENS * M * K * D  # 1,073,741,824 dot-product flops per flush
 
 
 def log(*a):
@@ -110,6 +116,40 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def c3_keys(g, dev):
+    """C3 input: pre-RoPE keys bf16 N(0,1) x per-channel U(0.5, 4), RoPE (rotate-half
+    convention, theta 500000, no frequency scaling) at positions 131008..131071,
+    flattened to [8 * 64, 128] fp32 rows."""
+    import torch
+    k = (torch.randn(HKV, ENC_TOKENS, D, generator=g) *
+         (torch.rand(D, generator=g) * 3.5 + 0.5)).bfloat16().float()
+    pos = torch.arange(ENC_POS0, ENC_POS0 + ENC_TOKENS, dtype=torch.float64)
+    inv = ROPE_THETA ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+    ang = pos[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).float()
+    sin = torch.cat([ang.sin(), ang.sin()], -1).float()
+    rot = torch.cat([-k[..., D // 2:], k[..., :D // 2]], -1)
+    return (k * cos + rot * sin).reshape(HKV * ENC_TOKENS, D).to(dev)
+
+
+def encode_cpu_baseline(x, cb, seconds: float) -> dict:
+    """The reference's fp32 greedy encode (restated in oracle/ref_path.py) at C3."""
+    import torch
+    from oracle import ref_path
+    xc, cbc = x.cpu(), cb.cpu()
+    ref_path.encode_fp32(xc, cbc)
+    ts = []
+    t_end = time.perf_counter() + seconds
+    while len(ts) < 5 or (time.perf_counter() < t_end and len(ts) < 30):
+        t0 = time.perf_counter()
+        ref_path.encode_fp32(xc, cbc)
+        ts.append(time.perf_counter() - t0)
+    med = sorted(ts)[len(ts) // 2]
+    return {"us": round(med * 1e6, 1), "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 warm-up + {len(ts)} timed calls of the reference fp32 greedy "
+                      "encode (laprune/quantizer.py:346-355, restated), median"}
+
+
 def traffic_from_profile() -> dict | None:
     p = ROOT / "profiles" / "score_g4_traffic.json"
     if not p.exists():
@@ -150,6 +190,9 @@ def main():
         vv = torch.randn(1, HKV, T + CAP, D, dtype=torch.bfloat16, device=dev)
         kv_sets.append((kk, vv))
     cb = (torch.randn(M, K, D, generator=g) * 0.02).to(dev)
+    from laprune_amd import aq_kernels as AK
+    enc_x = c3_keys(g, dev)
+    enc_prep = AK.aq_encode_prepare(cb)
 
     cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=TOPK, select="group",
                           score_dtype=torch.bfloat16)
@@ -183,9 +226,12 @@ def main():
         b = torch.empty_like(a)
         for _ in range(3):
             torch.neg(a, out=b)
+        for _ in range(4):
+            AK.aq_encode_greedy(enc_x, cb, enc_prep)
         torch.cuda.synchronize()
         print(f"counters pass: {2 * N_CODE_SETS} scorer launches of {CODE_BYTES} code bytes, "
-              f"3 fp32 negate launches of {CALIB_BYTES} bytes read + written", flush=True)
+              f"3 fp32 negate launches of {CALIB_BYTES} bytes read + written, "
+              f"4 C3 encode launches", flush=True)
         return
 
     log("warm-up")
@@ -275,6 +321,21 @@ def main():
     score_us = ev0.elapsed_time(ev1) * 1e3 / (reps * n_sets)
     score_gbs = CODE_BYTES / (score_us * 1e-6) / 1e9
 
+    # ---- C3 encode: one flush of 512 post-RoPE key rows (HIP events)
+    log("timing the C3 encode")
+    for _ in range(3):
+        AK.aq_encode_greedy(enc_x, cb, enc_prep)
+    torch.cuda.synchronize()
+    n_enc = max(5, args.steps // 10)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(n_enc):
+        AK.aq_encode_greedy(enc_x, cb, enc_prep)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    enc_us = ev0.elapsed_time(ev1) * 1e3 / n_enc
+
     # correctness guard: the selected index sets are valid and the right size
     sparse_step(0)
     torch.cuda.synchronize()
@@ -312,6 +373,15 @@ def main():
         "dense_hbm_gbs": round(2 * HKV * T * D * 2 / dense_s / 1e9, 1),
         "score_kernel_us": round(score_us, 3),
         "selection_check": ok,
+        "encode": {
+            "workload": "C3: 8 KV heads x 64-token flush = 512 post-RoPE key rows, D=128, "
+                        "32x256 fp32 codebooks N(0,0.02); greedy codes + residual norm",
+            "us": round(enc_us, 1),
+            "rows_per_s": round(HKV * ENC_TOKENS / (enc_us * 1e-6), 1),
+            "mfma_tflops": round(ENC_FLOP / (enc_us * 1e-6) / 1e12, 3),
+            "mfma_peak_tflops_bf16": 2500.0,
+            "search": "bf16 MFMA coarse distances + exact fp32 dot16 recheck",
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(score_gbs, 1),
@@ -324,6 +394,7 @@ def main():
     if not args.no_cpu_baseline:
         log("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["encode"]["cpu_baseline"] = encode_cpu_baseline(enc_x, cb, 4.0)
     print(json.dumps(result), flush=True)
 
 
