@@ -13,19 +13,26 @@
 //
 // Work shape: workgroup = (b, selection row, split) with 256 threads; a row
 // carries HPR query heads (HPR = G when one list serves a KV group, 1 for
-// per-head lists) so K/V rows are read once per group.  Keys are processed in
-// tiles of 64: phase 1 puts four lanes on each key (a quarter of D each) and
-// reduces q.k across them; the online-softmax update runs one wave per head;
-// phase 2 gives each wave 16 keys and each lane D/64 output dims.  V loads
-// of a tile are issued before phase 1 so they overlap the q.k work.  Splits
-// write (m, l, o) partials that a combine kernel merges.
+// per-head lists) so K/V rows are read once per group.  Each wave runs its
+// own online softmax over steps of 16 keys of the split (waves take steps
+// round-robin); q.k and p.V of a step are 16x16x16 MFMAs (layouts below), so
+// the VALU only does the softmax.  Memory is software-pipelined per wave: a
+// step's keep-list positions are read two steps ahead and its K/V rows one
+// step ahead, and nothing in the loop waits on the whole workgroup.  The
+// waves' states merge through LDS at the end; splits are merged by a combine
+// kernel (or, on request, in-kernel by the last-arriving workgroup of a row).
 #include "common.h"
+
+#include <cstdlib>
+#include <cstring>
 
 namespace lap {
 namespace {
 
-constexpr int kTile = 64;
+constexpr int kTile = 64;     // keys per workgroup step (4 waves x 16)
+constexpr int kKeys = 16;     // keys per wave step
 constexpr int kThreads = 256;
+constexpr int kMaxInKernelSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int DT>
@@ -50,26 +57,171 @@ struct AttnArgs {
   int per_split, nsplit;
   uint16_t* out;     // [B][Hq][D]
   float* part;       // [B][Hq][nsplit][D + 2] (m, l, o...)
+  unsigned* ctr;     // [B * H_idx] arrival counters (zero between calls), or null
 };
 
-template <typename IT>
-__device__ __forceinline__ int64_t keep_token(const AttnArgs& a, const IT* idx_row, int j) {
-  if (j < a.n_idx) return (int64_t)idx_row[j];
-  j -= a.n_idx;
-  if (j < a.sink) return j;
-  return (int64_t)a.tail_start + (j - a.sink);
+// Keep-list position j (0 <= j < L) -> cache row, -1 when outside [0, T).
+// Branch-free: with HAS_IDX the index load is always issued (clamped into
+// the list), so every call issues the same number of loads and the
+// compiler's wait counts stay exact through the software pipeline.
+template <bool HAS_IDX, typename IT>
+__device__ __forceinline__ int keep_token(const AttnArgs& a, const IT* idx_row, int j) {
+  const int jt = j - a.n_idx;
+  int64_t t = jt < a.sink ? jt : (int64_t)a.tail_start + (jt - a.sink);
+  if (HAS_IDX) {
+    const int ji = j < a.n_idx ? j : a.n_idx - 1;
+    const int64_t ti = (int64_t)idx_row[ji];
+    t = j < a.n_idx ? ti : t;
+  }
+  return (t < 0 || t >= a.T) ? -1 : (int)t;
 }
 
-template <int DT, typename IT, int HPR, int D>
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16x16x16 MFMA in the data type (fp32 accumulate).
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(i16x4 a, i16x4 b, f32x4 c) {
+  if constexpr (DT == LAP_DTYPE_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// One wave step = 16 keys, computed with 16x16x16 MFMAs.  Operand layouts
+// (lane l, r = l / 16, c = l % 16):
+//   q.k:  A = K (row = key c), B = Q^T (column = head c); the reduction index
+//         4r + e of k-step ks stands for dim r * D/4 + 4 ks + e, so a lane
+//         needs one contiguous quarter row of K.  Output: lane l holds the
+//         scores of keys 4r + e for head c.
+//   p.V:  A = P (row = head c, reduction index = key 4r + e): exactly the
+//         score layout, no data movement.  B = V with column c of chunk ch
+//         standing for dim c * D/16 + ch, so a lane needs D/16 contiguous
+//         values of each of its four keys.  Output: lane l holds o for heads
+//         4r + e and dims c * D/16 + ch.
+template <int D>
+struct KvStep {
+  static constexpr int NK = D / 32;  // uint4 of K per lane (a quarter row)
+  static constexpr int NV = D / 32;  // dwords of V per key per lane (D/16 values)
+  uint4 k[NK];
+  uint32_t v[4][NV];
+  int tv[4];  // cache rows of keys 4r + e (-1: invalid)
+};
+
+template <int D>
+__device__ __forceinline__ void kv_issue(KvStep<D>& st, const uint16_t* __restrict__ kb,
+                                         const uint16_t* __restrict__ vb, int64_t k_st,
+                                         int64_t v_st, int tok, int lane) {
+  const int r = lane >> 4, c = lane & 15;
+  const uint4* kp = reinterpret_cast<const uint4*>(kb + (int64_t)(tok < 0 ? 0 : tok) * k_st +
+                                                   r * (D / 4));
+#pragma unroll
+  for (int i = 0; i < KvStep<D>::NK; ++i) st.k[i] = kp[i];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int tv = __shfl(tok, 4 * r + e, 64);  // lane j < 16 holds key j's row
+    st.tv[e] = tv;
+    const uint16_t* vp = vb + (int64_t)(tv < 0 ? 0 : tv) * v_st + c * (D / 16);
+    if (KvStep<D>::NV == 2) {
+      const uint2 w = *reinterpret_cast<const uint2*>(vp);
+      st.v[e][0] = w.x;
+      st.v[e][1] = w.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < KvStep<D>::NV; i += 4) {
+        const uint4 w = reinterpret_cast<const uint4*>(vp)[i / 4];
+        st.v[e][i] = w.x;
+        st.v[e][i + 1] = w.y;
+        st.v[e][i + 2] = w.z;
+        st.v[e][i + 3] = w.w;
+      }
+    }
+  }
+}
+
+template <int DT, int HPR, int D>
+struct WaveState {
+  i16x4 qf[D / 16];     // Q^T fragments (head = lane % 16; zero past HPR)
+  f32x4 acc[D / 16];    // o, heads 4r + e, dims c * D/16 + ch
+  float m, l;           // running max / sum of head lane % 16 (equal in its 4 lanes)
+};
+
+// One step: scores by MFMA, online-softmax update, p.V by MFMA.
+template <int DT, int HPR, int D>
+__device__ __forceinline__ void attn_step(WaveState<DT, HPR, D>& ws, const KvStep<D>& st,
+                                          float scale_log2, int lane) {
+  const int r = lane >> 4, c = lane & 15;
+  f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    const uint4 w = st.k[ks / 2];
+    const uint2 kk = (ks & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
+    sacc = mfma16<DT>(__builtin_bit_cast(i16x4, kk), ws.qf[ks], sacc);
+  }
+  float sc[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sc[e] = (c < HPR && st.tv[e] >= 0) ? sacc[e] * scale_log2 : -INFINITY;
+    mx = fmaxf(mx, sc[e]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(ws.m, mx);
+  float pe[4], alpha = 1.f, ps = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    pe[e] = m_new == -INFINITY ? 0.f : exp2f(sc[e] - m_new);  // 0 for sc = -inf
+    ps += pe[e];
+  }
+  if (m_new != -INFINITY) alpha = exp2f(ws.m - m_new);  // 0 for the first finite max
+  ps += __shfl_xor(ps, 16, 64);
+  ps += __shfl_xor(ps, 32, 64);
+  ws.l = ws.l * alpha + ps;
+  ws.m = m_new;
+  // Rescale o: lane l holds heads 4r + e; head h's alpha lives in lanes h, h+16, ...
+  float al[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int a0 = __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), e);
+    float a = __builtin_bit_cast(float, a0);
+    if (HPR > 4) {
+      const float a1 =
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 4 + e));
+      a = r == 1 ? a1 : a;
+    }
+    al[e] = a;
+  }
+#pragma unroll
+  for (int ch = 0; ch < D / 16; ++ch)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ws.acc[ch][e] *= al[e];
+  // P operand (row = head c, keys 4r + e), in the data type.
+  i16x4 pa;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pa[e] = (short)st16<DT>(pe[e]);
+#pragma unroll
+  for (int ch = 0; ch < D / 16; ++ch) {
+    uint32_t vx[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t wv = st.v[e][ch / 2];
+      vx[e] = st.tv[e] >= 0 ? ((ch & 1) ? (wv >> 16) : (wv & 0xffffu)) : 0u;
+    }
+    const uint2 vb2 = make_uint2(vx[0] | (vx[1] << 16), vx[2] | (vx[3] << 16));
+    ws.acc[ch] = mfma16<DT>(pa, __builtin_bit_cast(i16x4, vb2), ws.acc[ch]);
+  }
+}
+
+template <int DT, typename IT, int HPR, int D, bool HAS_IDX>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
-  constexpr int DQ = D / 4;     // dims per phase-1 lane
-  constexpr int DPL = D / 64;   // dims per phase-2 lane
-  static_assert(D % 64 == 0 && DQ % 8 == 0, "D must be a multiple of 64");
-  __shared__ __attribute__((aligned(16))) float s_q[HPR][D];
-  __shared__ int64_t s_tok[kTile];
-  __shared__ __attribute__((aligned(16))) float s_p[kTile][HPR];
-  __shared__ float s_alpha[HPR], s_m[HPR], s_l[HPR];
+  static_assert(D % 64 == 0 && HPR <= 8, "D must be a multiple of 64, HPR <= 8");
+  __shared__ float s_m[4][HPR], s_l[4][HPR];
   __shared__ __attribute__((aligned(16))) float s_o[4][HPR][D];
+  __shared__ float s_w[HPR][kMaxInKernelSplits];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = blockIdx.x % a.nsplit;
@@ -86,164 +238,142 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const uint16_t* kb = a.k + (int64_t)b * a.k_sb + (int64_t)hkv * a.k_sh;
   const uint16_t* vb = a.v + (int64_t)b * a.v_sb + (int64_t)hkv * a.v_sh;
 
-  for (int i = tid; i < HPR * D; i += kThreads) {
-    const int g = i / D, d = i - g * D;
-    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + g) * a.q_sh;
-    s_q[g][d] = ld16<DT>(qp[d]) * a.scale_log2;
+  WaveState<DT, HPR, D> ws;
+  {
+    const int r = lane >> 4, c = lane & 15;
+    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (c < HPR ? c : 0)) * a.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const uint16_t* q4 = qp + r * (D / 4) + 4 * ks;  // q may be only 2-byte aligned
+      i16x4 f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) f[e] = c < HPR ? (short)q4[e] : (short)0;
+      ws.qf[ks] = f;
+      ws.acc[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    ws.m = -INFINITY;
+    ws.l = 0.f;
   }
-  if (tid < HPR) {
-    s_m[tid] = -INFINITY;
-    s_l[tid] = 0.f;
+  // This wave's steps: keys [lo + (w + 4i) * 16, +16) for i = 0, 1, ...
+  const int nsteps = (hi - lo + kKeys - 1) / kKeys;
+  const int mine = nsteps > wave ? (nsteps - wave + 3) / 4 : 0;
+  const int jmax = hi > lo ? hi - 1 : 0;
+  auto pos_tok = [&](int i) -> int {
+    const int jpos = lo + (wave + 4 * i) * kKeys + (lane & 15);
+    const int tk = keep_token<HAS_IDX, IT>(a, idx_row, jpos < jmax ? jpos : jmax);
+    return (i < mine && jpos < hi) ? tk : -1;
+  };
+  // Pipeline: keep-list rows two steps ahead, K/V one step ahead, ping-pong
+  // buffers.  The steady-state loop issues unconditionally (exact wait
+  // counts); the last steps run in the tail loop.
+  KvStep<D> bufA, bufB;
+  int tokA = pos_tok(0), tokB = pos_tok(1);
+  kv_issue<D>(bufA, kb, vb, a.k_st, a.v_st, tokA, lane);
+  int i = 0;
+  for (; i + 3 < mine; i += 2) {
+    const int tokC = pos_tok(i + 2);
+    kv_issue<D>(bufB, kb, vb, a.k_st, a.v_st, tokB, lane);
+    attn_step<DT, HPR, D>(ws, bufA, a.scale_log2, lane);
+    const int tokD = pos_tok(i + 3);
+    kv_issue<D>(bufA, kb, vb, a.k_st, a.v_st, tokC, lane);
+    attn_step<DT, HPR, D>(ws, bufB, a.scale_log2, lane);
+    tokA = tokC;
+    tokB = tokD;
   }
-  float o[HPR][DPL];
-#pragma unroll
-  for (int g = 0; g < HPR; ++g)
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) o[g][e] = 0.f;
-
-  for (int t0 = lo; t0 < hi; t0 += kTile) {
-    if (tid < kTile) {
-      const int j = t0 + tid;
-      int64_t tok = -1;
-      if (j < hi) {
-        tok = keep_token<IT>(a, idx_row, j);
-        if (tok < 0 || tok >= a.T) tok = -1;
-      }
-      s_tok[tid] = tok;
+  // Tail: steps i .. mine-1 (at most three); bufA holds step i when i < mine.
+  if (i < mine) {
+    if (i + 1 < mine) kv_issue<D>(bufB, kb, vb, a.k_st, a.v_st, tokB, lane);
+    attn_step<DT, HPR, D>(ws, bufA, a.scale_log2, lane);
+    if (i + 1 < mine) {
+      const int tokC = pos_tok(i + 2);
+      if (i + 2 < mine) kv_issue<D>(bufA, kb, vb, a.k_st, a.v_st, tokC, lane);
+      attn_step<DT, HPR, D>(ws, bufB, a.scale_log2, lane);
+      if (i + 2 < mine) attn_step<DT, HPR, D>(ws, bufA, a.scale_log2, lane);
     }
-    __syncthreads();
-
-    // Issue this wave's phase-2 V loads early.
-    uint32_t vraw[16][(DPL + 1) / 2];
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const int64_t tok = s_tok[wave * 16 + jj];
-      const uint16_t* vp = vb + (tok < 0 ? 0 : tok) * a.v_st + lane * DPL;
-      if (DPL == 1) {
-        vraw[jj][0] = tok < 0 ? 0u : (uint32_t)vp[0];
-      } else {
-#pragma unroll
-        for (int e = 0; e < DPL / 2; ++e)
-          vraw[jj][e] = tok < 0 ? 0u : reinterpret_cast<const uint32_t*>(vp)[e];
-      }
-    }
-
-    // Phase 1: four lanes per key, each over D/4 dims.
-    {
-      const int j = tid >> 2, qd = tid & 3;
-      const int64_t tok = s_tok[j];
-      float part[HPR];
-#pragma unroll
-      for (int g = 0; g < HPR; ++g) part[g] = 0.f;
-      if (tok >= 0) {
-        const uint4* kp = reinterpret_cast<const uint4*>(kb + tok * a.k_st + qd * DQ);
-#pragma unroll
-        for (int c = 0; c < DQ / 8; ++c) {
-          const uint4 w = kp[c];
-          const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float k0 = ld16<DT>((uint16_t)(ww[e] & 0xffffu));
-            const float k1 = ld16<DT>((uint16_t)(ww[e] >> 16));
-            const int d = qd * DQ + c * 8 + 2 * e;
-#pragma unroll
-            for (int g = 0; g < HPR; ++g) {
-              part[g] = __builtin_fmaf(s_q[g][d], k0, part[g]);
-              part[g] = __builtin_fmaf(s_q[g][d + 1], k1, part[g]);
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < HPR; ++g) {
-        part[g] += __shfl_xor(part[g], 1, 64);
-        part[g] += __shfl_xor(part[g], 2, 64);
-      }
-      if (qd == 0) {
-#pragma unroll
-        for (int g = 0; g < HPR; ++g) s_p[j][g] = tok >= 0 ? part[g] : -INFINITY;
-      }
-    }
-    __syncthreads();
-
-    // Online softmax update: one wave per head (lane = key).
-    for (int g = wave; g < HPR; g += 4) {
-      const float x = s_p[lane][g];
-      float tm = x;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) tm = fmaxf(tm, __shfl_xor(tm, d, 64));
-      const float m_old = s_m[g];
-      const float m_new = fmaxf(m_old, tm);
-      float p = 0.f, alpha = 1.f;
-      if (m_new != -INFINITY) {
-        p = (x == -INFINITY) ? 0.f : exp2f(x - m_new);
-        alpha = (m_old == -INFINITY) ? 0.f : exp2f(m_old - m_new);
-      }
-      float ps = p;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) ps += __shfl_xor(ps, d, 64);
-      s_p[lane][g] = p;
-      if (lane == 0) {
-        s_alpha[g] = alpha;
-        s_m[g] = m_new;
-        s_l[g] = s_l[g] * alpha + ps;
-      }
-    }
-    __syncthreads();
-
-    // Phase 2: o = o * alpha + sum_j p_j V_j over this wave's 16 keys.
-#pragma unroll
-    for (int g = 0; g < HPR; ++g) {
-      const float al = s_alpha[g];
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) o[g][e] *= al;
-    }
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const int j = wave * 16 + jj;
-      float vv[DPL];
-      if (DPL == 1) {
-        vv[0] = ld16<DT>((uint16_t)vraw[jj][0]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < DPL / 2; ++e) {
-          vv[2 * e] = ld16<DT>((uint16_t)(vraw[jj][e] & 0xffffu));
-          vv[2 * e + 1] = ld16<DT>((uint16_t)(vraw[jj][e] >> 16));
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < HPR; ++g) {
-        const float p = s_p[j][g];
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) o[g][e] = __builtin_fmaf(p, vv[e], o[g][e]);
-      }
-    }
-    __syncthreads();
   }
 
-  // Cross-wave sum of the partial outputs.
+  // Merge the four waves' states.
+  {
+    const int r = lane >> 4, c = lane & 15;
+    if (lane < HPR) {
+      s_m[wave][lane] = ws.m;
+      s_l[wave][lane] = ws.l;
+    }
 #pragma unroll
-  for (int g = 0; g < HPR; ++g)
+    for (int e = 0; e < 4; ++e) {
+      const int h = 4 * r + e;
+      if (h < HPR)
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) s_o[wave][g][lane * DPL + e] = o[g][e];
+        for (int ch = 0; ch < D / 16; ++ch) s_o[wave][h][c * (D / 16) + ch] = ws.acc[ch][e];
+    }
+  }
   __syncthreads();
   for (int i = tid; i < HPR * D; i += kThreads) {
     const int g = i / D, d = i - g * D;
-    const float sum = s_o[0][g][d] + s_o[1][g][d] + s_o[2][g][d] + s_o[3][g][d];
-    const int h = h0 + g;
-    const int64_t bh = (int64_t)b * a.Hq + h;
+    const float M = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
+    float l = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float wt = (M == -INFINITY || s_m[w][g] == -INFINITY) ? 0.f : exp2f(s_m[w][g] - M);
+      l += s_l[w][g] * wt;
+      o += s_o[w][g][d] * wt;
+    }
+    const int64_t bh = (int64_t)b * a.Hq + h0 + g;
     if (a.nsplit == 1) {
-      const float l = s_l[g];
-      a.out[bh * D + d] = st16<DT>(l > 0.f ? sum / l : 0.f);
+      a.out[bh * D + d] = st16<DT>(l > 0.f ? o / l : 0.f);
     } else {
       float* pp = a.part + (bh * a.nsplit + s) * (D + 2);
       if (d == 0) {
-        pp[0] = s_m[g];
-        pp[1] = s_l[g];
+        pp[0] = M;
+        pp[1] = l;
       }
-      pp[2 + d] = sum;
+      pp[2 + d] = o;
     }
   }
+  if (a.nsplit == 1 || !a.ctr) return;
+
+  // The last workgroup of the row to finish merges the splits.  One thread
+  // publishes (device-scope release after the workgroup barrier) and counts;
+  // a per-row counter keeps the atomics short.  The merging workgroup
+  // acquires before reading the other splits and leaves the counter at zero.
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    s_last = atomicAdd(&a.ctr[br], 1u) == (unsigned)(a.nsplit - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) __threadfence();
+  __syncthreads();
+  for (int i = tid; i < HPR * a.nsplit; i += kThreads) {
+    const int g = i / a.nsplit, sp = i - g * a.nsplit;
+    s_w[g][sp] = a.part[(((int64_t)b * a.Hq + h0 + g) * a.nsplit + sp) * (D + 2)];
+  }
+  __syncthreads();
+  if (tid < HPR) {
+    float M = -INFINITY;
+    for (int sp = 0; sp < a.nsplit; ++sp) M = fmaxf(M, s_w[tid][sp]);
+    const float* pp = a.part + ((int64_t)b * a.Hq + h0 + tid) * a.nsplit * (D + 2);
+    float l = 0.f;
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+      const float ms = s_w[tid][sp];
+      const float wt = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
+      s_w[tid][sp] = wt;
+      l += pp[(int64_t)sp * (D + 2) + 1] * wt;
+    }
+    s_l[0][tid] = l;
+  }
+  __syncthreads();
+  for (int i = tid; i < HPR * D; i += kThreads) {
+    const int g = i / D, d = i - g * D;
+    const float* pp = a.part + ((int64_t)b * a.Hq + h0 + g) * a.nsplit * (D + 2) + 2 + d;
+    float o = 0.f;
+#pragma unroll 4
+    for (int sp = 0; sp < a.nsplit; ++sp) o = __builtin_fmaf(pp[(int64_t)sp * (D + 2)], s_w[g][sp], o);
+    const float l = s_l[0][g];
+    a.out[((int64_t)b * a.Hq + h0 + g) * D + d] = st16<DT>(l > 0.f ? o / l : 0.f);
+  }
+  if (tid == 0) a.ctr[br] = 0u;  // ready for the next call
 }
 
 // Merge split partials: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
@@ -311,9 +441,18 @@ int choose_nsplit(int rows, int L) {
 template <int DT, typename IT, int HPR>
 hipError_t launch_attn_hpr(const AttnArgs& a, int D, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.H_idx * a.nsplit));
-  if (D == 64) hipLaunchKernelGGL((attn_decode_kernel<DT, IT, HPR, 64>), grid, dim3(kThreads), 0, st, a);
-  else if (D == 128) hipLaunchKernelGGL((attn_decode_kernel<DT, IT, HPR, 128>), grid, dim3(kThreads), 0, st, a);
-  else hipLaunchKernelGGL((attn_decode_kernel<DT, IT, HPR, 256>), grid, dim3(kThreads), 0, st, a);
+  const bool has_idx = a.idx && a.n_idx > 0;
+#define LAP_ATTN(D_)                                                                        \
+  if (has_idx)                                                                              \
+    hipLaunchKernelGGL((attn_decode_kernel<DT, IT, HPR, D_, true>), grid, dim3(kThreads), 0, \
+                       st, a);                                                              \
+  else                                                                                      \
+    hipLaunchKernelGGL((attn_decode_kernel<DT, IT, HPR, D_, false>), grid, dim3(kThreads), 0, \
+                       st, a)
+  if (D == 64) { LAP_ATTN(64); }
+  else if (D == 128) { LAP_ATTN(128); }
+  else { LAP_ATTN(256); }
+#undef LAP_ATTN
   return hipGetLastError();
 }
 
@@ -327,6 +466,16 @@ hipError_t launch_attn_dt(const AttnArgs& a, int hpr, int D, hipStream_t st) {
   }
 }
 
+// LAPRUNE_ATTN_MERGE=kernel merges splits in the attention kernel (last
+// workgroup of a row); default: a separate combine kernel.
+bool attn_merge_in_kernel() {
+  static const bool v = [] {
+    const char* e = getenv("LAPRUNE_ATTN_MERGE");
+    return e && strcmp(e, "kernel") == 0;
+  }();
+  return v;
+}
+
 int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_t ws_bytes,
              hipStream_t st) {
   const int L = a.n_idx + a.sink + a.tail_count;
@@ -338,15 +487,17 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
   a.per_split = (a.per_split + kTile - 1) / kTile * kTile;
   if (a.per_split < kTile) a.per_split = kTile;
   a.nsplit = L > 0 ? (L + a.per_split - 1) / a.per_split : 1;
-  // Workspace: split partials [B][Hq][nsplit][D + 2], merged by a combine
-  // kernel.  (An in-kernel merge by the last-arriving workgroup needs a
-  // device-scope release per workgroup, which on the multi-XCD part writes
-  // back the XCD's L2 and costs far more than the second launch.)
+  // Workspace: [B * H_idx arrival counters, 256-byte block][split partials
+  // [B][Hq][nsplit][D + 2]].  Up to 64 splits merge in-kernel (the counters
+  // must be zero before a call and are left zero); more use a combine kernel.
+  const size_t ctr_bytes = align_up((size_t)a.B * a.H_idx * sizeof(unsigned), 256);
+  const bool merge_in_kernel = a.nsplit <= kMaxInKernelSplits && attn_merge_in_kernel();
   if (a.nsplit > 1) {
-    const size_t need = (size_t)a.B * a.Hq * a.nsplit * (D + 2) * sizeof(float);
+    const size_t need = ctr_bytes + (size_t)a.B * a.Hq * a.nsplit * (D + 2) * sizeof(float);
     LAP_CHECK_CODE(workspace && ws_bytes >= need, LAP_ERR_WORKSPACE,
                    "attention decode: workspace of %zu bytes needed", need);
-    a.part = static_cast<float*>(workspace);
+    a.ctr = merge_in_kernel ? static_cast<unsigned*>(workspace) : nullptr;
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ctr_bytes);
   }
   hipError_t e;
   const bool i64 = idx_dtype == LAP_DTYPE_I64;
@@ -357,7 +508,7 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
     e = i64 ? launch_attn_dt<LAP_DTYPE_BF16, int64_t>(a, hpr, D, st)
             : launch_attn_dt<LAP_DTYPE_BF16, int32_t>(a, hpr, D, st);
   LAP_HIP(e, "attn_decode_kernel launch");
-  if (a.nsplit > 1) {
+  if (a.nsplit > 1 && !merge_in_kernel) {
     if (dtype == LAP_DTYPE_F16)
       hipLaunchKernelGGL(attn_combine_kernel<LAP_DTYPE_F16>, dim3(a.B * a.Hq), dim3(256), 0, st,
                          a.part, a.nsplit, D, a.out);
@@ -400,7 +551,10 @@ extern "C" int lap_attn_decode_workspace_size(int B, int Hq, int D, int max_keys
   int ns = (max_keys + kTile - 1) / kTile;
   if (ns > 1024) ns = 1024;
   if (ns < 1) ns = 1;
-  *bytes = (size_t)B * Hq * ns * (D + 2) * sizeof(float);  // split partials
+  // arrival counters (one per selection row; at most one per query head)
+  // followed by the split partials
+  *bytes = align_up((size_t)B * Hq * sizeof(unsigned), 256) +
+           (size_t)B * Hq * ns * (D + 2) * sizeof(float);
   return LAP_OK;
 }
 
