@@ -275,6 +275,24 @@ int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, int D,
                       uint8_t* codes_out, int64_t codes_row_stride,
                       float* resid_norm, lap_stream_t stream);
 
+/* Replaces: the encode of the not-yet-encoded key tail in _prepare_aq_cache,
+ *   laprune/llm/modifiers/aq_evaluation.py:367-405 (codes[:, :, encoded_len:
+ *   seq_len] = encode_keys_batch(keys[:, :, encoded_len:seq_len]), through
+ *   laprune/llm/aq_kv.py:390-428), and its prefill form (:430-447).
+ * Same contract as lap_encode_greedy, with the rows taken straight from a
+ * strided key cache and the codes written straight into a strided code cache:
+ * for every (b, h) and t in [t0, t1), keys[b, h, t, :] -> codes[b, h, t, :].
+ *   keys       f32/f16/bf16 [B][Hkv][T][D], strides (k_sb, k_sh, k_st, 1)
+ *   codes      u8 [B][Hkv][Tcap][M], strides (c_sb, c_sh, c_st, 1)
+ *   resid_norm fp32 [B*Hkv*(t1-t0)] in (b, h, t) order, may be NULL */
+int lap_encode_keys(const void* keys, int key_dtype,
+                    int64_t k_sb, int64_t k_sh, int64_t k_st,
+                    int B, int Hkv, int t0, int t1, int D,
+                    const float* codebooks, int M, int K,
+                    const void* prep, size_t prep_bytes,
+                    uint8_t* codes, int64_t c_sb, int64_t c_sh, int64_t c_st,
+                    float* resid_norm, lap_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

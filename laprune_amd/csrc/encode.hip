@@ -53,6 +53,29 @@ Prep carve_prep(void* base, int M, int K, int D) {
   return p;
 }
 
+// Row addressing of an encode call.  Row i of the N rows is token
+// t0 + i % L of segment s = i / L, and segment s is (b, h) = (s / Hs, s % Hs):
+// a block of L consecutive tokens of every (batch, KV head) pair of a
+// strided [B][H][T][D] key cache, and the same position in a strided
+// [B][H][Tcap][M] code cache.  A plain [N][D] input is L = N, Hs = 1.
+struct RowMap {
+  const void* x;
+  int x_dtype;  // f32 / f16 / bf16 (widened exactly to fp32)
+  int64_t x_sb, x_sh, x_st;
+  uint8_t* codes;
+  int64_t c_sb, c_sh, c_st;
+  int L, Hs, t0;
+  __device__ __forceinline__ int64_t off(int i, int64_t sb, int64_t sh, int64_t st) const {
+    const int sg = i / L, t = t0 + (i - sg * L);
+    const int b = sg / Hs, h = sg - b * Hs;
+    return (int64_t)b * sb + (int64_t)h * sh + (int64_t)t * st;
+  }
+  __device__ __forceinline__ float xval(int i, int d) const {
+    return load_as_f32(x, off(i, x_sb, x_sh, x_st) + d, x_dtype);
+  }
+  __device__ __forceinline__ uint8_t* crow(int i) const { return codes + off(i, c_sb, c_sh, c_st); }
+};
+
 // Fold 16 chain sums in the contract order.
 __device__ __forceinline__ float fold16(float s[16]) {
 #pragma unroll
@@ -115,16 +138,16 @@ __device__ __forceinline__ float wave_self_dot16(const float* r, int D, int lane
 
 template <int D>
 __global__ __launch_bounds__(256) void encode_greedy_kernel(
-    const float* __restrict__ x, int64_t x_rs, int N, const float* __restrict__ cb, int M,
+    RowMap rm, int N, const float* __restrict__ cb, int M,
     int K, const float* __restrict__ ct, const float* __restrict__ cn,
-    uint8_t* __restrict__ codes, int64_t c_rs, float* __restrict__ rnorm) {
+    float* __restrict__ rnorm) {
   constexpr int L = D / 16;
   __shared__ __attribute__((aligned(16))) float s_r[4][D];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + wave;
   const bool live = row < N;
   float* r = s_r[wave];
-  for (int d = lane; d < D; d += 64) r[d] = live ? x[(int64_t)row * x_rs + d] : 0.f;
+  for (int d = lane; d < D; d += 64) r[d] = live ? rm.xval(row, d) : 0.f;
   __syncthreads();
 
   const int k0 = 4 * lane;
@@ -176,7 +199,7 @@ __global__ __launch_bounds__(256) void encode_greedy_kernel(
     // No finite winner (all distances NaN): code 0, as the oracle's strict-<
     // scan from +inf leaves it.
     if (bk >= K) bk = 0;
-    if (live && lane == 0) codes[(int64_t)row * c_rs + m] = (uint8_t)bk;
+    if (live && lane == 0) rm.crow(row)[m] = (uint8_t)bk;
     const float* crow = cb + ((int64_t)m * K + bk) * D;
     for (int d = lane; d < D; d += 64) r[d] = r[d] - crow[d];
     __syncthreads();
@@ -346,8 +369,8 @@ template <int D>
 __device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st,
                                           const float* __restrict__ cb,
                                           const float* __restrict__ cn, int m, int K, int NT,
-                                          int row0, int N, uint8_t* __restrict__ codes,
-                                          int64_t c_rs, int wave, int lane, int tid) {
+                                          int row0, int N, const RowMap& rm, int wave,
+                                          int lane, int tid) {
   using C = EncCfg<D>;
   // A fragments: row l%16, d = ks*16 + 4*(l/16) + e, from the bf16 copy.
   bf16x4_t a[C::KS];
@@ -503,7 +526,7 @@ __device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st
     a2 = row_fold16(a2);
     if (j == 0) {
       s.rn[row] = a2;
-      if (row0 + row < N) codes[(int64_t)(row0 + row) * c_rs + m] = (uint8_t)code;
+      if (row0 + row < N) rm.crow(row0 + row)[m] = (uint8_t)code;
     }
   }
   lds_barrier();
@@ -511,10 +534,9 @@ __device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st
 
 template <int D>
 __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
-    const float* __restrict__ x, int64_t x_rs, int N, const float* __restrict__ cb, int M,
+    RowMap rm, int N, const float* __restrict__ cb, int M,
     int K, const uint2* __restrict__ frag, const float* __restrict__ cn,
-    const float* __restrict__ scn, uint8_t* __restrict__ codes, int64_t c_rs,
-    float* __restrict__ rnorm) {
+    const float* __restrict__ scn, float* __restrict__ rnorm) {
   using C = EncCfg<D>;
   __shared__ __attribute__((aligned(16))) EncShared<D> s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -522,7 +544,7 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
   const int NT = K / 16;
   for (int i = tid; i < 16 * D; i += C::THREADS) {
     const int r = i / D, d = i - r * D;
-    const float v = row0 + r < N ? x[(int64_t)(row0 + r) * x_rs + d] : 0.f;
+    const float v = row0 + r < N ? rm.xval(row0 + r, d) : 0.f;
     s.r[r][d] = v;
     s.rb[r][d] = __builtin_bit_cast(uint16_t, (__bf16)v);
   }
@@ -549,16 +571,16 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
   for (int m = 0; m < M; m += 2) {
     enc_load_stage<D>(st1, frag, cn, scn, min(m + 1, M - 1), NT, K, wave, lane);
     pfb = enc_prefetch_l2<D>(cb, min(m + 1, M - 1), K, wave, lane);
-    enc_stage<D>(s, st0, cb, cn, m, K, NT, row0, N, codes, c_rs, wave, lane, tid);
+    enc_stage<D>(s, st0, cb, cn, m, K, NT, row0, N, rm, wave, lane, tid);
     sink ^= pfa;
     if (m + 1 >= M) break;
     enc_load_stage<D>(st0, frag, cn, scn, min(m + 2, M - 1), NT, K, wave, lane);
     pfa = enc_prefetch_l2<D>(cb, min(m + 2, M - 1), K, wave, lane);
-    enc_stage<D>(s, st1, cb, cn, m + 1, K, NT, row0, N, codes, c_rs, wave, lane, tid);
+    enc_stage<D>(s, st1, cb, cn, m + 1, K, NT, row0, N, rm, wave, lane, tid);
     sink ^= pfb;
   }
   sink ^= pfa ^ pfb;
-  if (sink == 0x9e3779b9u && N < 0) codes[0] = 0;  // never true: keeps the prefetch loads
+  if (sink == 0x9e3779b9u && N < 0) rm.codes[0] = 0;  // never true: keeps the prefetch loads
   if (tid < 16 && rnorm && row0 + tid < N) rnorm[row0 + tid] = sqrtf(s.rn[tid]);
 }
 
@@ -610,32 +632,28 @@ extern "C" int lap_encode_prepare(const float* codebooks, int M, int K, int D, v
   return LAP_OK;
 }
 
-extern "C" int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, int D,
-                                 const float* codebooks, int M, int K, const void* prep,
-                                 size_t prep_bytes, uint8_t* codes_out, int64_t codes_row_stride,
-                                 float* resid_norm, lap_stream_t stream) {
-  clear_error();
-  LAP_CHECK(x && codebooks && prep && codes_out, "lap_encode_greedy: null pointer");
-  LAP_CHECK(N >= 0 && M > 0 && K > 0 && D > 0, "lap_encode_greedy: bad sizes");
-  LAP_CHECK(K <= 256, "lap_encode_greedy: K=%d exceeds 256 (uint8 codes)", K);
-  LAP_CHECK_CODE(K % 4 == 0, LAP_ERR_UNSUPPORTED, "lap_encode_greedy: K must be a multiple of 4");
+// Shared checks and launch of both encode entry points.
+static int run_encode(const RowMap& rm, int N, int D, const float* codebooks, int M, int K,
+                      const void* prep, size_t prep_bytes, float* resid_norm,
+                      lap_stream_t stream, const char* who) {
+  LAP_CHECK(codebooks && prep, "%s: null pointer", who);
+  LAP_CHECK(N >= 0 && M > 0 && K > 0 && D > 0, "%s: bad sizes", who);
+  LAP_CHECK(K <= 256, "%s: K=%d exceeds 256 (uint8 codes)", who, K);
+  LAP_CHECK_CODE(K % 4 == 0, LAP_ERR_UNSUPPORTED, "%s: K must be a multiple of 4", who);
   LAP_CHECK_CODE(D == 64 || D == 128 || D == 256, LAP_ERR_UNSUPPORTED,
-                 "lap_encode_greedy: D=%d unsupported (64/128/256)", D);
-  LAP_CHECK(x_row_stride >= D && codes_row_stride >= M, "lap_encode_greedy: bad row strides");
+                 "%s: D=%d unsupported (64/128/256)", who, D);
   Prep p = carve_prep(const_cast<void*>(prep), M, K, D);
-  LAP_CHECK_CODE(prep_bytes >= p.bytes, LAP_ERR_WORKSPACE,
-                 "lap_encode_greedy: prep buffer of %zu bytes needed", p.bytes);
-  LAP_CHECK((reinterpret_cast<uintptr_t>(p.ct) & 15) == 0, "lap_encode_greedy: prep misaligned");
+  LAP_CHECK_CODE(prep_bytes >= p.bytes, LAP_ERR_WORKSPACE, "%s: prep buffer of %zu bytes needed",
+                 who, p.bytes);
+  LAP_CHECK((reinterpret_cast<uintptr_t>(p.ct) & 15) == 0, "%s: prep misaligned", who);
   if (N == 0) return LAP_OK;
   hipStream_t st = as_stream(stream);
   if (K % 16 == 0 && encode_impl_mfma()) {
     dim3 g16((N + 15) / 16);
     const uint2* fr = reinterpret_cast<const uint2*>(p.frag);
 #define LAP_ENCM(D_)                                                                         \
-  hipLaunchKernelGGL(encode_mfma_kernel<D_>, g16, dim3(EncCfg<D_>::THREADS), 0, st, x,       \
-                     x_row_stride, N, codebooks, M, K, fr, p.cn, p.scn, codes_out,          \
-                     codes_row_stride,                                                         \
-                     resid_norm)
+  hipLaunchKernelGGL(encode_mfma_kernel<D_>, g16, dim3(EncCfg<D_>::THREADS), 0, st, rm, N,   \
+                     codebooks, M, K, fr, p.cn, p.scn, resid_norm)
     if (D == 64) LAP_ENCM(64);
     else if (D == 128) LAP_ENCM(128);
     else LAP_ENCM(256);
@@ -645,12 +663,47 @@ extern "C" int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, in
   }
   dim3 grid((N + 3) / 4);
 #define LAP_ENC(D_)                                                                          \
-  hipLaunchKernelGGL(encode_greedy_kernel<D_>, grid, dim3(256), 0, st, x, x_row_stride, N,   \
-                     codebooks, M, K, p.ct, p.cn, codes_out, codes_row_stride, resid_norm)
+  hipLaunchKernelGGL(encode_greedy_kernel<D_>, grid, dim3(256), 0, st, rm, N, codebooks, M,  \
+                     K, p.ct, p.cn, resid_norm)
   if (D == 64) LAP_ENC(64);
   else if (D == 128) LAP_ENC(128);
   else LAP_ENC(256);
 #undef LAP_ENC
   LAP_LAUNCH_CHECK("encode_greedy_kernel");
   return LAP_OK;
+}
+
+extern "C" int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, int D,
+                                 const float* codebooks, int M, int K, const void* prep,
+                                 size_t prep_bytes, uint8_t* codes_out, int64_t codes_row_stride,
+                                 float* resid_norm, lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(x && codes_out, "lap_encode_greedy: null pointer");
+  LAP_CHECK(N >= 0 && D > 0 && M > 0, "lap_encode_greedy: bad sizes");
+  LAP_CHECK(x_row_stride >= D && codes_row_stride >= M, "lap_encode_greedy: bad row strides");
+  const RowMap rm{x, LAP_DTYPE_F32, 0, 0, x_row_stride, codes_out, 0, 0, codes_row_stride,
+                  N > 0 ? N : 1, 1, 0};
+  return run_encode(rm, N, D, codebooks, M, K, prep, prep_bytes, resid_norm, stream,
+                    "lap_encode_greedy");
+}
+
+extern "C" int lap_encode_keys(const void* keys, int key_dtype, int64_t k_sb, int64_t k_sh,
+                               int64_t k_st, int B, int Hkv, int t0, int t1, int D,
+                               const float* codebooks, int M, int K, const void* prep,
+                               size_t prep_bytes, uint8_t* codes, int64_t c_sb, int64_t c_sh,
+                               int64_t c_st, float* resid_norm, lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(keys && codes, "lap_encode_keys: null pointer");
+  LAP_CHECK(key_dtype == LAP_DTYPE_F32 || key_dtype == LAP_DTYPE_F16 ||
+                key_dtype == LAP_DTYPE_BF16,
+            "lap_encode_keys: keys must be f32, f16 or bf16");
+  LAP_CHECK(B > 0 && Hkv > 0 && D > 0 && M > 0, "lap_encode_keys: bad sizes");
+  LAP_CHECK(0 <= t0 && t0 <= t1, "lap_encode_keys: bad token range [%d, %d)", t0, t1);
+  LAP_CHECK(k_st >= D && c_st >= M, "lap_encode_keys: token strides smaller than D / M");
+  const int64_t n = (int64_t)B * Hkv * (t1 - t0);
+  LAP_CHECK(n <= (int64_t)1 << 30, "lap_encode_keys: too many rows");
+  const RowMap rm{keys, key_dtype, k_sb, k_sh, k_st, codes, c_sb, c_sh, c_st,
+                  t1 > t0 ? t1 - t0 : 1, Hkv, t0};
+  return run_encode(rm, (int)n, D, codebooks, M, K, prep, prep_bytes, resid_norm, stream,
+                    "lap_encode_keys");
 }

@@ -170,9 +170,11 @@ class SparseDecoder:
         N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
                N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
                N.ptr(self.lut), st)
-        k = p["k"]
+        k = p["k"] if t_codes > 0 else 0
         self.last_k = k
-        if self.cfg.select == "group":
+        if k == 0:
+            H_idx = Hkv if self.cfg.select == "group" else Hq  # sink + local only
+        elif self.cfg.select == "group":
             N.call("lap_retrieve_topk", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
                    codes.stride(1), codes.stride(2), B, Hkv, t_codes, p["cand_start"],
                    p["cand_end"], k, self.key_mode, None, N.ptr(self.idx), N.I32,
@@ -198,6 +200,13 @@ class SparseDecoder:
                N.ptr(self.idx), N.I32, H_idx, k, p["sink"], p["tail_start"], p["tail_count"],
                scale, N.ptr(self.out), N.ptr(self.ws_attn), self.ws_attn.numel(), st)
         return self.out.unsqueeze(2)
+
+    @torch.no_grad()
+    def step_cached(self, q: torch.Tensor, cache) -> torch.Tensor:
+        """One decode step over a ``DecodeKVCache``: candidates are the encoded
+        tokens (``encoded_len``), attention covers all ``length`` tokens."""
+        return self.step(q, cache.codes, cache.k, cache.v, t_codes=cache.encoded_len,
+                         t_total=cache.length)
 
     def selected(self) -> torch.Tensor:
         """Indices chosen by the last step: [B, rows, k] int32 (ascending)."""

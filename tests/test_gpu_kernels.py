@@ -367,3 +367,88 @@ def test_fused_linear_encode_dropin(dev, K, orc):
     torch.cuda.synchronize()
     want, _ = orc.encode(x.half().float().numpy(), cbh.float().numpy())
     assert codes.dtype == torch.uint8 and np.array_equal(codes.cpu().numpy(), want)
+
+
+# ------------------------------------------------- decode caches (A2/A6 callers)
+
+def test_encode_keys_strided_matches_flat(dev, K, orc):
+    """lap_encode_keys on a token range of a strided [B][H][Tcap][D] bf16 cache
+    writes the same codes and residual norms as the flat encode of those rows."""
+    from laprune_amd import _native as Nn
+    g = _gen(150)
+    B, H, Tcap, D, M, Kc = 2, 3, 120, 128, 32, 256
+    t0, t1 = 37, 81
+    keys = (torch.randn(B, H, Tcap, D, generator=g) * 2).bfloat16()
+    cb = torch.randn(M, Kc, D, generator=g) * 0.02
+    kd, cbd = keys.to(dev), cb.to(dev)
+    prep = K.aq_encode_prepare(cbd)
+    codes = torch.zeros(B, H, Tcap + 8, M, dtype=torch.uint8, device=dev)
+    rn = torch.empty(B * H * (t1 - t0), dtype=torch.float32, device=dev)
+    Nn.call("lap_encode_keys", Nn.ptr(kd), Nn.BF16, kd.stride(0), kd.stride(1), kd.stride(2),
+            B, H, t0, t1, D, Nn.ptr(cbd), M, Kc, Nn.ptr(prep), prep.numel(), Nn.ptr(codes),
+            codes.stride(0), codes.stride(1), codes.stride(2), Nn.ptr(rn), Nn.stream_of(kd))
+    torch.cuda.synchronize()
+    flat = keys[:, :, t0:t1].float().reshape(-1, D)
+    want_c, want_r = orc.encode(flat.numpy(), cb.numpy())
+    got = codes[:, :, t0:t1].reshape(-1, M).cpu().numpy()
+    assert np.array_equal(got, want_c)
+    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+    # untouched outside the range
+    assert int(codes[:, :, :t0].abs().sum()) == 0 and int(codes[:, :, t1:].abs().sum()) == 0
+
+
+def test_decode_cache_growth_flushes_and_codes(dev, K, orc):
+    """Prefill, then single-token appends through capacity growth: views hold
+    what was appended, encodes follow the 64-token rule, codes are exact."""
+    from laprune_amd.cache import DecodeKVCache
+    g = _gen(160)
+    B, H, D, M, Kc = 1, 2, 128, 32, 256
+    cb = torch.randn(M, Kc, D, generator=g) * 0.02
+    cache = DecodeKVCache(cb.to(dev), B, H, D, capacity=64, group_size=64)
+    k_all = (torch.randn(B, H, 300 + 140, D, generator=g) * 1.5).bfloat16()
+    v_all = torch.randn(B, H, 300 + 140, D, generator=g).bfloat16()
+    cache.append(k_all[:, :, :300].to(dev), v_all[:, :, :300].to(dev), prefill=True)
+    assert cache.length == 300 and cache.encoded_len == 300 and cache.capacity >= 300
+    enc_points = []
+    for t in range(300, 440):
+        cache.append(k_all[:, :, t:t + 1].to(dev), v_all[:, :, t:t + 1].to(dev))
+        if cache.encoded_len == cache.length:
+            enc_points.append(cache.length)
+    torch.cuda.synchronize()
+    assert enc_points == [364, 428]
+    assert cache.length == 440 and cache.encoded_len == 428
+    assert torch.equal(cache.keys().cpu(), k_all) and torch.equal(cache.values().cpu(), v_all)
+    want, _ = orc.encode(k_all[:, :, :428].float().reshape(-1, D).numpy(), cb.numpy())
+    got = cache.encoded_codes().reshape(-1, M).cpu().numpy()
+    assert np.array_equal(got, want)
+
+
+def test_decode_step_over_cache(dev, K, orc):
+    """step_cached scores only encoded keys; the unencoded tail is attended
+    through the local window; output matches the float64 keep-list attention."""
+    from laprune_amd.cache import DecodeKVCache
+    from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
+    g = _gen(170)
+    B, Hq, Hkv, D, M, Kc = 1, 32, 8, 128, 32, 256
+    T0, steps = 1000, 30
+    cb = torch.randn(M, Kc, D, generator=g) * 0.02
+    cache = DecodeKVCache(cb.to(dev), B, Hkv, D, capacity=T0 + steps, group_size=64)
+    kk = torch.randn(B, Hkv, T0 + steps, D, generator=g).bfloat16()
+    vv = torch.randn(B, Hkv, T0 + steps, D, generator=g).bfloat16()
+    cache.append(kk[:, :, :T0].to(dev), vv[:, :, :T0].to(dev), prefill=True)
+    cfg = RetrievalConfig(topk=64, select="group")
+    dec = SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T0 + steps, cfg)
+    for t in range(T0, T0 + steps):
+        cache.append(kk[:, :, t:t + 1].to(dev), vv[:, :, t:t + 1].to(dev))
+        q = torch.randn(B, Hq, 1, D, generator=g).bfloat16()
+        out = dec.step_cached(q.to(dev), cache)
+        torch.cuda.synchronize()
+        sel = dec.selected().cpu().numpy()
+        assert sel.max() < cache.encoded_len and sel.shape[-1] == 64
+        p = dec.plan(cache.encoded_len, cache.length)
+        assert p["cand_end"] <= cache.encoded_len
+        keep = lambda b, h: np.concatenate([sel[b, h // 4], np.arange(p["sink"]),
+                                            np.arange(p["tail_start"], p["tail_start"] + p["tail_count"])])
+        want = orc.attn_decode_f64(q[:, :, 0].double().numpy(), kk[:, :, :t + 1].double().numpy(),
+                                   vv[:, :, :t + 1].double().numpy(), keep)
+        assert _rel(out[:, :, 0].double().cpu().numpy(), want) < 1e-2

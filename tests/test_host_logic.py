@@ -47,3 +47,42 @@ def test_decoder_requires_native_or_gpu():
     cb = torch.zeros(32, 256, 128)
     with pytest.raises(RuntimeError):
         R.SparseDecoder(cb, 1, 32, 8, 128, 1024)
+
+
+# ------------------------------------------------- decode caches (host policy)
+from laprune_amd import cache as KC
+
+
+def test_flush_range_policy():
+    """Encode when >= group_size keys are pending in decode; always in prefill
+    (aq_evaluation.py:369-382, :430-447)."""
+    assert KC.flush_range(100, 0, 64, prefill=True) == (0, 100)
+    assert KC.flush_range(100, 64, 64, prefill=False) is None      # 36 pending
+    assert KC.flush_range(128, 64, 64, prefill=False) == (64, 128)  # 64 pending
+    assert KC.flush_range(64, 64, 64, prefill=False) is None        # nothing pending
+    assert KC.flush_range(65, 64, 1, prefill=False) == (64, 65)     # group 1: every token
+    assert KC.flush_range(70, 64, 64, prefill=True) == (64, 70)
+
+
+def test_flush_sequence_matches_reference_rule():
+    """Prefill 300 keys, then decode one at a time: encodes happen exactly when
+    the pending tail reaches 64, and the tail never exceeds 63 keys after a step."""
+    length, enc = 300, 0
+    rng = KC.flush_range(length, enc, 64, prefill=True)
+    enc = rng[1]
+    flushes = []
+    for _ in range(200):
+        length += 1
+        rng = KC.flush_range(length, enc, 64, prefill=False)
+        if rng is not None:
+            assert rng == (enc, length) and length - enc == 64
+            flushes.append(length)
+            enc = length
+        assert 0 <= length - enc <= 63
+    assert flushes == [364, 428, 492]
+
+
+def test_grown_capacity():
+    assert KC.grown_capacity(16, 17) == 32
+    assert KC.grown_capacity(16, 100) == 100
+    assert KC.grown_capacity(1024, 1025) == 2048
