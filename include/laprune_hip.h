@@ -54,6 +54,26 @@ typedef void* lap_stream_t;
 #define LAP_KEY_F16   0   /* rank the fp16 score itself                     */
 #define LAP_KEY_BF16  1   /* rank bf16(fp16 score): the model-dtype cast    */
 
+/* ---- per-sequence plan of one decode step (ragged batches) ---------------
+ * The reference decodes a batch with one shared length
+ * (laprune/llm/modifiers/aq_evaluation.py:150-155: seq_len, total_seq_len).
+ * The *_ragged entry points take a device array plans[B] instead, one per
+ * sequence b; each field has the meaning of the scalar argument it replaces
+ * in the uniform entry point (the arithmetic of aq_evaluation.py:185-218):
+ *   t_codes     encoded tokens: columns [0, t_codes) are scored
+ *   t_total     cached tokens: keep-set rows must lie in [0, t_total)
+ *   cand_start, cand_end   candidate window (within [0, t_codes))
+ *   k           tokens to select (min'd with the window size and k_cols)
+ *   sink, tail_start, tail_count   keep set [0, sink) ++ [tail_start, +tail_count)
+ * Plans live in device memory so that a captured graph can be replayed after
+ * the host rewrites them. */
+typedef struct lap_row_plan {
+  int32_t t_codes, t_total;
+  int32_t cand_start, cand_end;
+  int32_t k;
+  int32_t sink, tail_start, tail_count;
+} lap_row_plan;
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* lap_last_error(void);
 /* ABI version: bumped when any signature below changes. */
@@ -179,6 +199,30 @@ int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
                       void* workspace, size_t workspace_bytes,
                       lap_stream_t stream);
 
+/* Ragged forms of lap_retrieve_topk and lap_topk_select (no counterpart in
+ * the reference, which has one length per batch; they replace the same
+ * torch.topk call, aq_evaluation.py:198-201, once per sequence).
+ * Row r belongs to sequence r / rows_per_plan (lap_retrieve_topk_ragged:
+ * rows_per_plan = Hkv).  T bounds the columns scored and read: every plan is
+ * clamped to [0, T).  Row r writes out[r][0..k_r) as the uniform call would
+ * for its own window and budget, k_r = min(plan.k, window size, k_cols), and
+ * sets out[r][k_r..k_cols) to -1.  Scores past a row's t_codes are not
+ * written.  Workspaces: lap_retrieve_workspace_size(B*Hkv, T) and
+ * lap_topk_workspace_size(R, T). */
+int lap_retrieve_topk_ragged(const void* lut_gmkg, const uint8_t* codes,
+                             int64_t codes_stride_b, int64_t codes_stride_h,
+                             int64_t codes_stride_t, int B, int Hkv, int T,
+                             const lap_row_plan* plans, int k_cols, int key_mode,
+                             void* scores_out, void* out_idx, int out_dtype,
+                             void* workspace, size_t workspace_bytes,
+                             lap_stream_t stream);
+int lap_topk_select_ragged(const void* scores, int64_t score_row_stride,
+                           int R, int group, int rows_per_plan, int T,
+                           const lap_row_plan* plans, int k_cols, int key_mode,
+                           void* out_idx, int out_dtype,
+                           void* workspace, size_t workspace_bytes,
+                           lap_stream_t stream);
+
 /* ======================================================================= *
  * A4  Native-GQA K/V gather                                                *
  * Replaces: gqa_gather_kv and gqa_gather_kv_with_tail,
@@ -246,6 +290,28 @@ int lap_dense_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                           float scale, void* out,
                           void* workspace, size_t workspace_bytes,
                           lap_stream_t stream);
+
+/* Ragged form of lap_sparse_attn_decode (no counterpart in the reference,
+ * which has one length per batch; it replaces the same gather + SDPA,
+ * aq_evaluation.py:243-251, once per sequence).  Sequence b attends over
+ *   indices[b, row(h), 0..k_cols) ++ [0, plans[b].sink)
+ *   ++ [plans[b].tail_start, + plans[b].tail_count)
+ * skipping index entries < 0 (the padding of the ragged top-k) and rows
+ * outside [0, min(plans[b].t_total, T)).  max_sink and max_tail bound every
+ * plan's sink and tail_count (they size the split-K grid; a plan above them
+ * is clamped).  With k_cols = 0, sink = 0 and tail [0, t_total) this is the
+ * dense decode of each sequence.  Workspace:
+ * lap_attn_decode_workspace_size(B, Hq, D, k_cols + max_sink + max_tail). */
+int lap_sparse_attn_decode_ragged(const void* q, int64_t q_sb, int64_t q_sh,
+                                  const void* keys, const void* vals, int dtype,
+                                  int B, int Hq, int Hkv, int T, int D,
+                                  int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                  int64_t v_sb, int64_t v_sh, int64_t v_st,
+                                  const void* indices, int idx_dtype, int H_idx,
+                                  int k_cols, const lap_row_plan* plans,
+                                  int max_sink, int max_tail, float scale,
+                                  void* out, void* workspace, size_t workspace_bytes,
+                                  lap_stream_t stream);
 
 /* ======================================================================= *
  * A6  Greedy AQ encode                                                     *

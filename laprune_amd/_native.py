@@ -59,12 +59,18 @@ SIGNATURES = {
                           i32, vp, sz, vp],
     "lap_retrieve_score": [vp, vp, i64, i64, i64, i32, i32, i32, i32, i32, i32, vp, vp, sz, vp],
     "lap_retrieve_select": [i32, i32, i32, i32, i32, i32, vp, i32, vp, sz, vp],
+    "lap_retrieve_topk_ragged": [vp, vp, i64, i64, i64, i32, i32, i32, vp, i32, i32, vp, vp, i32,
+                                 vp, sz, vp],
+    "lap_topk_select_ragged": [vp, i64, i32, i32, i32, i32, vp, i32, i32, vp, i32, vp, sz, vp],
     "lap_gqa_gather_kv": [vp, vp, i32, i32, i32, i32, i32, i64, i64, i64, i64, i64, i64, vp,
                           i32, i32, i32, i32, vp, vp, vp],
     "lap_attn_decode_workspace_size": [i32, i32, i32, i32, psz],
     "lap_sparse_attn_decode": [vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32, i64, i64,
                                i64, i64, i64, i64, vp, i32, i32, i32, i32, i32, i32, f32, vp,
                                vp, sz, vp],
+    "lap_sparse_attn_decode_ragged": [vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32, i64,
+                                      i64, i64, i64, i64, i64, vp, i32, i32, i32, vp, i32, i32,
+                                      f32, vp, vp, sz, vp],
     "lap_dense_attn_decode": [vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32, i64, i64,
                               i64, i64, i64, i64, f32, vp, vp, sz, vp],
     "lap_encode_prep_size": [i32, i32, i32, psz],

@@ -16,6 +16,11 @@ Mirrors two pieces of laprune/llm/modifiers/aq_evaluation.py:
 The encode goes straight from the strided K buffer into the strided code
 buffer with one ``lap_encode_keys`` launch (MFMA search, exact codes).  Growth
 allocates (torch); size ``capacity`` up front for HIP-graph capture.
+
+Sequences may have different lengths (ragged batches, which the reference
+does not have): each keeps its own ``lengths[b]`` and ``encoded_lens[b]``,
+new tokens land at each sequence's own end, and each flushes its encode
+buffer by the rule above on its own.
 """
 from __future__ import annotations
 
@@ -73,55 +78,124 @@ class DecodeKVCache:
         self.v = torch.empty_like(self.k)
         self.codes = torch.zeros((batch, num_kv_heads, cap, self.M), dtype=torch.uint8,
                                  device=self.dev)
-        self.length = 0
-        self.encoded_len = 0
+        self.lengths = [0] * batch
+        self.encoded_lens = [0] * batch
 
     @property
     def capacity(self) -> int:
         return int(self.k.shape[2])
+
+    @property
+    def ragged(self) -> bool:
+        return len(set(self.lengths)) > 1 or len(set(self.encoded_lens)) > 1
+
+    @property
+    def length(self) -> int:
+        """The common length of all sequences (RuntimeError when they differ)."""
+        if len(set(self.lengths)) > 1:
+            raise RuntimeError("sequences have different lengths: use .lengths")
+        return self.lengths[0]
+
+    @property
+    def encoded_len(self) -> int:
+        """The common encoded length (RuntimeError when sequences differ)."""
+        if len(set(self.encoded_lens)) > 1:
+            raise RuntimeError("sequences have different encoded lengths: use .encoded_lens")
+        return self.encoded_lens[0]
 
     def _grow(self, needed: int) -> None:
         cap = grown_capacity(self.capacity, needed)
         k = self.k.new_empty((self.B, self.Hkv, cap, self.D))
         v = self.v.new_empty((self.B, self.Hkv, cap, self.D))
         codes = self.codes.new_zeros((self.B, self.Hkv, cap, self.M))
-        if self.length:
-            k[:, :, :self.length] = self.k[:, :, :self.length]
-            v[:, :, :self.length] = self.v[:, :, :self.length]
-        if self.encoded_len:
-            codes[:, :, :self.encoded_len] = self.codes[:, :, :self.encoded_len]
+        n = max(self.lengths)
+        if n:
+            k[:, :, :n] = self.k[:, :, :n]
+            v[:, :, :n] = self.v[:, :, :n]
+        e = max(self.encoded_lens)
+        if e:
+            codes[:, :, :e] = self.codes[:, :, :e]
         self.k, self.v, self.codes = k, v, codes
 
-    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, prefill: bool = False) -> None:
-        """Append [B, Hkv, Tn, D] keys/values; encode the tail when the policy says so."""
+    def _check_new(self, k_new: torch.Tensor, v_new: torch.Tensor, batch: int) -> int:
         if k_new.shape != v_new.shape or k_new.dim() != 4:
             raise RuntimeError("k_new and v_new must both be [B, Hkv, Tn, D]")
         B, H, Tn, D = k_new.shape
-        if (B, H, D) != (self.B, self.Hkv, self.D):
-            raise RuntimeError(f"expected [{self.B}, {self.Hkv}, Tn, {self.D}], got "
+        if (B, H, D) != (batch, self.Hkv, self.D):
+            raise RuntimeError(f"expected [{batch}, {self.Hkv}, Tn, {self.D}], got "
                                f"{list(k_new.shape)}")
-        end = self.length + Tn
-        if end > self.capacity:
-            self._grow(end)
-        self.k[:, :, self.length:end] = k_new.to(self.dtype)
-        self.v[:, :, self.length:end] = v_new.to(self.dtype)
-        self.length = end
+        return Tn
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, prefill: bool = False) -> None:
+        """Append [B, Hkv, Tn, D] keys/values, Tn to every sequence at its own
+        end; encode the tails the policy says to."""
+        Tn = self._check_new(k_new, v_new, self.B)
+        ends = [n + Tn for n in self.lengths]
+        if max(ends) > self.capacity:
+            self._grow(max(ends))
+        if len(set(self.lengths)) == 1:
+            n = self.lengths[0]
+            self.k[:, :, n:n + Tn] = k_new.to(self.dtype)
+            self.v[:, :, n:n + Tn] = v_new.to(self.dtype)
+        else:
+            # one scatter per buffer: row b's tokens go to [lengths[b], +Tn)
+            pos = torch.tensor([[n + i for i in range(Tn)] for n in self.lengths],
+                               device=self.dev)
+            bidx = torch.arange(self.B, device=self.dev)[:, None]
+            self.k[bidx, :, pos] = k_new.to(self.dtype).permute(0, 2, 1, 3)
+            self.v[bidx, :, pos] = v_new.to(self.dtype).permute(0, 2, 1, 3)
+        self.lengths = ends
         self.encode(prefill=prefill)
+
+    def append_row(self, b: int, k_new: torch.Tensor, v_new: torch.Tensor,
+                   prefill: bool = True) -> None:
+        """Append [1, Hkv, Tn, D] keys/values to sequence b alone (a ragged
+        prefill fills each sequence this way); encode its tail by the policy."""
+        Tn = self._check_new(k_new, v_new, 1)
+        n = self.lengths[b]
+        if n + Tn > self.capacity:
+            self._grow(n + Tn)
+        self.k[b:b + 1, :, n:n + Tn] = k_new.to(self.dtype)
+        self.v[b:b + 1, :, n:n + Tn] = v_new.to(self.dtype)
+        self.lengths[b] = n + Tn
+        self._encode_rows([b], prefill, None)
 
     @torch.no_grad()
     def encode(self, prefill: bool = False, resid_norm: torch.Tensor | None = None) -> int:
-        """Encode [encoded_len, length) if the policy allows; returns rows encoded."""
-        rng = flush_range(self.length, self.encoded_len, self.group_size, prefill)
-        if rng is None:
+        """Encode each sequence's [encoded_len, length) if the policy allows;
+        returns rows encoded.  ``resid_norm`` ([B, Hkv, t1 - t0] fp32) needs
+        every sequence to flush the same range."""
+        return self._encode_rows(list(range(self.B)), prefill, resid_norm)
+
+    def _encode_rows(self, rows: list[int], prefill: bool, resid_norm) -> int:
+        todo = {}
+        for b in rows:
+            rng = flush_range(self.lengths[b], self.encoded_lens[b], self.group_size, prefill)
+            if rng is not None:
+                todo.setdefault(rng, []).append(b)
+        if not todo:
             return 0
-        t0, t1 = rng
-        k, c = self.k, self.codes
+        if resid_norm is not None and (len(todo) != 1 or len(rows) != self.B
+                                       or len(next(iter(todo.values()))) != self.B):
+            raise RuntimeError("resid_norm needs every sequence to flush the same range")
+        done = 0
+        for (t0, t1), bs in todo.items():
+            if len(bs) == self.B:
+                self._launch(0, self.B, t0, t1, resid_norm)
+            else:
+                for b in bs:
+                    self._launch(b, 1, t0, t1, None)
+            for b in bs:
+                self.encoded_lens[b] = t1
+            done += len(bs) * self.Hkv * (t1 - t0)
+        return done
+
+    def _launch(self, b0: int, nb: int, t0: int, t1: int, resid_norm) -> None:
+        k, c = self.k[b0:b0 + nb], self.codes[b0:b0 + nb]
         N.call("lap_encode_keys", N.ptr(k), N.dtype_code(k.dtype), k.stride(0), k.stride(1),
-               k.stride(2), self.B, self.Hkv, t0, t1, self.D, N.ptr(self.cb), self.M, self.K,
+               k.stride(2), nb, self.Hkv, t0, t1, self.D, N.ptr(self.cb), self.M, self.K,
                N.ptr(self.prep), self.prep.numel(), N.ptr(c), c.stride(0), c.stride(1),
                c.stride(2), N.ptr(resid_norm), N.stream_of(k))
-        self.encoded_len = t1
-        return self.B * self.Hkv * (t1 - t0)
 
     def keys(self) -> torch.Tensor:
         return self.k[:, :, :self.length]

@@ -58,22 +58,38 @@ struct AttnArgs {
   uint16_t* out;     // [B][Hq][D]
   float* part;       // [B][Hq][nsplit][D + 2] (m, l, o...)
   unsigned* ctr;     // [B * H_idx] arrival counters (zero between calls), or null
+  const int32_t* plans;  // lap_row_plan[B] (ragged batches) or null
 };
 
-// Keep-list position j (0 <= j < L) -> cache row, -1 when outside [0, T).
-// Branch-free: with HAS_IDX the index load is always issued (clamped into
-// the list), so every call issues the same number of loads and the
-// compiler's wait counts stay exact through the software pipeline.
+// The keep set of one sequence: [0, sink) ++ [tail_start, +tail_count) after
+// the index list, rows bounded by T.  The call's scalars, or the sequence's
+// plan with sink and tail clamped to the call's (which size the grid).
+struct RowKeep {
+  int sink, tail_start, tail_count, T;
+};
+__device__ __forceinline__ RowKeep row_keep(const AttnArgs& a, int b) {
+  if (!a.plans) return RowKeep{a.sink, a.tail_start, a.tail_count, a.T};
+  const int32_t* p = a.plans + (int64_t)b * kPlanInts;
+  return RowKeep{min(max(p[5], 0), a.sink), p[6], min(max(p[7], 0), a.tail_count),
+                 min(p[1], a.T)};
+}
+
+// Keep-list position j (0 <= j < n_idx + sink + tail_count) -> cache row, -1
+// when outside [0, T).  Branch-free: with HAS_IDX the index load is always
+// issued (clamped into the list), so every call issues the same number of
+// loads and the compiler's wait counts stay exact through the software
+// pipeline.
 template <bool HAS_IDX, typename IT>
-__device__ __forceinline__ int keep_token(const AttnArgs& a, const IT* idx_row, int j) {
+__device__ __forceinline__ int keep_token(const AttnArgs& a, const RowKeep& rk,
+                                          const IT* idx_row, int j) {
   const int jt = j - a.n_idx;
-  int64_t t = jt < a.sink ? jt : (int64_t)a.tail_start + (jt - a.sink);
+  int64_t t = jt < rk.sink ? jt : (int64_t)rk.tail_start + (jt - rk.sink);
   if (HAS_IDX) {
     const int ji = j < a.n_idx ? j : a.n_idx - 1;
     const int64_t ti = (int64_t)idx_row[ji];
     t = j < a.n_idx ? ti : t;
   }
-  return (t < 0 || t >= a.T) ? -1 : (int)t;
+  return (t < 0 || t >= rk.T) ? -1 : (int)t;
 }
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -230,7 +246,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int G = a.Hq / a.Hkv;
   const int h0 = (a.H_idx == a.Hq) ? ri : ri * G;  // first query head of the row
   const int hkv = h0 / G;
-  const int L = a.n_idx + a.sink + a.tail_count;
+  const RowKeep rk = row_keep(a, b);
+  const int L = a.n_idx + rk.sink + rk.tail_count;
   const int lo = s * a.per_split;
   const int hi = min(L, lo + a.per_split);
   const IT* idx_row =
@@ -260,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int jmax = hi > lo ? hi - 1 : 0;
   auto pos_tok = [&](int i) -> int {
     const int jpos = lo + (wave + 4 * i) * kKeys + (lane & 15);
-    const int tk = keep_token<HAS_IDX, IT>(a, idx_row, jpos < jmax ? jpos : jmax);
+    const int tk = keep_token<HAS_IDX, IT>(a, rk, idx_row, jpos < jmax ? jpos : jmax);
     return (i < mine && jpos < hi) ? tk : -1;
   };
   // Pipeline: keep-list rows two steps ahead, K/V one step ahead, ping-pong
@@ -587,6 +604,42 @@ extern "C" int lap_sparse_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
   a.idx = indices;
   a.H_idx = H_idx; a.n_idx = n_idx; a.sink = sink_count;
   a.tail_start = tail_start; a.tail_count = tail_count;
+  a.scale_log2 = scale * kLog2e;
+  a.out = static_cast<uint16_t*>(out);
+  return run_attn(a, dtype, idx_dtype, D, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int lap_sparse_attn_decode_ragged(
+    const void* q, int64_t q_sb, int64_t q_sh, const void* keys, const void* vals, int dtype,
+    int B, int Hq, int Hkv, int T, int D, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
+    int64_t v_sh, int64_t v_st, const void* indices, int idx_dtype, int H_idx, int k_cols,
+    const lap_row_plan* plans, int max_sink, int max_tail, float scale, void* out,
+    void* workspace, size_t workspace_bytes, lap_stream_t stream) {
+  clear_error();
+  int s = check_common(q, keys, vals, out, dtype, B, Hq, Hkv, T, D, q_sh, k_st, v_st);
+  if (s != LAP_OK) return s;
+  LAP_CHECK(plans, "ragged decode: null plans");
+  LAP_CHECK(H_idx == Hq || H_idx == Hkv, "ragged decode: H_idx must be Hq or Hkv");
+  LAP_CHECK(k_cols >= 0 && max_sink >= 0 && max_tail >= 0, "ragged decode: negative count");
+  LAP_CHECK(k_cols == 0 || indices, "ragged decode: indices required");
+  LAP_CHECK(idx_dtype == LAP_DTYPE_I32 || idx_dtype == LAP_DTYPE_I64,
+            "ragged decode: idx must be int64 or int32");
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.k = static_cast<const uint16_t*>(keys);
+  a.v = static_cast<const uint16_t*>(vals);
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T = T;
+  a.idx = indices;
+  a.H_idx = H_idx; a.n_idx = k_cols;
+  // grid bounds; each sequence's own windows come from its plan
+  a.sink = max_sink;
+  a.tail_start = 0;
+  a.tail_count = max_tail;
+  a.plans = reinterpret_cast<const int32_t*>(plans);
   a.scale_log2 = scale * kLog2e;
   a.out = static_cast<uint16_t*>(out);
   return run_attn(a, dtype, idx_dtype, D, workspace, workspace_bytes, as_stream(stream));

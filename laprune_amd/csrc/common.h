@@ -14,6 +14,12 @@
 
 namespace lap {
 
+// lap_row_plan as seen by kernels: kPlanInts int32 fields per sequence, in
+// declaration order (t_codes, t_total, cand_start, cand_end, k, sink,
+// tail_start, tail_count).
+constexpr int kPlanInts = 8;
+static_assert(sizeof(lap_row_plan) == kPlanInts * sizeof(int32_t), "lap_row_plan layout");
+
 // ---------------------------------------------------------------- errors
 void set_error(const char* fmt, ...);
 void clear_error();

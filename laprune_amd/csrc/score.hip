@@ -47,7 +47,28 @@ struct ScoreOut {
   uint32_t* hist;    // [R][nchunk][256] or null
   int key_mode;
   int cand_start, cand_end;
+  const int32_t* plans;  // lap_row_plan[B] (ragged batches) or null
 };
+
+// Columns a row scores, [0, t_end), and its histogram window [cs, ce): the
+// call's scalars, or the sequence's plan clamped to the T scored columns.
+struct RowCols {
+  int t_end, cs, ce;
+};
+__device__ __forceinline__ RowCols row_cols(const ScoreOut& so, int b, int T) {
+  if (!so.plans) return RowCols{T, so.cand_start, so.cand_end};
+  const int32_t* p = so.plans + (int64_t)b * kPlanInts;
+  return RowCols{min(max(p[0], 0), T), p[2], p[3]};
+}
+
+// A workgroup whose chunk lies past its row's columns: empty histogram.
+__device__ __forceinline__ void write_empty_hist(const ScoreOut& so, int r, int R, int chunk,
+                                                 int tid, int threads) {
+  if (!so.hist) return;
+  const int nchunk = gridDim.x / R;
+  uint32_t* dst = so.hist + ((int64_t)r * nchunk + chunk) * 256;
+  for (int i = tid; i < 256; i += threads) dst[i] = 0u;
+}
 
 // Accumulate one token's 32 lookups into four fp32 head sums.
 __device__ __forceinline__ void score_token(const char* __restrict__ lds, const uint4 c0,
@@ -77,6 +98,13 @@ __global__ __launch_bounds__(THREADS) void score_g4_kernel(
   const int chunk = blockIdx.x / R;
   const int tid = threadIdx.x;
   const int b = r / Hkv, hkv = r - b * Hkv;
+  const RowCols rc = row_cols(so, b, T);
+  const int t0 = chunk * chunk_tokens;
+  const int t1 = min(rc.t_end, t0 + chunk_tokens);
+  if (t0 >= t1) {
+    write_empty_hist(so, r, R, chunk, tid, THREADS);
+    return;
+  }
 
   // Fill the [M][K][G] table.
   if (LUT_IL) {
@@ -100,8 +128,6 @@ __global__ __launch_bounds__(THREADS) void score_g4_kernel(
 
   const char* lds = reinterpret_cast<const char*>(s_lut);
   const uint8_t* crow = codes + (int64_t)b * cs_b + (int64_t)hkv * cs_h;
-  const int t0 = chunk * chunk_tokens;
-  const int t1 = min(T, t0 + chunk_tokens);
 
   for (int base = t0; base < t1; base += 2 * THREADS) {
     const int ta = base + tid, tb = base + THREADS + tid;
@@ -141,7 +167,7 @@ __global__ __launch_bounds__(THREADS) void score_g4_kernel(
         const uint16_t hm = f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
         const uint32_t key = so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(hm) : f16_key(hm);
         if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
-        if (so.hist && t >= so.cand_start && t < so.cand_end) atomicAdd(&s_hist[key >> 8], 1u);
+        if (so.hist && t >= rc.cs && t < rc.ce) atomicAdd(&s_hist[key >> 8], 1u);
       }
     }
   }
@@ -227,8 +253,13 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
   const int chunk = blockIdx.x / R;
   const int tid = threadIdx.x;
   const int b = r / Hkv, hkv = r - b * Hkv;
+  const RowCols rc = row_cols(so, b, T);
   const int t0 = chunk * (THREADS * TOK);
-  const int t1 = min(T, t0 + THREADS * TOK);  // t1 > t0 by the grid
+  const int t1 = min(rc.t_end, t0 + THREADS * TOK);  // without plans t1 > t0 by the grid
+  if (t0 >= t1) {
+    write_empty_hist(so, r, R, chunk, tid, THREADS);
+    return;
+  }
 
   const uint4* src = reinterpret_cast<const uint4*>(lut + (int64_t)r * (kG * kM * kK));
   u32x4 f[kFill];
@@ -279,7 +310,7 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
       const uint16_t hm = f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
       const uint32_t key = so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(hm) : f16_key(hm);
       if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
-      if (so.hist && t >= so.cand_start && t < so.cand_end) atomicAdd(&s_hist[key >> 8], 1u);
+      if (so.hist && t >= rc.cs && t < rc.ce) atomicAdd(&s_hist[key >> 8], 1u);
     }
   }
 
@@ -512,12 +543,12 @@ static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, const uin
 int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int64_t cs_b,
                     int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, uint16_t* heads,
                     uint16_t* keys, uint32_t* hist, int key_mode, int cand_start,
-                    int cand_end, int* nchunk_out, hipStream_t st) {
+                    int cand_end, const int32_t* plans, int* nchunk_out, hipStream_t st) {
   const int R = B * Hkv;
   G4Plan pl;
   int s = g4_plan(R, T, lut_il, &pl);
   if (s != LAP_OK) return s;
-  ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end};
+  ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end, plans};
   dim3 grid((unsigned)(R * pl.nchunk));
   if (pl.kind == 0) {
     if (lut_il)
@@ -588,7 +619,7 @@ extern "C" int lap_lut_score_grouped(const void* lut, int lut_layout, const uint
   if (G == 4 && M == kM && K == kK && score_g4_supported(codes, 0, codes_stride_h, codes_stride_t)) {
     return launch_score_g4(L, lut_layout == LAP_LUT_GMKG, codes, 0, codes_stride_h,
                            codes_stride_t, 1, Hkv, T, static_cast<uint16_t*>(out), nullptr,
-                           nullptr, LAP_KEY_F16, 0, 0, nullptr, st);
+                           nullptr, LAP_KEY_F16, 0, 0, nullptr, nullptr, st);
   }
   DevInfo di;
   int s = device_info(&di);

@@ -23,7 +23,7 @@ namespace lap {
 int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int64_t cs_b,
                     int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, uint16_t* heads,
                     uint16_t* keys, uint32_t* hist, int key_mode, int cand_start, int cand_end,
-                    int* nchunk_out, hipStream_t st);
+                    const int32_t* plans, int* nchunk_out, hipStream_t st);
 bool score_g4_supported(const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t);
 int score_g4_nchunk(int R, int T);
 
@@ -65,33 +65,63 @@ __device__ __forceinline__ uint32_t key_of(uint16_t h) {
   return KEYMODE == LAP_KEY_BF16 ? bf16_key_of_f16(h) : f16_key(h);
 }
 
+// Candidate window [cs, cs + n) and budget k of one top-k row.
+struct SelRow {
+  int n, k, cs;
+};
+
+// Window and budget of every row: one for all rows, or per sequence from
+// lap_row_plan (ragged batches; row r belongs to sequence r / rows_per_plan).
+struct SelSpec {
+  int n, k, cs;              // uniform window and budget (k <= n)
+  const int32_t* plans;      // lap_row_plan[B] or null
+  int rows_per_plan;
+  int k_cols;                // output row width when plans are given
+  int t_cols;                // columns available; plans are clamped to them
+  __device__ __forceinline__ SelRow row(int r) const {
+    if (!plans) return SelRow{n, k, cs};
+    const int32_t* p = plans + (int64_t)(r / rows_per_plan) * kPlanInts;
+    const int te = min(max(p[0], 0), t_cols);
+    const int c0 = min(max(p[2], 0), te), c1 = min(max(p[3], c0), te);
+    const int nn = c1 - c0;
+    return SelRow{nn, max(0, min(min(p[4], nn), k_cols)), c0};
+  }
+};
+
 template <int KEYMODE>
 __global__ __launch_bounds__(kThreads) void topk_prep_kernel(
-    const uint16_t* __restrict__ scores, int64_t row_stride, int R, int group, int cand_start,
-    int n, int C, uint16_t* __restrict__ keys, uint32_t* __restrict__ hist1) {
+    const uint16_t* __restrict__ scores, int64_t row_stride, int R, int group, SelSpec sp,
+    int64_t key_stride, int C, uint16_t* __restrict__ keys, uint32_t* __restrict__ hist1) {
   __shared__ uint32_t s_h[256];
   const int r = blockIdx.x % R, c = blockIdx.x / R;
+  const SelRow sr = sp.row(r);
   s_h[threadIdx.x] = 0;
   __syncthreads();
-  const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
+  const int e0 = c * kChunk, e1 = min(sr.n, e0 + kChunk);
 #pragma unroll 8
   for (int e = e0 + threadIdx.x; e < e1; e += kThreads) {
     uint32_t key = 0;
     for (int g = 0; g < group; ++g) {
-      const uint16_t h = scores[(int64_t)(r * group + g) * row_stride + cand_start + e];
+      const uint16_t h = scores[(int64_t)(r * group + g) * row_stride + sr.cs + e];
       key = max(key, key_of<KEYMODE>(h));
     }
-    keys[(int64_t)r * n + e] = (uint16_t)key;
+    keys[(int64_t)r * key_stride + e] = (uint16_t)key;
     atomicAdd(&s_h[key >> 8], 1u);
   }
   __syncthreads();
   hist1[((int64_t)r * C + c) * 256 + threadIdx.x] = s_h[threadIdx.x];
 }
 
+// Keys of a row: candidate e of row r is keys[r * stride + e] when the keys
+// were stored window-relative (topk_prep_kernel), keys[r * stride + cs + e]
+// when they are indexed by column (the fused scorer).
 struct KeySrc {
   const uint16_t* keys;
-  int64_t stride;  // row stride of keys
-  int off;         // column of candidate 0
+  int64_t stride;
+  bool by_column;
+  __device__ __forceinline__ const uint16_t* row(int r, const SelRow& sr) const {
+    return keys + (int64_t)r * stride + (by_column ? sr.cs : 0);
+  }
 };
 
 // Sum of n values p[0], p[stride], ... with 32 independent loads in flight
@@ -147,14 +177,20 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t x, uint32_t* s
 constexpr int kPer = kChunk / kThreads;  // keys per thread, contiguous
 
 __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
-    KeySrc ks, int R, int n, int k, const uint32_t* __restrict__ hist1, int C1, int C,
+    KeySrc ks, int R, SelSpec sp, const uint32_t* __restrict__ hist1, int C1, int C,
     uint32_t* __restrict__ hist2, uint32_t* __restrict__ gtc, uint32_t* __restrict__ info) {
   __shared__ uint32_t s_h[256], s_h2[256], s_wsum[kWaves], s_res[2], s_gt;
   const int r = blockIdx.x % R, c = blockIdx.x / R;
   const int tid = threadIdx.x;
+  const SelRow sr = sp.row(r);
+  const int e0 = c * kChunk, e1 = min(sr.n, e0 + kChunk);
+  if (sr.k == 0 || e0 >= e1) {  // nothing of this row here (ragged rows only)
+    hist2[((int64_t)r * C + c) * 256 + tid] = 0u;
+    if (tid == 0) gtc[(int64_t)r * C + c] = 0u;
+    return;
+  }
   // this thread's keys first, so their latency overlaps the histogram sum
-  const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
-  const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
+  const uint16_t* kr = ks.row(r, sr);
   uint32_t kv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -167,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
   s_h2[tid] = 0;
   if (tid == 0) s_gt = 0;
   __syncthreads();
-  select_bin(s_h, (uint32_t)k, s_wsum, s_res);
+  select_bin(s_h, (uint32_t)sr.k, s_wsum, s_res);
   const uint32_t b1 = s_res[0];
   if (c == 0 && tid == 0) {
     info[r * 4 + 0] = b1;
@@ -189,14 +225,19 @@ __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
 
 template <typename OUT_T>
 __global__ __launch_bounds__(kThreads) void topk_select_kernel(
-    KeySrc ks, int R, int n, int k, int C, const uint32_t* __restrict__ hist2,
-    const uint32_t* __restrict__ gtc, const uint32_t* __restrict__ info, int cand_start,
+    KeySrc ks, int R, SelSpec sp, int C, const uint32_t* __restrict__ hist2,
+    const uint32_t* __restrict__ gtc, const uint32_t* __restrict__ info,
     OUT_T* __restrict__ out, int64_t out_stride) {
   __shared__ uint32_t s_tot[256], s_pre[256], s_wsum[kWaves], s_res[2], s_red[kWaves];
   const int r = blockIdx.x % R, c = blockIdx.x / R;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int e0 = c * kChunk, e1 = min(n, e0 + kChunk);
-  const uint16_t* kr = ks.keys + (int64_t)r * ks.stride + ks.off;
+  const SelRow sr = sp.row(r);
+  OUT_T* orow = out + (int64_t)r * out_stride;
+  if (sp.plans && c == 0)  // ragged rows: pad past the row's k with -1
+    for (int i = sr.k + tid; i < sp.k_cols; i += kThreads) orow[i] = (OUT_T)-1;
+  const int e0 = c * kChunk, e1 = min(sr.n, e0 + kChunk);
+  if (sr.k == 0 || e0 >= e1) return;
+  const uint16_t* kr = ks.row(r, sr);
   uint32_t kv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -212,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
   uint32_t g = 0;
   for (int cc = tid; cc < c; cc += kThreads) g += gtc[(int64_t)r * C + cc];
   __syncthreads();
-  const uint32_t k2 = (uint32_t)k - gt1;
+  const uint32_t k2 = (uint32_t)sr.k - gt1;
   select_bin(s_tot, k2, s_wsum, s_res);
   const uint32_t b2 = s_res[0];
   const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
@@ -242,7 +283,6 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
   const uint32_t take = tie_rank0 >= need ? 0u : min(ntie, need - tie_rank0);
   uint32_t all_sel;
   uint32_t pos = base + block_exclusive_scan(ngt + take, s_wsum, &all_sel);
-  OUT_T* orow = out + (int64_t)r * out_stride;
   uint32_t taken = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -253,7 +293,7 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
       sel = true;
       ++taken;
     }
-    if (sel) orow[pos++] = (OUT_T)(cand_start + e);
+    if (sel) orow[pos++] = (OUT_T)(sr.cs + e);
   }
 }
 
@@ -286,20 +326,21 @@ Ws carve(void* base, int R, int64_t key_cols, int C1, int C2) {
   return w;
 }
 
-int run_levels(const Ws& w, KeySrc ks, int R, int n, int k, int C1, int cand_start,
+// Level 2 and the compaction over C2 chunks of kChunk candidates; n_max is
+// the widest row's window.
+int run_levels(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int C1,
                void* out, int out_dtype, int64_t out_stride, hipStream_t st) {
-  const int C2 = (n + kChunk - 1) / kChunk;
-  hipLaunchKernelGGL(topk_level2_kernel, dim3(R * C2), dim3(kThreads), 0, st, ks, R, n, k,
+  const int C2 = (n_max + kChunk - 1) / kChunk;
+  if (C2 == 0) return LAP_OK;
+  hipLaunchKernelGGL(topk_level2_kernel, dim3(R * C2), dim3(kThreads), 0, st, ks, R, sp,
                      w.hist1, C1, C2, w.hist2, w.gtc, w.info);
   LAP_LAUNCH_CHECK("topk_level2_kernel");
   if (out_dtype == LAP_DTYPE_I64)
     hipLaunchKernelGGL(topk_select_kernel<int64_t>, dim3(R * C2), dim3(kThreads), 0, st, ks, R,
-                       n, k, C2, w.hist2, w.gtc, w.info, cand_start,
-                       static_cast<int64_t*>(out), out_stride);
+                       sp, C2, w.hist2, w.gtc, w.info, static_cast<int64_t*>(out), out_stride);
   else
     hipLaunchKernelGGL(topk_select_kernel<int32_t>, dim3(R * C2), dim3(kThreads), 0, st, ks, R,
-                       n, k, C2, w.hist2, w.gtc, w.info, cand_start,
-                       static_cast<int32_t*>(out), out_stride);
+                       sp, C2, w.hist2, w.gtc, w.info, static_cast<int32_t*>(out), out_stride);
   LAP_LAUNCH_CHECK("topk_select_kernel");
   return LAP_OK;
 }
@@ -312,6 +353,58 @@ int retrieve_chunk_bound(int T) { return (T + 255) / 256; }
 }  // namespace lap
 
 using namespace lap;
+
+namespace {
+
+SelSpec uniform_spec(int cand_start, int n, int k_eff) {
+  SelSpec sp{};
+  sp.n = n;
+  sp.k = k_eff;
+  sp.cs = cand_start;
+  sp.rows_per_plan = 1;
+  sp.k_cols = k_eff;
+  return sp;
+}
+
+SelSpec ragged_spec(const lap_row_plan* plans, int rows_per_plan, int k_cols, int T) {
+  SelSpec sp{};
+  sp.plans = reinterpret_cast<const int32_t*>(plans);
+  sp.rows_per_plan = rows_per_plan;
+  sp.k_cols = k_cols;
+  sp.t_cols = T;
+  return sp;
+}
+
+// fp16 scores -> window-relative keys (row stride n_max) and level-1
+// histograms, then the two levels.
+int select_from_scores(const void* scores, int64_t row_stride, int R, int group, int key_mode,
+                       const SelSpec& sp, int n_max, void* out_idx, int out_dtype,
+                       int64_t out_stride, void* workspace, size_t ws_bytes, const char* who,
+                       hipStream_t st) {
+  const int C = (n_max + kChunk - 1) / kChunk;
+  Ws w = carve(workspace, R, n_max, C, C);
+  LAP_CHECK_CODE(workspace && ws_bytes >= w.bytes, LAP_ERR_WORKSPACE,
+                 "%s: workspace of %zu bytes needed", who, w.bytes);
+  const uint16_t* S = static_cast<const uint16_t*>(scores);
+  if (key_mode == LAP_KEY_BF16)
+    hipLaunchKernelGGL(topk_prep_kernel<LAP_KEY_BF16>, dim3(R * C), dim3(kThreads), 0, st, S,
+                       row_stride, R, group, sp, (int64_t)n_max, C, w.keys, w.hist1);
+  else
+    hipLaunchKernelGGL(topk_prep_kernel<LAP_KEY_F16>, dim3(R * C), dim3(kThreads), 0, st, S,
+                       row_stride, R, group, sp, (int64_t)n_max, C, w.keys, w.hist1);
+  LAP_LAUNCH_CHECK("topk_prep_kernel");
+  KeySrc ks{w.keys, n_max, false};
+  return run_levels(w, ks, R, sp, n_max, C, out_idx, out_dtype, out_stride, st);
+}
+
+int check_key_and_out(int key_mode, int out_dtype, const char* who) {
+  LAP_CHECK(key_mode == LAP_KEY_F16 || key_mode == LAP_KEY_BF16, "%s: bad key mode", who);
+  LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
+            "%s: out dtype must be int32/int64", who);
+  return LAP_OK;
+}
+
+}  // namespace
 
 extern "C" int lap_topk_workspace_size(int R, int cand_len, size_t* bytes) {
   clear_error();
@@ -333,27 +426,35 @@ extern "C" int lap_topk_select(const void* scores, int64_t score_row_stride, int
             "lap_topk_select: candidate window [%d,%d) outside [0,%d)", cand_start, cand_end, T);
   LAP_CHECK(k >= 0, "lap_topk_select: k must be non-negative");
   LAP_CHECK(score_row_stride >= T, "lap_topk_select: row stride < T");
-  LAP_CHECK(key_mode == LAP_KEY_F16 || key_mode == LAP_KEY_BF16, "lap_topk_select: bad key mode");
-  LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
-            "lap_topk_select: out dtype must be int32/int64");
+  int s = check_key_and_out(key_mode, out_dtype, "lap_topk_select");
+  if (s != LAP_OK) return s;
   const int n = cand_end - cand_start;
   const int ke = std::min(k, n);
   if (ke == 0) return LAP_OK;
-  const int C = (n + kChunk - 1) / kChunk;
-  Ws w = carve(workspace, R, n, C, C);
-  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
-                 "lap_topk_select: workspace of %zu bytes needed", w.bytes);
-  hipStream_t st = as_stream(stream);
-  const uint16_t* S = static_cast<const uint16_t*>(scores);
-  if (key_mode == LAP_KEY_BF16)
-    hipLaunchKernelGGL(topk_prep_kernel<LAP_KEY_BF16>, dim3(R * C), dim3(kThreads), 0, st, S,
-                       score_row_stride, R, group, cand_start, n, C, w.keys, w.hist1);
-  else
-    hipLaunchKernelGGL(topk_prep_kernel<LAP_KEY_F16>, dim3(R * C), dim3(kThreads), 0, st, S,
-                       score_row_stride, R, group, cand_start, n, C, w.keys, w.hist1);
-  LAP_LAUNCH_CHECK("topk_prep_kernel");
-  KeySrc ks{w.keys, n, 0};
-  return run_levels(w, ks, R, n, ke, C, cand_start, out_idx, out_dtype, k, st);
+  return select_from_scores(scores, score_row_stride, R, group, key_mode,
+                            uniform_spec(cand_start, n, ke), n, out_idx, out_dtype, k, workspace,
+                            workspace_bytes, "lap_topk_select", as_stream(stream));
+}
+
+extern "C" int lap_topk_select_ragged(const void* scores, int64_t score_row_stride, int R,
+                                      int group, int rows_per_plan, int T,
+                                      const lap_row_plan* plans, int k_cols, int key_mode,
+                                      void* out_idx, int out_dtype, void* workspace,
+                                      size_t workspace_bytes, lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(scores && plans && (out_idx || k_cols == 0), "lap_topk_select_ragged: null pointer");
+  LAP_CHECK(R > 0 && group > 0 && T > 0 && k_cols >= 0, "lap_topk_select_ragged: bad sizes");
+  LAP_CHECK(rows_per_plan > 0 && R % rows_per_plan == 0,
+            "lap_topk_select_ragged: R=%d is not a multiple of rows_per_plan=%d", R,
+            rows_per_plan);
+  LAP_CHECK(score_row_stride >= T, "lap_topk_select_ragged: row stride < T");
+  int s = check_key_and_out(key_mode, out_dtype, "lap_topk_select_ragged");
+  if (s != LAP_OK) return s;
+  if (k_cols == 0) return LAP_OK;
+  return select_from_scores(scores, score_row_stride, R, group, key_mode,
+                            ragged_spec(plans, rows_per_plan, k_cols, T), T, out_idx, out_dtype,
+                            k_cols, workspace, workspace_bytes, "lap_topk_select_ragged",
+                            as_stream(stream));
 }
 
 extern "C" int lap_retrieve_workspace_size(int R, int T, size_t* bytes) {
@@ -366,18 +467,55 @@ extern "C" int lap_retrieve_workspace_size(int R, int T, size_t* bytes) {
 }
 
 static int retrieve_checks(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b,
-                           int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, int cand_start,
-                           int cand_end, int k, int key_mode) {
-  LAP_CHECK(lut_gmkg && codes, "lap_retrieve: null pointer");
-  LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "lap_retrieve: bad sizes");
-  LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
-            "lap_retrieve: candidate window [%d,%d) outside [0,%d)", cand_start, cand_end, T);
-  LAP_CHECK(k >= 0, "lap_retrieve: k must be non-negative");
-  LAP_CHECK(key_mode == LAP_KEY_F16 || key_mode == LAP_KEY_BF16, "lap_retrieve: bad key mode");
-  LAP_CHECK(cs_t >= 32, "lap_retrieve: codes token stride < M=32");
+                           int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, int key_mode,
+                           const char* who) {
+  LAP_CHECK(lut_gmkg && codes, "%s: null pointer", who);
+  LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "%s: bad sizes", who);
+  LAP_CHECK(key_mode == LAP_KEY_F16 || key_mode == LAP_KEY_BF16, "%s: bad key mode", who);
+  LAP_CHECK(cs_t >= 32, "%s: codes token stride < M=32", who);
   LAP_CHECK_CODE(score_g4_supported(codes, cs_b, cs_h, cs_t), LAP_ERR_UNSUPPORTED,
-                 "lap_retrieve: codes base and strides must be 16-byte aligned");
+                 "%s: codes base and strides must be 16-byte aligned", who);
   return LAP_OK;
+}
+
+// The fused scorer: per-head scores (optional), column-indexed group keys
+// and level-1 histograms in the workspace.
+static int retrieve_score_impl(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b,
+                               int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, int cand_start,
+                               int cand_end, const lap_row_plan* plans, int key_mode,
+                               void* scores_out, void* workspace, size_t workspace_bytes,
+                               const char* who, hipStream_t st) {
+  const int R = B * Hkv;
+  const int C2 = (T + kChunk - 1) / kChunk;
+  Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
+  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
+                 "%s: workspace of %zu bytes needed", who, w.bytes);
+  int C1 = 0;
+  int s = launch_score_g4(static_cast<const uint16_t*>(lut_gmkg), true, codes, cs_b, cs_h, cs_t,
+                          B, Hkv, T, static_cast<uint16_t*>(scores_out), w.keys, w.hist1,
+                          key_mode, cand_start, cand_end,
+                          reinterpret_cast<const int32_t*>(plans), &C1, st);
+  if (s != LAP_OK) return s;
+  LAP_CHECK_CODE(C1 <= retrieve_chunk_bound(T), LAP_ERR_INVALID,
+                 "%s: internal chunk bound exceeded", who);
+  return LAP_OK;
+}
+
+// Levels over the keys and histograms retrieve_score_impl left.
+static int retrieve_select_impl(int B, int Hkv, int T, const SelSpec& sp, int n_max,
+                                void* out_idx, int out_dtype, int64_t out_stride,
+                                void* workspace, size_t workspace_bytes, const char* who,
+                                hipStream_t st) {
+  const int R = B * Hkv;
+  const int C2 = (T + kChunk - 1) / kChunk;
+  Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
+  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
+                 "%s: workspace of %zu bytes needed", who, w.bytes);
+  const int C1 = score_g4_nchunk(R, T);
+  LAP_CHECK_CODE(C1 > 0 && C1 <= retrieve_chunk_bound(T), LAP_ERR_HIP,
+                 "%s: device query failed", who);
+  KeySrc ks{w.keys, T, true};
+  return run_levels(w, ks, R, sp, n_max, C1, out_idx, out_dtype, out_stride, st);
 }
 
 extern "C" int lap_retrieve_score(const void* lut_gmkg, const uint8_t* codes,
@@ -388,22 +526,14 @@ extern "C" int lap_retrieve_score(const void* lut_gmkg, const uint8_t* codes,
                                   lap_stream_t stream) {
   clear_error();
   int s = retrieve_checks(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
-                          Hkv, T, cand_start, cand_end, 0, key_mode);
+                          Hkv, T, key_mode, "lap_retrieve_score");
   if (s != LAP_OK) return s;
-  const int R = B * Hkv;
-  const int C2 = (T + kChunk - 1) / kChunk;
-  Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
-  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
-                 "lap_retrieve_score: workspace of %zu bytes needed", w.bytes);
-  int C1 = 0;
-  s = launch_score_g4(static_cast<const uint16_t*>(lut_gmkg), true, codes, codes_stride_b,
-                      codes_stride_h, codes_stride_t, B, Hkv, T,
-                      static_cast<uint16_t*>(scores_out), w.keys, w.hist1, key_mode,
-                      cand_start, cand_end, &C1, as_stream(stream));
-  if (s != LAP_OK) return s;
-  LAP_CHECK_CODE(C1 <= retrieve_chunk_bound(T), LAP_ERR_INVALID,
-                 "lap_retrieve_score: internal chunk bound exceeded");
-  return LAP_OK;
+  LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
+            "lap_retrieve_score: candidate window [%d,%d) outside [0,%d)", cand_start, cand_end,
+            T);
+  return retrieve_score_impl(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
+                             Hkv, T, cand_start, cand_end, nullptr, key_mode, scores_out,
+                             workspace, workspace_bytes, "lap_retrieve_score", as_stream(stream));
 }
 
 extern "C" int lap_retrieve_select(int B, int Hkv, int T, int cand_start, int cand_end, int k,
@@ -418,19 +548,12 @@ extern "C" int lap_retrieve_select(int B, int Hkv, int T, int cand_start, int ca
   LAP_CHECK(k >= 0, "lap_retrieve_select: k must be non-negative");
   LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
             "lap_retrieve_select: out dtype must be int32/int64");
-  const int R = B * Hkv;
   const int n = cand_end - cand_start;
   const int ke = std::min(k, n);
   if (ke == 0) return LAP_OK;
-  const int C2 = (T + kChunk - 1) / kChunk;
-  Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
-  LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
-                 "lap_retrieve_select: workspace of %zu bytes needed", w.bytes);
-  const int C1 = score_g4_nchunk(R, T);
-  LAP_CHECK_CODE(C1 > 0 && C1 <= retrieve_chunk_bound(T), LAP_ERR_HIP,
-                 "lap_retrieve_select: device query failed");
-  KeySrc ks{w.keys, T, cand_start};
-  return run_levels(w, ks, R, n, ke, C1, cand_start, out_idx, out_dtype, k, as_stream(stream));
+  return retrieve_select_impl(B, Hkv, T, uniform_spec(cand_start, n, ke), n, out_idx, out_dtype,
+                              k, workspace, workspace_bytes, "lap_retrieve_select",
+                              as_stream(stream));
 }
 
 extern "C" int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
@@ -441,10 +564,36 @@ extern "C" int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
                                  size_t workspace_bytes, lap_stream_t stream) {
   clear_error();
   LAP_CHECK(out_idx || k == 0, "lap_retrieve_topk: null output");
+  LAP_CHECK(k >= 0, "lap_retrieve_topk: k must be non-negative");
   int s = lap_retrieve_score(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
                              Hkv, T, cand_start, cand_end, key_mode, scores_out, workspace,
                              workspace_bytes, stream);
-  if (s != LAP_OK) return s;
+  if (s != LAP_OK || k == 0) return s;
   return lap_retrieve_select(B, Hkv, T, cand_start, cand_end, k, out_idx, out_dtype, workspace,
                              workspace_bytes, stream);
+}
+
+extern "C" int lap_retrieve_topk_ragged(const void* lut_gmkg, const uint8_t* codes,
+                                        int64_t codes_stride_b, int64_t codes_stride_h,
+                                        int64_t codes_stride_t, int B, int Hkv, int T,
+                                        const lap_row_plan* plans, int k_cols, int key_mode,
+                                        void* scores_out, void* out_idx, int out_dtype,
+                                        void* workspace, size_t workspace_bytes,
+                                        lap_stream_t stream) {
+  clear_error();
+  const char* who = "lap_retrieve_topk_ragged";
+  int s = retrieve_checks(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
+                          Hkv, T, key_mode, who);
+  if (s != LAP_OK) return s;
+  LAP_CHECK(plans, "%s: null plans", who);
+  LAP_CHECK(k_cols >= 0 && (out_idx || k_cols == 0), "%s: bad output", who);
+  LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
+            "%s: out dtype must be int32/int64", who);
+  hipStream_t st = as_stream(stream);
+  s = retrieve_score_impl(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B, Hkv,
+                          T, 0, 0, plans, key_mode, scores_out, workspace, workspace_bytes, who,
+                          st);
+  if (s != LAP_OK || k_cols == 0) return s;
+  return retrieve_select_impl(B, Hkv, T, ragged_spec(plans, Hkv, k_cols, T), T, out_idx,
+                              out_dtype, k_cols, workspace, workspace_bytes, who, st);
 }

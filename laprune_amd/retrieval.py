@@ -18,6 +18,12 @@ Two selection modes:
     group.
 Every buffer is preallocated so that ``step`` can be captured in a HIP graph
 (``torch.cuda.CUDAGraph``); no step allocates.
+
+Ragged batches: ``step`` also takes one length per sequence (lists for
+``t_codes`` / ``t_total``).  The reference decodes a batch with one shared
+length (aq_evaluation.py:150-155); here every sequence gets the window,
+budget and keep set it would get alone, through per-sequence plans
+(``lap_row_plan``) uploaded to the device before the kernels that read them.
 """
 from __future__ import annotations
 
@@ -82,6 +88,54 @@ def keep_segments(t_total: int, sink: int, local: int) -> tuple[int, int, int]:
     return sb_eff, start, tail_count
 
 
+PLAN_FIELDS = ("t_codes", "t_total", "cand_start", "cand_end", "k", "sink", "tail_start",
+               "tail_count")
+
+
+class PlanBuffer:
+    """Device array of ``lap_row_plan`` [B] written from the host each step.
+
+    Uploads go through a ring of pinned staging buffers; a slot is rewritten
+    only after the copy that last read it has completed (its event), so the
+    host may run ahead of the device."""
+
+    SLOTS = 4
+
+    def __init__(self, batch: int, device: torch.device):
+        self.dev = torch.zeros((batch, len(PLAN_FIELDS)), dtype=torch.int32, device=device)
+        self._host = [torch.zeros((batch, len(PLAN_FIELDS)), dtype=torch.int32).pin_memory()
+                      for _ in range(self.SLOTS)]
+        self._done = [None] * self.SLOTS
+        self._i = 0
+
+    def upload(self, rows: list[tuple[int, ...]]) -> torch.Tensor:
+        i = self._i
+        self._i = (i + 1) % self.SLOTS
+        if self._done[i] is not None:
+            self._done[i].synchronize()
+        h = self._host[i]
+        h.copy_(torch.tensor(rows, dtype=torch.int32))
+        self.dev.copy_(h, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.dev.device))
+        self._done[i] = ev
+        return self.dev
+
+
+def _per_row(v, B: int, name: str) -> list[int] | None:
+    """A per-sequence length argument as a list of B ints (None stays None)."""
+    if v is None:
+        return None
+    if isinstance(v, torch.Tensor):
+        v = v.tolist()
+    if isinstance(v, int):
+        return [v] * B
+    v = [int(x) for x in v]
+    if len(v) != B:
+        raise RuntimeError(f"{name} needs one length per sequence ({B}), got {len(v)}")
+    return v
+
+
 class SparseDecoder:
     """Preallocated single-layer retrieval + sparse attention for one decode step.
 
@@ -129,6 +183,7 @@ class SparseDecoder:
         self.ws_attn = torch.zeros(max(ws_a, 1), dtype=torch.uint8, device=self.dev)  # counters start at 0
         self.key_mode = N.KEY_BF16 if self.cfg.score_dtype == torch.bfloat16 else N.KEY_F16
         self.last_k = 0
+        self._plans = None
 
     def _k_cap(self, t: int) -> int:
         cs, ce = candidate_window(t, t, self.cfg.sink_size, self.cfg.local_window)
@@ -148,6 +203,15 @@ class SparseDecoder:
         return dict(cand_start=cs, cand_end=ce, k=k, sink=sink, tail_start=tail_start,
                     tail_count=tail_count)
 
+    def row_plans(self, t_codes: list[int], t_total: list[int]) -> list[dict]:
+        """One plan per sequence (the uniform plan of each sequence's lengths)."""
+        out = []
+        for tc, tt in zip(t_codes, t_total):
+            p = self.plan(tc, tt)
+            p["k"] = p["k"] if tc > 0 else 0
+            out.append(dict(t_codes=tc, t_total=tt, **p))
+        return out
+
     @torch.no_grad()
     def step(self, q: torch.Tensor, codes: torch.Tensor, keys: torch.Tensor,
              vals: torch.Tensor, t_codes: int | None = None,
@@ -160,8 +224,15 @@ class SparseDecoder:
         if q.dim() == 4:
             q = q[:, :, 0, :]
         B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
-        t_codes = codes.shape[2] if t_codes is None else t_codes
-        t_total = keys.shape[2] if t_total is None else t_total
+        tc_rows = _per_row(t_codes, B, "t_codes")
+        tt_rows = _per_row(t_total, B, "t_total")
+        if (tc_rows is not None and len(set(tc_rows)) > 1) or \
+                (tt_rows is not None and len(set(tt_rows)) > 1):
+            if tc_rows is None or tt_rows is None:
+                raise RuntimeError("ragged steps need both t_codes and t_total per sequence")
+            return self._step_ragged(q, codes, keys, vals, tc_rows, tt_rows)
+        t_codes = codes.shape[2] if tc_rows is None else tc_rows[0]
+        t_total = keys.shape[2] if tt_rows is None else tt_rows[0]
         if t_total > self.T_max or t_codes > t_total:
             raise RuntimeError("cache length exceeds the decoder's max_tokens")
         p = self.plan(t_codes, t_total)
@@ -181,15 +252,14 @@ class SparseDecoder:
                    N.ptr(self.ws_sel), self.ws_sel.numel(), st)
             H_idx = Hkv
         else:
+            # The scorer writes the head scores as [B*Hq][t_codes] rows; the
+            # per-head selection reads them with that row stride.
             sc = self.scores
             N.call("lap_retrieve_topk", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
                    codes.stride(1), codes.stride(2), B, Hkv, t_codes, p["cand_start"],
                    p["cand_end"], 0, self.key_mode, N.ptr(sc), N.ptr(self.idx), N.I32,
                    N.ptr(self.ws_sel), self.ws_sel.numel(), st)
-            # per-head selection over the fp16 head scores (scores row stride = T_max)
-            if B != 1:
-                raise RuntimeError("per-head selection serves batch 1")
-            N.call("lap_topk_select", N.ptr(sc), sc.stride(1), Hq, 1, t_codes, p["cand_start"],
+            N.call("lap_topk_select", N.ptr(sc), t_codes, B * Hq, 1, t_codes, p["cand_start"],
                    p["cand_end"], k, self.key_mode, N.ptr(self.idx), N.I32,
                    N.ptr(self.ws_sel), self.ws_sel.numel(), st)
             H_idx = Hq
@@ -201,16 +271,63 @@ class SparseDecoder:
                scale, N.ptr(self.out), N.ptr(self.ws_attn), self.ws_attn.numel(), st)
         return self.out.unsqueeze(2)
 
+    def _step_ragged(self, q, codes, keys, vals, t_codes: list[int],
+                     t_total: list[int]) -> torch.Tensor:
+        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
+        if max(t_total) > self.T_max or any(c > t for c, t in zip(t_codes, t_total)):
+            raise RuntimeError("cache length exceeds the decoder's max_tokens")
+        if max(t_total) > keys.shape[2] or max(t_codes) > codes.shape[2]:
+            raise RuntimeError("a sequence length exceeds the cache views")
+        plans = self.row_plans(t_codes, t_total)
+        if self._plans is None:
+            self._plans = PlanBuffer(B, self.dev)
+        pdev = self._plans.upload([tuple(p[f] for f in PLAN_FIELDS) for p in plans])
+        st = N.stream_of(q)
+        qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
+        N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
+               N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
+               N.ptr(self.lut), st)
+        k_cols = max(p["k"] for p in plans)
+        T = max(max(t_codes), 1)
+        H_idx = Hkv if self.cfg.select == "group" else Hq
+        if k_cols > 0 and self.cfg.select == "group":
+            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
+                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(pdev), k_cols,
+                   self.key_mode, None, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
+                   self.ws_sel.numel(), st)
+        elif k_cols > 0:
+            sc = self.scores
+            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
+                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(pdev), 0,
+                   self.key_mode, N.ptr(sc), None, N.I32, N.ptr(self.ws_sel),
+                   self.ws_sel.numel(), st)
+            N.call("lap_topk_select_ragged", N.ptr(sc), T, B * Hq, 1, Hq, T, N.ptr(pdev), k_cols,
+                   self.key_mode, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
+                   self.ws_sel.numel(), st)
+        self.last_k = k_cols
+        max_sink = max(p["sink"] for p in plans)
+        max_tail = max(p["tail_count"] for p in plans)
+        N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
+               N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, keys.shape[2], D, keys.stride(0),
+               keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
+               N.ptr(self.idx), N.I32, H_idx, k_cols, N.ptr(pdev), max_sink, max_tail,
+               1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws_attn), self.ws_attn.numel(),
+               st)
+        return self.out.unsqueeze(2)
+
     @torch.no_grad()
     def step_cached(self, q: torch.Tensor, cache) -> torch.Tensor:
         """One decode step over a ``DecodeKVCache``: candidates are the encoded
-        tokens (``encoded_len``), attention covers all ``length`` tokens."""
-        return self.step(q, cache.codes, cache.k, cache.v, t_codes=cache.encoded_len,
-                         t_total=cache.length)
+        tokens of each sequence, attention covers all of its cached tokens."""
+        return self.step(q, cache.codes, cache.k, cache.v, t_codes=cache.encoded_lens,
+                         t_total=cache.lengths)
 
     def selected(self) -> torch.Tensor:
-        """Indices chosen by the last step: [B, rows, k] int32 (ascending)."""
-        return self.idx[:, :, :self.last_k]
+        """Indices chosen by the last step: [B, rows, k] int32 (ascending; in a
+        ragged step, rows past their sequence's k hold -1)."""
+        rows = self.idx.shape[1]
+        n = self.B * rows * self.last_k
+        return self.idx.view(-1)[:n].view(self.B, rows, self.last_k)
 
 
 class DenseDecoder:
@@ -224,13 +341,31 @@ class DenseDecoder:
         ws = N.size_query("lap_attn_decode_workspace_size", batch, num_q_heads, head_dim,
                           max(max_tokens, 1))
         self.ws = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)  # counters start at 0
+        self._plans = None
 
     @torch.no_grad()
-    def step(self, q: torch.Tensor, keys: torch.Tensor, vals: torch.Tensor) -> torch.Tensor:
+    def step(self, q: torch.Tensor, keys: torch.Tensor, vals: torch.Tensor,
+             lengths=None) -> torch.Tensor:
+        """Attention over all cached tokens: keys.shape[2] of them, or
+        ``lengths[b]`` for sequence b (ragged batches)."""
         if q.dim() == 4:
             q = q[:, :, 0, :]
         B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
         T = keys.shape[2]
+        rows = _per_row(lengths, B, "lengths")
+        if rows is not None and (len(set(rows)) > 1 or rows[0] != T):
+            if max(rows) > T or min(rows) < 1:
+                raise RuntimeError("lengths must lie in [1, keys.shape[2]]")
+            if self._plans is None:
+                self._plans = PlanBuffer(B, q.device)
+            pdev = self._plans.upload([(t, t, 0, 0, 0, 0, 0, t) for t in rows])
+            N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1),
+                   N.ptr(keys), N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D,
+                   keys.stride(0), keys.stride(1), keys.stride(2), vals.stride(0),
+                   vals.stride(1), vals.stride(2), None, N.I32, Hkv, 0, N.ptr(pdev), 0,
+                   max(rows), 1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws),
+                   self.ws.numel(), N.stream_of(q))
+            return self.out.unsqueeze(2)
         N.call("lap_dense_attn_decode", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
                N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D, keys.stride(0),
                keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),

@@ -38,7 +38,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.lap_abi_version() == 2
+    assert lib.lap_abi_version() == 3
 
 
 def _err(lib):
@@ -64,6 +64,31 @@ def test_invalid_arguments_return_status_and_message(lib):
     st = lib.lap_sparse_attn_decode(one, 0, 128, one, one, N.BF16, 1, 32, 8, 100, 128, 0, 0, 128,
                                     0, 0, 128, one, N.I32, 5, 10, 0, -1, 0, 1.0, one, None, 0, None)
     assert st == N.LAP_ERR_INVALID and "H_idx" in _err(lib)
+
+
+def test_ragged_entry_points_validate_before_any_device_call(lib):
+    from laprune_amd import _native as N
+    one = C.c_void_p(256)  # never dereferenced: validation fails first
+    st = lib.lap_retrieve_topk_ragged(one, one, 0, 0, 32, 2, 8, 1000, None, 64, N.KEY_F16, None,
+                                      one, N.I32, one, 1 << 30, None)
+    assert st == N.LAP_ERR_INVALID and "null plans" in _err(lib)
+    st = lib.lap_retrieve_topk_ragged(one, one, 0, 0, 32, 2, 8, 1000, one, 64, N.KEY_F16, None,
+                                      one, N.F32, one, 1 << 30, None)
+    assert st == N.LAP_ERR_INVALID and "int32/int64" in _err(lib)
+    st = lib.lap_topk_select_ragged(one, 1000, 10, 1, 4, 1000, one, 64, N.KEY_F16, one, N.I32,
+                                    one, 1 << 30, None)
+    assert st == N.LAP_ERR_INVALID and "rows_per_plan" in _err(lib)
+    st = lib.lap_topk_select_ragged(one, 999, 8, 1, 4, 1000, one, 64, N.KEY_F16, one, N.I32,
+                                    one, 1 << 30, None)
+    assert st == N.LAP_ERR_INVALID and "row stride" in _err(lib)
+    st = lib.lap_sparse_attn_decode_ragged(one, 0, 128, one, one, N.BF16, 2, 32, 8, 100, 128, 0,
+                                           0, 128, 0, 0, 128, one, N.I32, 8, 10, None, 4, 64,
+                                           1.0, one, None, 0, None)
+    assert st == N.LAP_ERR_INVALID and "null plans" in _err(lib)
+    st = lib.lap_sparse_attn_decode_ragged(one, 0, 128, one, one, N.BF16, 2, 32, 8, 100, 128, 0,
+                                           0, 128, 0, 0, 128, one, N.I32, 8, 10, one, -1, 64,
+                                           1.0, one, None, 0, None)
+    assert st == N.LAP_ERR_INVALID and "negative" in _err(lib)
 
 
 def test_workspace_size_queries(lib):

@@ -86,3 +86,23 @@ def test_grown_capacity():
     assert KC.grown_capacity(16, 17) == 32
     assert KC.grown_capacity(16, 100) == 100
     assert KC.grown_capacity(1024, 1025) == 2048
+
+
+def test_per_row_lengths_argument():
+    from laprune_amd.retrieval import _per_row
+    assert _per_row(None, 3, "x") is None
+    assert _per_row(7, 3, "x") == [7, 7, 7]
+    assert _per_row((1, 2, 3), 3, "x") == [1, 2, 3]
+    with pytest.raises(RuntimeError, match="one length per sequence"):
+        _per_row([1, 2], 3, "x")
+
+
+def test_plan_fields_match_the_c_struct():
+    """PLAN_FIELDS is the field order of lap_row_plan in include/laprune_hip.h."""
+    import re
+    from pathlib import Path
+    from laprune_amd.retrieval import PLAN_FIELDS
+    text = (Path(__file__).resolve().parent.parent / "include" / "laprune_hip.h").read_text()
+    body = re.search(r"typedef struct lap_row_plan \{(.*?)\} lap_row_plan;", text, re.S).group(1)
+    fields = re.findall(r"(\w+)\s*[,;]", body)
+    assert tuple(fields) == PLAN_FIELDS
