@@ -26,6 +26,11 @@ so that the 256 MB Infinity Cache cannot serve the step from cache.
                  post-RoPE keys (8 KV heads x 64 tokens = 512 rows, 32x256
                  codebooks), MFMA coarse search + exact recheck, next to the
                  reference's fp32 greedy path on the host cores.
+``ragged``       one attention layer of configs[4] (C5): batch 16, per-sequence
+                 lengths uniform in [16384, 32768] (seeded), top-1024 per KV
+                 group + 4 sink + 64 local, the newest < 64 keys of each
+                 sequence not yet encoded; sparse step (per-sequence plans) vs
+                 the dense decode of each sequence over its own length.
 """
 from __future__ import annotations
 
@@ -50,6 +55,7 @@ CODE_BYTES = HKV * T * M  # 33,554,432 algorithmic bytes per scorer launch
 CALIB_BYTES = 256 << 20   # copy-like calibration kernel: bytes read (= bytes written)
 ENC_TOKENS, ENC_POS0, ROPE_THETA = 64, 131008, 500000.0
 ENC_FLOP = 2 * HKV * ENC_TOKENS * M * K * D  # 1,073,741,824 dot-product flops per flush
+RAG_B, RAG_T0, RAG_T1, RAG_TOPK, RAG_SETS = 16, 16384, 32768, 1024, 2
 
 
 def log(*a):
@@ -65,6 +71,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget for the CPU baseline sample")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the C5 ragged-batch leg")
+    ap.add_argument("--only-ragged", action="store_true",
+                    help="run only the C5 ragged-batch leg (for profiling); prints its JSON")
     ap.add_argument("--counters", action="store_true",
                     help="counter-collection pass: eager scorer launches over the rotating "
                          "code sets, then a 256 MiB copy-like kernel (fp32 negate) that "
@@ -160,6 +169,91 @@ def traffic_from_profile() -> dict | None:
         return None
 
 
+def ragged_leg(args, dev, cb) -> dict:
+    """One C5 attention layer: sparse ragged step vs per-sequence dense decode."""
+    import torch
+    from laprune_amd.retrieval import DenseDecoder, RetrievalConfig, SparseDecoder
+    g = torch.Generator(device="cpu").manual_seed(5)  # same lengths in every mode
+    lens = torch.randint(RAG_T0, RAG_T1 + 1, (RAG_B,), generator=g).tolist()
+    t_codes = [t - (t % 64) for t in lens]  # the encode buffer holds t % 64 keys
+    cap = RAG_T1 + 64
+    log(f"ragged leg: lengths {min(lens)}..{max(lens)}, {RAG_SETS} input sets")
+    sets = []
+    for _ in range(RAG_SETS):
+        codes = torch.randint(0, 256, (RAG_B, HKV, cap, M), generator=g,
+                              dtype=torch.uint8).to(dev)
+        kk = torch.randn(RAG_B, HKV, cap, D, dtype=torch.bfloat16, device=dev)
+        vv = torch.randn(RAG_B, HKV, cap, D, dtype=torch.bfloat16, device=dev)
+        q = torch.randn(RAG_B, HQ, 1, D, generator=g).bfloat16().to(dev)
+        sets.append((q, codes, kk, vv))
+    cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=RAG_TOPK, select="group",
+                          score_dtype=torch.bfloat16)
+    dec = SparseDecoder(cb, RAG_B, HQ, HKV, D, cap, cfg)
+    dense = DenseDecoder(RAG_B, HQ, HKV, D, cap, dev)
+
+    def sparse(i):
+        q, c, kk, vv = sets[i % RAG_SETS]
+        return dec.step(q, c, kk, vv, t_codes=t_codes, t_total=lens)
+
+    def dense_(i):
+        q, _, kk, vv = sets[i % RAG_SETS]
+        return dense.step(q, kk, vv, lengths=lens)
+
+    for i in range(4):
+        sparse(i)
+        dense_(i)
+    torch.cuda.synchronize()
+    sel = dec.selected()
+    ok = bool(sel.shape[-1] == RAG_TOPK and int(sel.min()) >= SINK
+              and int((sel < 0).sum()) == 0)
+    if args.eager:
+        run_s, run_d = sparse, dense_
+    else:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(2):
+                sparse(i)
+                dense_(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        sg, dg = [], []
+        for j in range(RAG_SETS):
+            for fn, lst in ((sparse, sg), (dense_, dg)):
+                gph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gph):
+                    fn(j)
+                lst.append(gph)
+        run_s = lambda i: sg[i % RAG_SETS].replay()  # noqa: E731
+        run_d = lambda i: dg[i % RAG_SETS].replay()  # noqa: E731
+    for i in range(args.warmup):
+        run_s(i)
+        run_d(i)
+    torch.cuda.synchronize()
+    out = {}
+    for name, fn in (("sparse", run_s), ("dense", run_d)):
+        log(f"timing {args.steps} ragged {name} steps")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            fn(i)
+        torch.cuda.synchronize()
+        out[name] = (time.perf_counter() - t0) / args.steps
+    kv_bytes = sum(lens) * HKV * D * 2 * 2
+    return {
+        "workload": ("C5 layer: batch 16, context lengths uniform in [16384, 32768] (seeded), "
+                     "32 q / 8 kv heads, head_dim 128, top-1024 per KV group + 4 sink + 64 "
+                     "local; codes for all but the newest len % 64 keys; bf16 K/V"),
+        "lengths": lens,
+        "sparse_step_us": round(out["sparse"] * 1e6, 2),
+        "dense_step_us": round(out["dense"] * 1e6, 2),
+        "speedup_vs_dense": round(out["dense"] / out["sparse"], 3),
+        "dense_hbm_gbs": round(kv_bytes / out["dense"] / 1e9, 1),
+        "score_code_bytes": sum(t_codes) * HKV * M,
+        "selection_check": ok,
+    }
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -179,6 +273,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     g = torch.Generator(device="cpu").manual_seed(0)
+    if args.only_ragged:
+        cb = (torch.randn(M, K, D, generator=g) * 0.02).to(dev)
+        print(json.dumps({"ragged": ragged_leg(args, dev, cb)}), flush=True)
+        return
     log("allocating inputs")
     codes_sets = [torch.randint(0, 256, (1, HKV, T + CAP, M), generator=g,
                                 dtype=torch.uint8).to(dev) for _ in range(N_CODE_SETS)]
@@ -391,6 +489,8 @@ def main():
             "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
         },
     }
+    if not args.no_ragged:
+        result["ragged"] = ragged_leg(args, dev, cb)
     if not args.no_cpu_baseline:
         log("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -6,18 +6,30 @@
 // (the order the CPU oracle restates).  The reference forms this LUT with a
 // vendor GEMM (laprune/llm/aq_kv.py:681-682) or an fp32 einsum (:620).
 //
-// Work shape: one lane per codebook row (row = m*K + k), four query heads per
-// wave, 64 rows x 16 heads per workgroup (1024 waves at Hq = 32, M*K = 8192).
-// The interleaved layout [Hq/G][M][K][G] is written directly so the scorer can
-// fill its LDS table with a linear copy.
+// Work shape: a workgroup owns a tile of 32 codebook rows (row = m*K + k) x
+// 8*HPT query heads; thread t runs HPT independent fmaf chains, row t % 32
+// against heads (t / 32) * HPT + j.  The 32 rows are one contiguous block of
+// the [M*K][D] codebook, staged in LDS as fp32 with coalesced loads.  The
+// chains need one codebook value and HPT query values per step; where the
+// query values come from decides the cost:
+//   * lut_dpp_kernel (D = 64 or 128): lane l keeps q[h][64 b + 4 (l % 16) + e]
+//     in four VGPRs per 64-wide block b (one 8-byte load), and every FMA
+//     takes its query operand through DPP row_newbcast:n (lane n of the
+//     lane's 16-lane row), so LDS serves only the codebook: one ds_read_b128
+//     per 4*HPT FMAs.
+//   * lut_tile_kernel (any D): the query tile sits in LDS too and is read as
+//     16-byte broadcasts, which makes the chains LDS-bound.
+// The interleaved layout [Hq/G][M][K][G] is written directly (8 contiguous
+// bytes per row and KV group) so the scorer can fill its LDS table with a
+// linear copy.
 #include "common.h"
 
 namespace lap {
 namespace {
 
-constexpr int kRows = 64;        // codebook rows per workgroup (one per lane)
-constexpr int kHeadsPerWG = 16;  // query heads per workgroup (4 per wave)
+constexpr int kTileRows = 32;    // codebook rows per workgroup
 constexpr int kThreads = 256;
+constexpr int kHeadGroups = kThreads / kTileRows;  // 8
 
 // Load 4 consecutive elements of dtype DT at element offset i as fp32.
 template <int DT>
@@ -29,93 +41,311 @@ __device__ __forceinline__ float4 load4(const void* p, int64_t i) {
   return make_float4(bf2f(w.x & 0xffffu), bf2f(w.x >> 16), bf2f(w.y & 0xffffu), bf2f(w.y >> 16));
 }
 
-// Workgroup = 64 codebook rows x 16 query heads; wave w owns heads
-// head0 + 4w .. head0 + 4w + 3 and lane l owns row row0 + l, so each lane runs
-// four independent fmaf chains over d.  The query slice is staged once in LDS
-// as fp32 and read as wave-wide broadcasts (one address per instruction, no
-// bank conflicts); the codebook row is read straight from L1/L2.
-template <int QDT, int CDT>
-__global__ __launch_bounds__(kThreads) void lut_build_kernel(
+// Codebook rows sit in LDS with a row pitch of D + 4 floats: a 16-lane pass
+// of ds_read_b128 over 16 consecutive rows then covers 64 distinct banks.
+__host__ __device__ constexpr int c_pitch(int D) { return D + 4; }
+
+// Stage the tile's 32 codebook rows in LDS.  Every load is issued before the
+// first LDS write (at most 8 float4 per thread for D <= 256), unconditionally
+// with clamped indices so that the compiler keeps them all in flight.
+template <int CDT>
+__device__ __forceinline__ void stage_rows(const void* __restrict__ cb, int D, int MK, int row0,
+                                           float* s_c) {
+  constexpr int kC = kTileRows * 64 / kThreads;
+  const int D4 = D / 4, P = c_pitch(D), nC = kTileRows * D4;
+  const int tid = threadIdx.x;
+  float4 vc[kC];
+#pragma unroll
+  for (int j = 0; j < kC; ++j) {
+    const int i = min(tid + j * kThreads, nC - 1);
+    const int r = i / D4, d = (i - r * D4) * 4;
+    vc[j] = load4<CDT>(cb, (int64_t)min(row0 + r, MK - 1) * D + d);
+  }
+#pragma unroll
+  for (int j = 0; j < kC; ++j) {
+    const int i = tid + j * kThreads;
+    const int r = i / D4, d = (i - r * D4) * 4;
+    if (i < nC) *reinterpret_cast<float4*>(s_c + r * P + d) = vc[j];
+  }
+}
+
+// Write the thread's HPT results for one row (heads h0 .. h0 + HPT - 1).
+template <int HPT>
+__device__ __forceinline__ void write_row(const float (&acc)[HPT], int h0, int row, int Hq,
+                                          int MK, int G, int layout, uint16_t* __restrict__ out) {
+#pragma unroll
+  for (int j0 = 0; j0 < HPT; j0 += 4) {
+    const int h = h0 + j0;
+    if (layout == LAP_LUT_GMKG && G == 4 && h + 3 < Hq) {
+      // the four heads of one KV group: 8 contiguous bytes; 32 lanes write
+      // 256 contiguous bytes
+      const uint32_t w0 = (uint32_t)f2h(acc[j0]) | ((uint32_t)f2h(acc[j0 + 1]) << 16);
+      const uint32_t w1 = (uint32_t)f2h(acc[j0 + 2]) | ((uint32_t)f2h(acc[j0 + 3]) << 16);
+      *reinterpret_cast<uint2*>(out + ((int64_t)(h >> 2) * MK + row) * 4) = make_uint2(w0, w1);
+      continue;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int head = h + j;
+      if (head >= Hq) continue;
+      int64_t idx;
+      if (layout == LAP_LUT_HMK) idx = (int64_t)head * MK + row;
+      else idx = ((int64_t)(head / G) * MK + row) * G + (head % G);
+      out[idx] = f2h(acc[j0 + j]);
+    }
+  }
+}
+
+// Sixteen steps of one chain, d = 64 B + 4 n + e for n = N0..N0+3, e = 0..3
+// (ascending d):  acc = fmaf(q[h][d], c[d], acc).  Lane l holds
+// q[h][64 B + 4 (l % 16) + e] in qv[e], so q[h][d] is lane n of the lane's
+// 16-lane row of qv[e] (DPP row_newbcast:n).  A DPP source VGPR written by a
+// VALU instruction needs two wait states before it is read; the leading s_nop
+// covers that for qv, and nothing inside the block writes qv.
+#define LAP_FMA_DPP(N, E, C) \
+  "v_fmac_f32_dpp %0, %" #E ", %" #C " row_newbcast:" #N " row_mask:0xf bank_mask:0xf\n\t"
+#define LAP_FMA16(N0, N1, N2, N3)                                                           \
+  template <>                                                                              \
+  __device__ __forceinline__ void fma16_bcast<N0>(float& acc, const float(&qv)[4],         \
+                                                  const float4& c0, const float4& c1,      \
+                                                  const float4& c2, const float4& c3) {    \
+    asm("s_nop 1\n\t"                                                                      \
+        LAP_FMA_DPP(N0, 1, 5) LAP_FMA_DPP(N0, 2, 6) LAP_FMA_DPP(N0, 3, 7) LAP_FMA_DPP(N0, 4, 8) \
+        LAP_FMA_DPP(N1, 1, 9) LAP_FMA_DPP(N1, 2, 10) LAP_FMA_DPP(N1, 3, 11)                  \
+        LAP_FMA_DPP(N1, 4, 12) LAP_FMA_DPP(N2, 1, 13) LAP_FMA_DPP(N2, 2, 14)                 \
+        LAP_FMA_DPP(N2, 3, 15) LAP_FMA_DPP(N2, 4, 16) LAP_FMA_DPP(N3, 1, 17)                 \
+        LAP_FMA_DPP(N3, 2, 18) LAP_FMA_DPP(N3, 3, 19) LAP_FMA_DPP(N3, 4, 20)                 \
+        : "+v"(acc)                                                                        \
+        : "v"(qv[0]), "v"(qv[1]), "v"(qv[2]), "v"(qv[3]), "v"(c0.x), "v"(c0.y), "v"(c0.z),  \
+          "v"(c0.w), "v"(c1.x), "v"(c1.y), "v"(c1.z), "v"(c1.w), "v"(c2.x), "v"(c2.y),      \
+          "v"(c2.z), "v"(c2.w), "v"(c3.x), "v"(c3.y), "v"(c3.z), "v"(c3.w));                 \
+  }
+template <int N0>
+__device__ __forceinline__ void fma16_bcast(float& acc, const float (&qv)[4], const float4& c0,
+                                            const float4& c1, const float4& c2,
+                                            const float4& c3);
+LAP_FMA16(0, 1, 2, 3)
+LAP_FMA16(4, 5, 6, 7)
+LAP_FMA16(8, 9, 10, 11)
+LAP_FMA16(12, 13, 14, 15)
+#undef LAP_FMA16
+#undef LAP_FMA_DPP
+
+// Workgroup -> (head tile, first row tile).  A workgroup computes `tpw`
+// consecutive row tiles with the same heads: its query values are loaded once
+// and the next tile's codebook rows are fetched while the current one is
+// computed.  Workgroups are dispatched to the eight XCDs round-robin
+// (workgroup i to XCD i % 8) and each XCD has its own L2, so XCD x takes a
+// contiguous range of work units with all head tiles of a row group back to
+// back: every codebook row is then fetched into one L2 only.
+struct TileId {
+  int row_tile, head_tile;
+};
+__device__ __forceinline__ TileId tile_of(int wg, int n_wg, int head_tiles, int tpw) {
+  constexpr int kXcds = 8;
+  const int u = n_wg % kXcds == 0 ? (wg % kXcds) * (n_wg / kXcds) + wg / kXcds : wg;
+  return TileId{(u / head_tiles) * tpw, u % head_tiles};
+}
+
+// Issue the loads of one tile's 32 codebook rows (at most 8 float4 per
+// thread for D <= 256), unconditionally with clamped indices so that the
+// compiler keeps them all in flight; rows_to_lds writes them.
+template <int CDT, int D>
+__device__ __forceinline__ void rows_load(const void* __restrict__ cb, int MK, int row0,
+                                          float4 (&vc)[kTileRows * D / 4 / kThreads]) {
+  constexpr int D4 = D / 4, kC = kTileRows * D4 / kThreads;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < kC; ++j) {
+    const int i = tid + j * kThreads;
+    const int r = i / D4, d = (i - r * D4) * 4;
+    vc[j] = load4<CDT>(cb, (int64_t)min(row0 + r, MK - 1) * D + d);
+  }
+}
+template <int D>
+__device__ __forceinline__ void rows_to_lds(const float4 (&vc)[kTileRows * D / 4 / kThreads],
+                                            float* s_c) {
+  constexpr int D4 = D / 4, kC = kTileRows * D4 / kThreads;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < kC; ++j) {
+    const int i = tid + j * kThreads;
+    const int r = i / D4, d = (i - r * D4) * 4;
+    *reinterpret_cast<float4*>(s_c + r * c_pitch(D) + d) = vc[j];
+  }
+}
+
+template <int QDT, int CDT, int HPT, int D>
+__global__ __launch_bounds__(kThreads) void lut_dpp_kernel(
+    const void* __restrict__ q, int64_t q_row_stride,
+    const void* __restrict__ cb, int Hq, int MK, int G, int layout,
+    uint16_t* __restrict__ out, int head_tiles, int tpw) {
+  static_assert(HPT % 4 == 0 && D % 64 == 0 && D <= 256, "bad shape");
+  constexpr int NB = D / 64;
+  constexpr int P = c_pitch(D);
+  __shared__ __attribute__((aligned(16))) float s_c[kTileRows * P];
+  const int tid = threadIdx.x;
+  const TileId ti = tile_of(blockIdx.x, gridDim.x, head_tiles, tpw);
+  const int h0 = ti.head_tile * (kHeadGroups * HPT) + (tid / kTileRows) * HPT;
+  const int row_tiles = (MK + kTileRows - 1) / kTileRows;
+  const int n_tiles = min(tpw, row_tiles - ti.row_tile);
+
+  float4 vc[kTileRows * D / 4 / kThreads];
+  rows_load<CDT, D>(cb, MK, ti.row_tile * kTileRows, vc);
+  // This lane's query values: qv[j][B][e] = q[h0 + j][64 B + 4 (lane % 16) + e]
+  // (heads past Hq read the last head; their results are not written).
+  float qv[HPT][NB][4];
+  const int n = tid & 15;
+#pragma unroll
+  for (int j = 0; j < HPT; ++j) {
+    const int64_t base = (int64_t)min(h0 + j, Hq - 1) * q_row_stride + 4 * n;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float4 v = load4<QDT>(q, base + 64 * b);
+      qv[j][b][0] = v.x;
+      qv[j][b][1] = v.y;
+      qv[j][b][2] = v.z;
+      qv[j][b][3] = v.w;
+    }
+  }
+  rows_to_lds<D>(vc, s_c);
+
+  const float* cr = s_c + (tid % kTileRows) * P;
+  for (int t = 0; t < n_tiles; ++t) {
+    __syncthreads();  // tile t is in LDS
+    const int row0 = (ti.row_tile + t) * kTileRows;
+    if (t + 1 < n_tiles) rows_load<CDT, D>(cb, MK, row0 + kTileRows, vc);
+    float acc[HPT];
+#pragma unroll
+    for (int j = 0; j < HPT; ++j) acc[j] = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {  // d = 64 b + 16 g .. + 15
+        const float* cp = cr + 64 * b + 16 * g;
+        const float4 c0 = *reinterpret_cast<const float4*>(cp);
+        const float4 c1 = *reinterpret_cast<const float4*>(cp + 4);
+        const float4 c2 = *reinterpret_cast<const float4*>(cp + 8);
+        const float4 c3 = *reinterpret_cast<const float4*>(cp + 12);
+#pragma unroll
+        for (int j = 0; j < HPT; ++j) {
+          if (g == 0) fma16_bcast<0>(acc[j], qv[j][b], c0, c1, c2, c3);
+          else if (g == 1) fma16_bcast<4>(acc[j], qv[j][b], c0, c1, c2, c3);
+          else if (g == 2) fma16_bcast<8>(acc[j], qv[j][b], c0, c1, c2, c3);
+          else fma16_bcast<12>(acc[j], qv[j][b], c0, c1, c2, c3);
+        }
+      }
+    }
+    const int row = row0 + tid % kTileRows;
+    if (row < MK) write_row<HPT>(acc, h0, row, Hq, MK, G, layout, out);
+    if (t + 1 < n_tiles) {
+      __syncthreads();  // every read of tile t is done
+      rows_to_lds<D>(vc, s_c);
+    }
+  }
+}
+
+template <int QDT, int CDT, int HPT>
+__global__ __launch_bounds__(kThreads) void lut_tile_kernel(
     const void* __restrict__ q, int64_t q_row_stride,
     const void* __restrict__ cb, int Hq, int D, int MK, int G, int layout,
     uint16_t* __restrict__ out) {
-  extern __shared__ __attribute__((aligned(16))) float s_q[];  // [16][D]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row0 = blockIdx.x * kRows;
-  const int head0 = blockIdx.y * kHeadsPerWG;
+  static_assert(HPT % 4 == 0, "heads per thread must be a multiple of 4");
+  constexpr int TH = kHeadGroups * HPT;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int P = c_pitch(D);
+  float* s_c = smem;                   // [32][P]
+  float* s_q = smem + kTileRows * P;   // [TH][D]
+  const int tid = threadIdx.x;
+  const int row0 = blockIdx.x * kTileRows;
+  const int head0 = blockIdx.y * TH;
   const int D4 = D / 4;
 
-  for (int i = tid; i < kHeadsPerWG * D4; i += kThreads) {
+  for (int i = tid; i < TH * D4; i += kThreads) {
     const int h = i / D4, d = (i - h * D4) * 4;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (head0 + h < Hq) v = load4<QDT>(q, (int64_t)(head0 + h) * q_row_stride + d);
     *reinterpret_cast<float4*>(s_q + h * D + d) = v;
   }
+  stage_rows<CDT>(cb, D, MK, row0, s_c);
   __syncthreads();
 
-  const int row = row0 + lane;
-  const int rowc = row < MK ? row : MK - 1;  // clamped for the loads
-  const float* qw = s_q + (4 * wave) * D;
-  float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+  const int hg = tid / kTileRows;
+  const float* cr = s_c + (tid % kTileRows) * P;
+  const float* qh = s_q + hg * HPT * D;
+  float acc[HPT];
+#pragma unroll
+  for (int j = 0; j < HPT; ++j) acc[j] = 0.f;
 #pragma unroll 4
   for (int d = 0; d < D; d += 4) {
-    const float4 c = load4<CDT>(cb, (int64_t)rowc * D + d);
-    const float4 q0 = *reinterpret_cast<const float4*>(qw + d);
-    const float4 q1 = *reinterpret_cast<const float4*>(qw + D + d);
-    const float4 q2 = *reinterpret_cast<const float4*>(qw + 2 * D + d);
-    const float4 q3 = *reinterpret_cast<const float4*>(qw + 3 * D + d);
-    acc0 = __builtin_fmaf(q0.x, c.x, acc0);
-    acc1 = __builtin_fmaf(q1.x, c.x, acc1);
-    acc2 = __builtin_fmaf(q2.x, c.x, acc2);
-    acc3 = __builtin_fmaf(q3.x, c.x, acc3);
-    acc0 = __builtin_fmaf(q0.y, c.y, acc0);
-    acc1 = __builtin_fmaf(q1.y, c.y, acc1);
-    acc2 = __builtin_fmaf(q2.y, c.y, acc2);
-    acc3 = __builtin_fmaf(q3.y, c.y, acc3);
-    acc0 = __builtin_fmaf(q0.z, c.z, acc0);
-    acc1 = __builtin_fmaf(q1.z, c.z, acc1);
-    acc2 = __builtin_fmaf(q2.z, c.z, acc2);
-    acc3 = __builtin_fmaf(q3.z, c.z, acc3);
-    acc0 = __builtin_fmaf(q0.w, c.w, acc0);
-    acc1 = __builtin_fmaf(q1.w, c.w, acc1);
-    acc2 = __builtin_fmaf(q2.w, c.w, acc2);
-    acc3 = __builtin_fmaf(q3.w, c.w, acc3);
-  }
-  if (row >= MK) return;
-  const int headA = head0 + 4 * wave;
-  const float acc[4] = {acc0, acc1, acc2, acc3};
-  if (layout == LAP_LUT_GMKG && G == 4 && headA + 3 < Hq) {
-    // The four heads of one KV group for this row: 8 contiguous bytes; a
-    // wave writes 512 contiguous bytes.
-    const uint32_t w0 = (uint32_t)f2h(acc0) | ((uint32_t)f2h(acc1) << 16);
-    const uint32_t w1 = (uint32_t)f2h(acc2) | ((uint32_t)f2h(acc3) << 16);
-    *reinterpret_cast<uint2*>(out + ((int64_t)(headA >> 2) * MK + row) * 4) = make_uint2(w0, w1);
-    return;
-  }
+    const float4 c = *reinterpret_cast<const float4*>(cr + d);
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    const int head = headA + h;
-    if (head >= Hq) continue;
-    int64_t idx;
-    if (layout == LAP_LUT_HMK) idx = (int64_t)head * MK + row;
-    else idx = ((int64_t)(head / G) * MK + row) * G + (head % G);
-    out[idx] = f2h(acc[h]);
+    for (int j = 0; j < HPT; ++j) {
+      const float4 qq = *reinterpret_cast<const float4*>(qh + j * D + d);
+      acc[j] = __builtin_fmaf(qq.x, c.x, acc[j]);
+      acc[j] = __builtin_fmaf(qq.y, c.y, acc[j]);
+      acc[j] = __builtin_fmaf(qq.z, c.z, acc[j]);
+      acc[j] = __builtin_fmaf(qq.w, c.w, acc[j]);
+    }
   }
+  const int row = row0 + tid % kTileRows;
+  if (row < MK) write_row<HPT>(acc, head0 + hg * HPT, row, Hq, MK, G, layout, out);
 }
 
-size_t lut_smem_bytes(int D) { return (size_t)kHeadsPerWG * D * sizeof(float); }
+size_t lut_tile_smem_bytes(int D) {
+  return ((size_t)kTileRows * c_pitch(D) + (size_t)kHeadGroups * 4 * D) * sizeof(float);
+}
+
+// Heads per thread: 8 when there are enough heads to give every CU several
+// tiles (batched decode), else 4 (batch 1 at Hq = 32: 256 tiles).
+int lut_heads_per_thread(int Hq, int MK, const DevInfo& di) {
+  const int64_t tiles = (int64_t)(MK + kTileRows - 1) / kTileRows;
+  return tiles * ((Hq + 8 * kHeadGroups - 1) / (8 * kHeadGroups)) >= 4 * di.cu_count ? 8 : 4;
+}
+
+// Row tiles per workgroup: enough workgroups for four per CU, the rest as
+// consecutive tiles of one workgroup.  LAPRUNE_LUT_TPW overrides it.
+int lut_tiles_per_wg(int Hq, int MK, int hpt, const DevInfo& di) {
+  static const int forced = [] {
+    const char* e = getenv("LAPRUNE_LUT_TPW");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced > 0) return forced;
+  const int64_t tiles = (int64_t)((MK + kTileRows - 1) / kTileRows) *
+                        ((Hq + hpt * kHeadGroups - 1) / (hpt * kHeadGroups));
+  const int64_t t = tiles / (4 * (int64_t)di.cu_count);
+  return t < 1 ? 1 : (int)t;
+}
+
+template <int QDT, int CDT, int HPT>
+void launch_hpt(const void* q, int64_t qs, const void* cb, int Hq, int D, int MK, int G,
+                int layout, uint16_t* out, int tpw, hipStream_t st) {
+  const int row_tiles = (MK + kTileRows - 1) / kTileRows;
+  const int head_tiles = (Hq + kHeadGroups * HPT - 1) / (kHeadGroups * HPT);
+  const int groups = (row_tiles + tpw - 1) / tpw;
+  const dim3 grid((unsigned)(groups * head_tiles));
+  if (D == 128)
+    hipLaunchKernelGGL((lut_dpp_kernel<QDT, CDT, HPT, 128>), grid, dim3(kThreads), 0, st, q, qs,
+                       cb, Hq, MK, G, layout, out, head_tiles, tpw);
+  else if (D == 64)
+    hipLaunchKernelGGL((lut_dpp_kernel<QDT, CDT, HPT, 64>), grid, dim3(kThreads), 0, st, q, qs,
+                       cb, Hq, MK, G, layout, out, head_tiles, tpw);
+  else
+    hipLaunchKernelGGL((lut_tile_kernel<QDT, CDT, 4>), dim3(row_tiles, (Hq + 31) / 32),
+                       dim3(kThreads), lut_tile_smem_bytes(D), st, q, qs, cb, Hq, D, MK, G,
+                       layout, out);
+}
 
 template <int QDT>
-hipError_t launch_lut(const void* q, int64_t qs, const void* cb, int cb_dtype, int Hq,
-                      int D, int MK, int G, int layout, uint16_t* out, hipStream_t st) {
-  dim3 grid((MK + kRows - 1) / kRows, (Hq + kHeadsPerWG - 1) / kHeadsPerWG);
-  const size_t smem = lut_smem_bytes(D);
+hipError_t launch_lut(const void* q, int64_t qs, const void* cb, int cb_dtype, int Hq, int D,
+                      int MK, int G, int layout, uint16_t* out, int hpt, int tpw,
+                      hipStream_t st) {
   if (cb_dtype == LAP_DTYPE_F32) {
-    hipLaunchKernelGGL((lut_build_kernel<QDT, LAP_DTYPE_F32>), grid, dim3(kThreads), smem, st,
-                       q, qs, cb, Hq, D, MK, G, layout, out);
+    if (hpt == 8) launch_hpt<QDT, LAP_DTYPE_F32, 8>(q, qs, cb, Hq, D, MK, G, layout, out, tpw, st);
+    else launch_hpt<QDT, LAP_DTYPE_F32, 4>(q, qs, cb, Hq, D, MK, G, layout, out, tpw, st);
   } else {
-    hipLaunchKernelGGL((lut_build_kernel<QDT, LAP_DTYPE_F16>), grid, dim3(kThreads), smem, st,
-                       q, qs, cb, Hq, D, MK, G, layout, out);
+    if (hpt == 8) launch_hpt<QDT, LAP_DTYPE_F16, 8>(q, qs, cb, Hq, D, MK, G, layout, out, tpw, st);
+    else launch_hpt<QDT, LAP_DTYPE_F16, 4>(q, qs, cb, Hq, D, MK, G, layout, out, tpw, st);
   }
   return hipGetLastError();
 }
@@ -144,22 +374,27 @@ extern "C" int lap_lut_build(const void* q, int q_dtype, int64_t q_row_stride,
   DevInfo di;
   int ds = device_info(&di);
   if (ds != LAP_OK) return ds;
-  const size_t smem = lut_smem_bytes(D);
+  const size_t smem = lut_tile_smem_bytes(D);
   LAP_CHECK_CODE(smem <= (size_t)di.lds_per_block, LAP_ERR_UNSUPPORTED,
                  "lap_lut_build: D=%d needs %zu bytes of LDS", D, smem);
-  hipError_t e;
   const int MK = M * K;
+  const int hpt = lut_heads_per_thread(Hq, MK, di);
+  const int tpw = lut_tiles_per_wg(Hq, MK, hpt, di);
+  hipError_t e;
   uint16_t* out = static_cast<uint16_t*>(lut_out);
   hipStream_t st = as_stream(stream);
   switch (q_dtype) {
     case LAP_DTYPE_F32:
-      e = launch_lut<LAP_DTYPE_F32>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout, out, st);
+      e = launch_lut<LAP_DTYPE_F32>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout,
+                                    out, hpt, tpw, st);
       break;
     case LAP_DTYPE_F16:
-      e = launch_lut<LAP_DTYPE_F16>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout, out, st);
+      e = launch_lut<LAP_DTYPE_F16>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout,
+                                    out, hpt, tpw, st);
       break;
     default:
-      e = launch_lut<LAP_DTYPE_BF16>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout, out, st);
+      e = launch_lut<LAP_DTYPE_BF16>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout,
+                                     out, hpt, tpw, st);
       break;
   }
   LAP_HIP(e, "lap_lut_build launch");

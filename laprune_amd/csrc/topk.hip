@@ -18,6 +18,9 @@
 // No atomics touch global memory and nothing needs zero-initialised scratch.
 #include "common.h"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace lap {
 
 int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int64_t cs_b,
@@ -345,6 +348,186 @@ int run_levels(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int 
   return LAP_OK;
 }
 
+// ---- One workgroup per row: level 2 and the compaction in one launch.
+//
+// The row's keys stay in registers (thread t owns columns [t*KPT, (t+1)*KPT),
+// KPT <= 128, so up to 131072 columns), the level-1 histogram is the sum of
+// the scorer's chunk histograms, the level-2 histogram is built from the
+// registers, and the ordered compaction is two block-wide scans.  Same
+// result as run_levels (threshold tau, then the `need` lowest-column ties).
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / 64;
+
+// Exclusive prefix sum over the 1024 threads of the block; *total = sum.
+__device__ __forceinline__ uint32_t row_exclusive_scan(uint32_t x, uint32_t* s_wsum,
+                                                       uint32_t* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t inc = x;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += y;
+  }
+  if (lane == 63) s_wsum[wave] = inc;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) {
+    const uint32_t v = s_wsum[w];
+    before += w < wave ? v : 0u;
+    all += v;
+  }
+  __syncthreads();
+  *total = all;
+  return before + inc - x;
+}
+
+// select_bin for a 1024-thread block: threads 0..255 scan, all synchronise.
+__device__ void row_select_bin(const uint32_t* s_h, uint32_t target, uint32_t* s_wsum,
+                               uint32_t* s_res) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t x = tid < 256 ? s_h[255 - tid] : 0u;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (tid < 256 && lane == 63) s_wsum[wave] = x;
+  __syncthreads();
+  if (tid < 256) {
+    uint32_t add = 0;
+    for (int w = 0; w < wave; ++w) add += s_wsum[w];
+    const uint32_t S_i = x + add;                  // S(255 - tid)
+    const uint32_t S_next = S_i - s_h[255 - tid];  // S(256 - tid)
+    if (S_i >= target && S_next < target) {
+      s_res[0] = 255 - tid;
+      s_res[1] = S_next;
+    }
+  }
+  __syncthreads();
+}
+
+template <int KPT, typename OUT_T>
+__global__ __launch_bounds__(kRowThreads) void topk_row_kernel(
+    const uint16_t* __restrict__ keys, int64_t key_stride, int T,
+    const uint32_t* __restrict__ hist1, int C1, SelSpec sp, OUT_T* __restrict__ out,
+    int64_t out_stride) {
+  static_assert(KPT % 8 == 0, "KPT must be a multiple of 8");
+  __shared__ uint32_t s_h[4][256], s_h2[256], s_wsum[kRowWaves], s_res[2];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const SelRow sr = sp.row(r);
+  OUT_T* orow = out + (int64_t)r * out_stride;
+  if (sp.plans)  // ragged rows: pad past the row's k with -1
+    for (int i = sr.k + tid; i < sp.k_cols; i += kRowThreads) orow[i] = (OUT_T)-1;
+  if (sr.k == 0) return;
+  const int c0 = sr.cs, c1 = sr.cs + sr.n;
+
+  // Keys of columns [tid*KPT, +KPT), 8 per 16-byte load; granules past the
+  // row's T columns load the last granule and are masked by the window.
+  uint32_t kw[KPT / 2];
+  const uint16_t* kr = keys + (int64_t)r * key_stride;
+#pragma unroll
+  for (int i = 0; i < KPT / 8; ++i) {
+    const int col = min(tid * KPT + 8 * i, T - 8);
+    const uint4 v = *reinterpret_cast<const uint4*>(kr + col);
+    kw[4 * i] = v.x;
+    kw[4 * i + 1] = v.y;
+    kw[4 * i + 2] = v.z;
+    kw[4 * i + 3] = v.w;
+  }
+  auto key_at = [&](int e) -> uint32_t { return (kw[e >> 1] >> ((e & 1) * 16)) & 0xffffu; };
+  auto live = [&](int e) -> bool {
+    const int col = tid * KPT + e;
+    return col >= c0 && col < c1;
+  };
+
+  // Level 1: the scorer's chunk histograms summed per bin (4 partial sums).
+  {
+    const int bin = tid & 255, part = tid >> 8;
+    const uint32_t* hp = hist1 + (int64_t)r * C1 * 256 + bin;
+    uint32_t a = 0;
+    for (int c = part; c < C1; c += 4) a += hp[(int64_t)c * 256];
+    s_h[part][bin] = a;
+    if (tid < 256) s_h2[tid] = 0;
+  }
+  __syncthreads();
+  if (tid < 256) s_h[0][tid] += s_h[1][tid] + s_h[2][tid] + s_h[3][tid];
+  __syncthreads();
+  row_select_bin(s_h[0], (uint32_t)sr.k, s_wsum, s_res);
+  const uint32_t b1 = s_res[0], gt1 = s_res[1];
+
+  // Level 2 over the keys of bin b1.
+#pragma unroll
+  for (int e = 0; e < KPT; ++e) {
+    const uint32_t key = key_at(e);
+    if ((key >> 8) == b1 && live(e)) atomicAdd(&s_h2[key & 255u], 1u);
+  }
+  __syncthreads();
+  const uint32_t k2 = (uint32_t)sr.k - gt1;
+  row_select_bin(s_h2, k2, s_wsum, s_res);
+  const uint32_t tau = (b1 << 8) | s_res[0];
+  const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
+
+  // Ordered compaction: keys > tau, then the `need` lowest-column ties.
+  uint32_t ngt = 0, ntie = 0;
+#pragma unroll
+  for (int e = 0; e < KPT; ++e) {
+    const uint32_t key = key_at(e);
+    const bool ok = live(e);
+    ngt += (ok && key > tau) ? 1u : 0u;
+    ntie += (ok && key == tau) ? 1u : 0u;
+  }
+  uint32_t all;
+  const uint32_t tie0 = row_exclusive_scan(ntie, s_wsum, &all);
+  const uint32_t take = tie0 >= need ? 0u : min(ntie, need - tie0);
+  uint32_t pos = row_exclusive_scan(ngt + take, s_wsum, &all);
+  uint32_t taken = 0;
+#pragma unroll
+  for (int e = 0; e < KPT; ++e) {
+    const uint32_t key = key_at(e);
+    if (!live(e)) continue;
+    bool sel = key > tau;
+    if (key == tau && taken < take) {
+      sel = true;
+      ++taken;
+    }
+    if (sel) orow[pos++] = (OUT_T)(tid * KPT + e);
+  }
+}
+
+// Keys per thread of topk_row_kernel for a row of T columns, or 0 for the
+// two-kernel path.  One workgroup per row pays off up to 32 keys per thread
+// (T <= 32768: batched decode rows); longer rows want the parallelism of the
+// chunked levels (at 128 keys per thread the row kernel spills and runs 8
+// workgroups for a batch-1 step).  LAPRUNE_TOPK=levels|row forces a path.
+int row_kernel_kpt(int T) {
+  static const int mode = [] {
+    const char* e = getenv("LAPRUNE_TOPK");
+    if (!e) return 0;
+    return strcmp(e, "levels") == 0 ? 1 : strcmp(e, "row") == 0 ? 2 : 0;
+  }();
+  if (mode == 1 || T % 8 != 0) return 0;
+  const int max_kpt = mode == 2 ? 128 : 32;
+  for (int kpt = 8; kpt <= max_kpt; kpt *= 2)
+    if ((int64_t)kpt * kRowThreads >= T) return kpt;
+  return 0;
+}
+
+template <typename OUT_T>
+void launch_row_kernel(int kpt, const uint16_t* keys, int64_t key_stride, int T,
+                       const uint32_t* hist1, int C1, const SelSpec& sp, int R, OUT_T* out,
+                       int64_t out_stride, hipStream_t st) {
+  switch (kpt) {
+#define LAP_ROWK(K)                                                                       \
+  case K:                                                                                 \
+    hipLaunchKernelGGL((topk_row_kernel<K, OUT_T>), dim3(R), dim3(kRowThreads), 0, st, keys, \
+                       key_stride, T, hist1, C1, sp, out, out_stride);                    \
+    break;
+    LAP_ROWK(8) LAP_ROWK(16) LAP_ROWK(32) LAP_ROWK(64) LAP_ROWK(128)
+#undef LAP_ROWK
+  }
+}
+
 // Upper bound on the scorer's workgroup chunks per row: a chunk holds at
 // least one pass of the smallest launch shape (256 threads x 1 token).
 int retrieve_chunk_bound(int T) { return (T + 255) / 256; }
@@ -514,6 +697,17 @@ static int retrieve_select_impl(int B, int Hkv, int T, const SelSpec& sp, int n_
   const int C1 = score_g4_nchunk(R, T);
   LAP_CHECK_CODE(C1 > 0 && C1 <= retrieve_chunk_bound(T), LAP_ERR_HIP,
                  "%s: device query failed", who);
+  const int kpt = row_kernel_kpt(T);
+  if (kpt > 0) {
+    if (out_dtype == LAP_DTYPE_I64)
+      launch_row_kernel<int64_t>(kpt, w.keys, T, T, w.hist1, C1, sp, R,
+                                 static_cast<int64_t*>(out_idx), out_stride, st);
+    else
+      launch_row_kernel<int32_t>(kpt, w.keys, T, T, w.hist1, C1, sp, R,
+                                 static_cast<int32_t*>(out_idx), out_stride, st);
+    LAP_LAUNCH_CHECK("topk_row_kernel");
+    return LAP_OK;
+  }
   KeySrc ks{w.keys, T, true};
   return run_levels(w, ks, R, sp, n_max, C1, out_idx, out_dtype, out_stride, st);
 }

@@ -184,6 +184,7 @@ class SparseDecoder:
         self.key_mode = N.KEY_BF16 if self.cfg.score_dtype == torch.bfloat16 else N.KEY_F16
         self.last_k = 0
         self._plans = None
+        self._plan_key = None
 
     def _k_cap(self, t: int) -> int:
         cs, ce = candidate_window(t, t, self.cfg.sink_size, self.cfg.local_window)
@@ -281,7 +282,13 @@ class SparseDecoder:
         plans = self.row_plans(t_codes, t_total)
         if self._plans is None:
             self._plans = PlanBuffer(B, self.dev)
-        pdev = self._plans.upload([tuple(p[f] for f in PLAN_FIELDS) for p in plans])
+        key = (tuple(t_codes), tuple(t_total))
+        if key != self._plan_key:
+            # the device plans change only here; a step with the same lengths
+            # (a graph replay) reuses them
+            self._plans.upload([tuple(p[f] for f in PLAN_FIELDS) for p in plans])
+            self._plan_key = key
+        pdev = self._plans.dev
         st = N.stream_of(q)
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
         N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
@@ -342,6 +349,7 @@ class DenseDecoder:
                           max(max_tokens, 1))
         self.ws = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)  # counters start at 0
         self._plans = None
+        self._plan_key = None
 
     @torch.no_grad()
     def step(self, q: torch.Tensor, keys: torch.Tensor, vals: torch.Tensor,
@@ -358,7 +366,10 @@ class DenseDecoder:
                 raise RuntimeError("lengths must lie in [1, keys.shape[2]]")
             if self._plans is None:
                 self._plans = PlanBuffer(B, q.device)
-            pdev = self._plans.upload([(t, t, 0, 0, 0, 0, 0, t) for t in rows])
+            if tuple(rows) != self._plan_key:
+                self._plans.upload([(t, t, 0, 0, 0, 0, 0, t) for t in rows])
+                self._plan_key = tuple(rows)
+            pdev = self._plans.dev
             N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1),
                    N.ptr(keys), N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D,
                    keys.stride(0), keys.stride(1), keys.stride(2), vals.stride(0),

@@ -46,6 +46,26 @@ def test_lut_build_bit_exact(dev, K, orc, qdt, layout):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("Hq,D,M,Kc,G,layout", [
+    (512, 128, 32, 256, 4, "gmkg"),   # batch 16 x 32 heads: 64-head tiles
+    (40, 128, 32, 256, 4, "gmkg"),    # partial head tile
+    (24, 128, 5, 100, 2, "gmkg"),     # G = 2, M*K not a multiple of the row tile
+    (64, 256, 8, 64, 4, "hmk"),       # D = 256
+])
+def test_lut_build_tiles(dev, K, orc, Hq, D, M, Kc, G, layout):
+    from laprune_amd import _native as N
+    print("device info (CUs, LDS per block, wave):", N.device_info(), flush=True)
+    g = _gen(3 + Hq + D)
+    q = torch.randn(Hq, D, generator=g).bfloat16()
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    lut = K.aq_lut_build(q.to(dev), cb.to(dev), G=G, layout=layout)
+    torch.cuda.synchronize()
+    want = orc.lut_build(q.float().numpy(), cb.numpy())
+    if layout == "gmkg":
+        want = orc.lut_to_gmkg(want, G)
+    assert np.array_equal(_np_u16(lut), want)
+
+
 def test_lut_build_odd_shapes(dev, K, orc):
     g = _gen(2)
     q = torch.randn(5, 64, generator=g)
