@@ -1,5 +1,7 @@
 """Host-side selection arithmetic of laprune_amd.retrieval against the oracle's
 restatement of aq_evaluation.py:185-237 and closed forms."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -106,3 +108,64 @@ def test_plan_fields_match_the_c_struct():
     body = re.search(r"typedef struct lap_row_plan \{(.*?)\} lap_row_plan;", text, re.S).group(1)
     fields = re.findall(r"(\w+)\s*[,;]", body)
     assert tuple(fields) == PLAN_FIELDS
+
+
+# ------------------------------------------------------------ codebook files
+
+def test_codebook_file_round_trip(tmp_path):
+    from laprune_amd import codebooks as CB
+    g = torch.Generator().manual_seed(11)
+    cb = torch.randn(4, 16, 8, generator=g)
+    CB.save_file(str(tmp_path / "layer_3_group_0.pt"), cb, metadata={"target": "key_post_rope"})
+    got = CB.load_file(str(tmp_path / "layer_3_group_0.pt"))
+    assert (got.layer, got.group, got.M, got.K, got.d) == (3, 0, 4, 16, 8)
+    assert torch.equal(got.codebooks, cb) and got.extras["metadata"]["target"] == "key_post_rope"
+
+
+def test_codebook_dir_rules(tmp_path):
+    """Unparsable names are ignored; groups the head grouping cannot use are
+    skipped (the reference's rule); a layer filter applies."""
+    from laprune_amd import codebooks as CB
+    cb = torch.zeros(2, 4, 8)
+    for name in ("layer_0_group_0.pt", "layer_0_group_1.pt", "layer_1_group_0.pt",
+                 "layer_x_group_0.pt", "notes.txt"):
+        CB.save_file(str(tmp_path / name), cb) if name.endswith(".pt") else \
+            (tmp_path / name).write_text("x")
+    assert sorted(CB.load_dir(str(tmp_path))) == [(0, 0), (0, 1), (1, 0)]
+    # 8 KV heads in one group of 8 -> only group 0 is usable
+    assert sorted(CB.load_dir(str(tmp_path), num_heads=8, heads_per_group=8)) == [(0, 0), (1, 0)]
+    assert sorted(CB.load_dir(str(tmp_path), layers=[1])) == [(1, 0)]
+    with pytest.raises(FileNotFoundError):
+        CB.load_dir(str(tmp_path / "missing"))
+
+
+def test_codebook_file_checks(tmp_path):
+    from laprune_amd import codebooks as CB
+    torch.save({"M": 2, "K": 4, "d": 8, "codebooks": torch.zeros(2, 4, 9)}, tmp_path / "a.pt")
+    with pytest.raises(RuntimeError, match="do not match"):
+        CB.load_file(str(tmp_path / "a.pt"))
+    torch.save({"M": 2, "K": 300, "d": 8, "codebooks": torch.zeros(2, 300, 8)}, tmp_path / "b.pt")
+    with pytest.raises(RuntimeError, match="uint8"):
+        CB.load_file(str(tmp_path / "b.pt"))
+    torch.save({"M": 2, "d": 8, "codebooks": torch.zeros(2, 4, 8)}, tmp_path / "c.pt")
+    with pytest.raises(RuntimeError, match="missing 'K'"):
+        CB.load_file(str(tmp_path / "c.pt"))
+
+
+SHIPPED = "/root/reference/codebooks/llama31-8b-instruct"
+
+
+@pytest.mark.skipif(not os.path.isdir(SHIPPED), reason="reference codebooks not present")
+def test_shipped_codebooks_load():
+    """The reference's Llama-3.1 files (read only where they exist, never
+    copied): 32 layers of [32, 256, 128] float32; layer 0 has std 0.426 and
+    absmax 8.82, and its stage norms decay (residual-ordered stages)."""
+    from laprune_amd import codebooks as CB
+    books = CB.load_dir(SHIPPED, num_heads=8, heads_per_group=8)
+    assert len(books) == 32 and all(g == 0 for _, g in books)
+    b0 = books[(0, 0)]
+    assert (b0.M, b0.K, b0.d) == (32, 256, 128)
+    assert abs(b0.codebooks.std().item() - 0.426) < 5e-3
+    assert abs(b0.codebooks.abs().max().item() - 8.82) < 1e-2
+    stage_norm = b0.codebooks.norm(dim=2).mean(dim=1)
+    assert stage_norm[0] > 4 * stage_norm[-1]
