@@ -50,30 +50,37 @@ class DecodeKVCache:
     """K/V buffer + AQ code cache of one layer.
 
     Args:
-      codebooks: [M, K, D] fp32 codebooks of the layer (on the GPU).
+      codebooks: [M, K, D] fp32 codebooks of the layer (on the GPU), or None
+        for a layer that keeps K/V only (a dense layer: nothing is encoded).
       batch, num_kv_heads, head_dim: cache geometry.
       capacity: initial token capacity (grows by doubling when exceeded).
       dtype: K/V dtype (bf16 or fp16).
       group_size: decode encode buffer (64 in the reference configs).
     """
 
-    def __init__(self, codebooks: torch.Tensor, batch: int, num_kv_heads: int, head_dim: int,
-                 capacity: int, dtype: torch.dtype = torch.bfloat16, group_size: int = 64):
-        N.require_cuda(codebooks)
-        if codebooks.dim() != 3 or codebooks.shape[2] != head_dim:
-            raise RuntimeError(f"codebooks must be [M, K, {head_dim}]")
+    def __init__(self, codebooks: torch.Tensor | None, batch: int, num_kv_heads: int,
+                 head_dim: int, capacity: int, dtype: torch.dtype = torch.bfloat16,
+                 group_size: int = 64, device=None):
         if dtype not in (torch.bfloat16, torch.float16):
             raise RuntimeError("K/V dtype must be bf16 or fp16")
-        self.dev = codebooks.device
-        self.cb = codebooks.to(torch.float32).contiguous()
-        self.M, self.K = int(self.cb.shape[0]), int(self.cb.shape[1])
-        if self.K > 256:
-            raise RuntimeError("K must be <= 256 for uint8 codes")
         self.B, self.Hkv, self.D = batch, num_kv_heads, head_dim
         self.dtype = dtype
         self.group_size = int(group_size)
-        self.prep = aq_encode_prepare(self.cb)
         cap = max(int(capacity), 16)
+        if codebooks is None:
+            self.dev = torch.device(device if device is not None else "cuda")
+            self.cb = self.prep = None
+            self.M = self.K = 0
+        else:
+            N.require_cuda(codebooks)
+            if codebooks.dim() != 3 or codebooks.shape[2] != head_dim:
+                raise RuntimeError(f"codebooks must be [M, K, {head_dim}]")
+            self.dev = codebooks.device
+            self.cb = codebooks.to(torch.float32).contiguous()
+            self.M, self.K = int(self.cb.shape[0]), int(self.cb.shape[1])
+            if self.K > 256:
+                raise RuntimeError("K must be <= 256 for uint8 codes")
+            self.prep = aq_encode_prepare(self.cb)
         self.k = torch.empty((batch, num_kv_heads, cap, head_dim), dtype=dtype, device=self.dev)
         self.v = torch.empty_like(self.k)
         self.codes = torch.zeros((batch, num_kv_heads, cap, self.M), dtype=torch.uint8,
@@ -168,6 +175,10 @@ class DecodeKVCache:
         return self._encode_rows(list(range(self.B)), prefill, resid_norm)
 
     def _encode_rows(self, rows: list[int], prefill: bool, resid_norm) -> int:
+        if self.cb is None:  # K/V-only layer: the whole cache counts as encoded
+            for b in rows:
+                self.encoded_lens[b] = self.lengths[b]
+            return 0
         todo = {}
         for b in rows:
             rng = flush_range(self.lengths[b], self.encoded_lens[b], self.group_size, prefill)

@@ -1,0 +1,225 @@
+"""LAPrune decode attention inside a transformers Llama model.
+
+Mirrors the reference's model plumbing for the decode path:
+  * ``Decoder`` (laprune/llm/modifiers/aq_evaluation.py:496-540) patches
+    every attention layer; layers in ``apply_layers`` are LAPrune layers, the
+    rest stay dense;
+  * ``self_attn_forward`` (:279-322): q/k/v projections, RoPE, append to the
+    layer's K/V cache, encode new keys (prefill: all of them; decode: in
+    64-token groups), causal SDPA at prefill, sparse retrieval at decode;
+  * ``AQGeneration.generate`` (aq_generation.py:114-151): prefill all prompt
+    tokens but the last, then greedy decode one token at a time.
+
+Each layer owns a :class:`~laprune_amd.cache.DecodeKVCache`; LAPrune layers
+decode through :class:`~laprune_amd.retrieval.SparseDecoder` (LUT -> fused
+score -> top-k -> sparse attention, all HIP), dense layers through
+:class:`~laprune_amd.retrieval.DenseDecoder`.  Sequences of one batch may have
+different lengths (ragged): prefill them one row at a time with
+:meth:`LAPruneLlama.prefill_row`, then decode the batch together.
+
+The model is a plain ``transformers`` ``LlamaForCausalLM``; nothing here
+downloads anything (build it from a local ``LlamaConfig``).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+from .cache import DecodeKVCache
+from .retrieval import DenseDecoder, RetrievalConfig, SparseDecoder
+
+
+@dataclass
+class LAPruneSettings:
+    """Decode settings (the reference's ``draft_kwargs`` keys on this path)."""
+
+    apply_layers: list[int] = field(default_factory=list)  # LAPrune layers
+    retrieval: RetrievalConfig = field(default_factory=RetrievalConfig)
+    group_size: int = 64                                   # decode encode buffer
+
+    def __post_init__(self):
+        if self.retrieval.local_window < self.group_size - 1:
+            raise ValueError("local_window must cover the encode buffer "
+                             "(local_window >= group_size - 1)")
+
+
+class _LayerState:
+    def __init__(self, cache: DecodeKVCache, sparse: SparseDecoder | None, dense: DenseDecoder):
+        self.cache = cache
+        self.sparse = sparse
+        self.dense = dense
+
+
+class LAPruneLlama:
+    """A Llama model whose attention layers run the LAPrune decode path.
+
+    Args:
+      model: ``transformers`` ``LlamaForCausalLM`` on the GPU (bf16 or fp16).
+      codebooks: {layer index: [M=32, K=256, head_dim] fp32 codebooks} for the
+        layers in ``settings.apply_layers``.
+      settings: which layers are LAPrune layers and the selection settings.
+      batch: sequences decoded together.
+      capacity: token capacity of every layer's cache (prompt + new tokens).
+    """
+
+    def __init__(self, model, codebooks: dict[int, torch.Tensor], settings: LAPruneSettings,
+                 batch: int, capacity: int):
+        from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+        self._rope = apply_rotary_pos_emb
+        self.model = model
+        self.settings = settings
+        cfg = model.config
+        self.B = batch
+        self.Hq = cfg.num_attention_heads
+        self.Hkv = cfg.num_key_value_heads
+        self.D = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.Hq
+        self.capacity = capacity
+        p = next(model.parameters())
+        self.dev, self.dtype = p.device, p.dtype
+        missing = [i for i in settings.apply_layers if i not in codebooks]
+        if missing:
+            raise RuntimeError(f"no codebooks for LAPrune layers {missing}")
+        self.layers = model.model.layers
+        self.states: list[_LayerState] = []
+        for i, layer in enumerate(self.layers):
+            cb = codebooks[i].to(self.dev, torch.float32) if i in settings.apply_layers else None
+            cache = DecodeKVCache(cb, batch, self.Hkv, self.D, capacity, dtype=self.dtype,
+                                  group_size=settings.group_size, device=self.dev)
+            sparse = None
+            if cb is not None:
+                sparse = SparseDecoder(cb, batch, self.Hq, self.Hkv, self.D, capacity,
+                                       settings.retrieval, dtype=self.dtype)
+            dense = DenseDecoder(batch, self.Hq, self.Hkv, self.D, capacity, self.dev, self.dtype)
+            self.states.append(_LayerState(cache, sparse, dense))
+            attn = layer.self_attn
+            attn.forward = self._make_forward(i, attn)
+        self._row = None  # sequence being prefilled alone (ragged prefill)
+
+    # ------------------------------------------------------------ attention
+    def _make_forward(self, idx: int, attn):
+        def forward(hidden_states, position_embeddings=None, attention_mask=None,
+                    past_key_values=None, **kwargs):
+            return self._attention(idx, attn, hidden_states, position_embeddings)
+        return forward
+
+    def _attention(self, idx, attn, h, position_embeddings):
+        B, T, _ = h.shape
+        Hq, Hkv, D = self.Hq, self.Hkv, self.D
+        q = attn.q_proj(h).view(B, T, Hq, D).transpose(1, 2)
+        k = attn.k_proj(h).view(B, T, Hkv, D).transpose(1, 2)
+        v = attn.v_proj(h).view(B, T, Hkv, D).transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = self._rope(q, k, cos, sin)
+        st = self.states[idx]
+        if T > 1:  # prefill: causal attention over the prompt, encode all its keys
+            if self._row is None:
+                if any(n != 0 for n in st.cache.lengths):
+                    raise RuntimeError("batched prefill needs empty caches (use reset())")
+                st.cache.append(k, v, prefill=True)
+            else:
+                st.cache.append_row(self._row, k, v, prefill=True)
+            G = Hq // Hkv
+            kk = k.repeat_interleave(G, dim=1)
+            vv = v.repeat_interleave(G, dim=1)
+            o = F.scaled_dot_product_attention(q, kk, vv, is_causal=True,
+                                               scale=1.0 / math.sqrt(D))
+        else:
+            if self._row is not None:
+                raise RuntimeError("single-token steps decode the whole batch")
+            st.cache.append(k, v)  # encodes each sequence's 64-token groups
+            if st.sparse is not None:
+                o = st.sparse.step_cached(q, st.cache)
+            else:
+                o = st.dense.step(q, st.cache.k, st.cache.v, lengths=st.cache.lengths)
+        o = o.transpose(1, 2).reshape(B, T, Hq * D)
+        return attn.o_proj(o), None
+
+    # ------------------------------------------------------------ model calls
+    def reset(self) -> None:
+        """Forget every sequence (the reference's Decoder.reset)."""
+        for st in self.states:
+            st.cache.lengths = [0] * self.B
+            st.cache.encoded_lens = [0] * self.B
+
+    @property
+    def lengths(self) -> list[int]:
+        return list(self.states[0].cache.lengths)
+
+    def _forward(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        out = self.model(input_ids=ids, position_ids=pos, use_cache=False, logits_to_keep=1)
+        return out.logits[:, -1]
+
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """Prefill [B, T] prompts of one length; returns last-position logits [B, V]."""
+        if input_ids.shape[0] != self.B:
+            raise RuntimeError(f"expected {self.B} sequences, got {input_ids.shape[0]}")
+        T = input_ids.shape[1]
+        pos = torch.arange(T, device=self.dev)[None].expand(self.B, T)
+        return self._forward(input_ids.to(self.dev), pos)
+
+    @torch.no_grad()
+    def prefill_row(self, b: int, input_ids: torch.Tensor) -> torch.Tensor:
+        """Prefill sequence b alone ([1, T_b] prompt); returns its logits [1, V]."""
+        T = input_ids.shape[-1]
+        self._row = b
+        try:
+            pos = torch.arange(T, device=self.dev)[None]
+            return self._forward(input_ids.reshape(1, T).to(self.dev), pos)
+        finally:
+            self._row = None
+
+    @torch.no_grad()
+    def decode(self, tokens: torch.Tensor) -> torch.Tensor:
+        """One decode step for all sequences: tokens [B, 1]; returns logits [B, V]."""
+        pos = torch.tensor(self.lengths, device=self.dev)[:, None]
+        return self._forward(tokens.reshape(self.B, 1).to(self.dev), pos)
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int,
+                 eos_token_id: int | None = None) -> torch.Tensor:
+        """Greedy generation as AQGeneration.generate: prefill all prompt
+        tokens but the last, then decode from it.  Returns [B, T + n] ids."""
+        self.reset()
+        ids = input_ids.to(self.dev)
+        if ids.shape[1] > 1:
+            self.prefill(ids[:, :-1])
+        tok = ids[:, -1:]
+        new = []
+        for _ in range(max_new_tokens):
+            tok = self.decode(tok).argmax(dim=-1, keepdim=True)
+            new.append(tok)
+            if eos_token_id is not None and bool((tok == eos_token_id).all()):
+                break
+        return torch.cat([ids] + new, dim=1)
+
+
+def llama31_8b_config(num_layers: int = 32, max_position_embeddings: int = 131072):
+    """A local LlamaConfig with Llama-3.1-8B's public geometry (no download)."""
+    from transformers import LlamaConfig
+    return LlamaConfig(
+        vocab_size=128256, hidden_size=4096, intermediate_size=14336,
+        num_hidden_layers=num_layers, num_attention_heads=32, num_key_value_heads=8,
+        head_dim=128, max_position_embeddings=max_position_embeddings, rms_norm_eps=1e-5,
+        rope_theta=500000.0, tie_word_embeddings=False,
+        rope_scaling={"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                      "high_freq_factor": 4.0, "original_max_position_embeddings": 8192},
+        attn_implementation="sdpa")
+
+
+def random_model(config, device, dtype=torch.bfloat16, seed: int = 0, std: float = 0.02):
+    """Random-init LlamaForCausalLM: every weight N(0, std), norms at 1."""
+    from transformers import LlamaForCausalLM
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = LlamaForCausalLM(config).to(dtype)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if p.dim() >= 2:
+                p.normal_(0.0, std)
+            else:
+                p.fill_(1.0)
+    return model.eval()
