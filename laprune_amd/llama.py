@@ -27,6 +27,7 @@ from dataclasses import dataclass, field
 
 import torch
 import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from .cache import DecodeKVCache
 from .retrieval import DenseDecoder, RetrievalConfig, SparseDecoder
@@ -124,8 +125,10 @@ class LAPruneLlama:
             G = Hq // Hkv
             kk = k.repeat_interleave(G, dim=1)
             vv = v.repeat_interleave(G, dim=1)
-            o = F.scaled_dot_product_attention(q, kk, vv, is_causal=True,
-                                               scale=1.0 / math.sqrt(D))
+            # fused kernels only: the math fallback would materialise T x T scores
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                o = F.scaled_dot_product_attention(q, kk, vv, is_causal=True,
+                                                   scale=1.0 / math.sqrt(D))
         else:
             if self._row is not None:
                 raise RuntimeError("single-token steps decode the whole batch")
