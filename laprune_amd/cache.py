@@ -208,6 +208,51 @@ class DecodeKVCache:
                N.ptr(self.prep), self.prep.numel(), N.ptr(c), c.stride(0), c.stride(1),
                c.stride(2), N.ptr(resid_norm), N.stream_of(k))
 
+    # ---- device-resident decode steps (one captured graph per step) ------
+    # The positions and flush ranges of a step live in device tensors, so the
+    # same launches serve every step; the host only advances its bookkeeping
+    # (advance_decode) and uploads the step's values.  Capacity cannot grow
+    # here: size it for the whole generation.
+
+    def advance_decode(self) -> list[tuple[int, int]]:
+        """Host bookkeeping of one decode token per sequence: lengths grow by
+        one and each sequence whose encode buffer is full flushes it.  Returns
+        the per-sequence flush ranges ((0, 0) for none)."""
+        if max(self.lengths) + 1 > self.capacity:
+            raise RuntimeError("decode step past the cache capacity")
+        ranges = []
+        for b in range(self.B):
+            self.lengths[b] += 1
+            if self.cb is None:
+                self.encoded_lens[b] = self.lengths[b]
+                ranges.append((0, 0))
+                continue
+            rng = flush_range(self.lengths[b], self.encoded_lens[b], self.group_size, False)
+            if rng is None:
+                ranges.append((0, 0))
+            else:
+                ranges.append(rng)
+                self.encoded_lens[b] = rng[1]
+        return ranges
+
+    def append_at(self, k_new: torch.Tensor, v_new: torch.Tensor, pos: torch.Tensor,
+                  bidx: torch.Tensor) -> None:
+        """Write one token per sequence ([B, Hkv, 1, D]) at device positions
+        pos [B, 1] (int64); bidx is arange(B)[:, None] on the device."""
+        self.k[bidx, :, pos] = k_new.to(self.dtype).permute(0, 2, 1, 3)
+        self.v[bidx, :, pos] = v_new.to(self.dtype).permute(0, 2, 1, 3)
+
+    def encode_ranges(self, ranges: torch.Tensor) -> None:
+        """Encode each sequence's device range ([B, 2] int32, at most
+        group_size tokens; empty ranges cost a workgroup exit)."""
+        if self.cb is None:
+            return
+        k, c = self.k, self.codes
+        N.call("lap_encode_keys_ranges", N.ptr(k), N.dtype_code(k.dtype), k.stride(0),
+               k.stride(1), k.stride(2), self.B, self.Hkv, N.ptr(ranges), self.group_size,
+               self.D, N.ptr(self.cb), self.M, self.K, N.ptr(self.prep), self.prep.numel(),
+               N.ptr(c), c.stride(0), c.stride(1), c.stride(2), N.stream_of(k))
+
     def keys(self) -> torch.Tensor:
         return self.k[:, :, :self.length]
 

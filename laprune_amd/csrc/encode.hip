@@ -58,6 +58,8 @@ Prep carve_prep(void* base, int M, int K, int D) {
 // a block of L consecutive tokens of every (batch, KV head) pair of a
 // strided [B][H][T][D] key cache, and the same position in a strided
 // [B][H][Tcap][M] code cache.  A plain [N][D] input is L = N, Hs = 1.
+// With per-batch ranges (device [B][2] = t0_b, t1_b), segment s covers
+// tokens t0_b + j for j < min(t1_b - t0_b, L); rows past that are not live.
 struct RowMap {
   const void* x;
   int x_dtype;  // f32 / f16 / bf16 (widened exactly to fp32)
@@ -65,10 +67,17 @@ struct RowMap {
   uint8_t* codes;
   int64_t c_sb, c_sh, c_st;
   int L, Hs, t0;
+  const int32_t* ranges;  // [B][2] or null
   __device__ __forceinline__ int64_t off(int i, int64_t sb, int64_t sh, int64_t st) const {
-    const int sg = i / L, t = t0 + (i - sg * L);
+    const int sg = i / L, j = i - sg * L;
     const int b = sg / Hs, h = sg - b * Hs;
+    const int t = (ranges ? ranges[2 * b] : t0) + j;
     return (int64_t)b * sb + (int64_t)h * sh + (int64_t)t * st;
+  }
+  __device__ __forceinline__ bool live(int i) const {
+    if (!ranges) return true;
+    const int sg = i / L, b = sg / Hs;
+    return i - sg * L < ranges[2 * b + 1] - ranges[2 * b];
   }
   __device__ __forceinline__ float xval(int i, int d) const {
     return load_as_f32(x, off(i, x_sb, x_sh, x_st) + d, x_dtype);
@@ -145,7 +154,7 @@ __global__ __launch_bounds__(256) void encode_greedy_kernel(
   __shared__ __attribute__((aligned(16))) float s_r[4][D];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + wave;
-  const bool live = row < N;
+  const bool live = row < N && rm.live(row);
   float* r = s_r[wave];
   for (int d = lane; d < D; d += 64) r[d] = live ? rm.xval(row, d) : 0.f;
   __syncthreads();
@@ -526,7 +535,7 @@ __device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st
     a2 = row_fold16(a2);
     if (j == 0) {
       s.rn[row] = a2;
-      if (row0 + row < N) rm.crow(row0 + row)[m] = (uint8_t)code;
+      if (row0 + row < N && rm.live(row0 + row)) rm.crow(row0 + row)[m] = (uint8_t)code;
     }
   }
   lds_barrier();
@@ -542,9 +551,14 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = blockIdx.x * 16;
   const int NT = K / 16;
+  if (rm.ranges) {  // a workgroup with no live row leaves at once (same test in every thread)
+    bool any = false;
+    for (int r = 0; r < 16; ++r) any = any || (row0 + r < N && rm.live(row0 + r));
+    if (!any) return;
+  }
   for (int i = tid; i < 16 * D; i += C::THREADS) {
     const int r = i / D, d = i - r * D;
-    const float v = row0 + r < N ? rm.xval(row0 + r, d) : 0.f;
+    const float v = (row0 + r < N && rm.live(row0 + r)) ? rm.xval(row0 + r, d) : 0.f;
     s.r[r][d] = v;
     s.rb[r][d] = __builtin_bit_cast(uint16_t, (__bf16)v);
   }
@@ -581,7 +595,8 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
   }
   sink ^= pfa ^ pfb;
   if (sink == 0x9e3779b9u && N < 0) rm.codes[0] = 0;  // never true: keeps the prefetch loads
-  if (tid < 16 && rnorm && row0 + tid < N) rnorm[row0 + tid] = sqrtf(s.rn[tid]);
+  if (tid < 16 && rnorm && row0 + tid < N && rm.live(row0 + tid))
+    rnorm[row0 + tid] = sqrtf(s.rn[tid]);
 }
 
 }  // namespace
@@ -682,7 +697,7 @@ extern "C" int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, in
   LAP_CHECK(N >= 0 && D > 0 && M > 0, "lap_encode_greedy: bad sizes");
   LAP_CHECK(x_row_stride >= D && codes_row_stride >= M, "lap_encode_greedy: bad row strides");
   const RowMap rm{x, LAP_DTYPE_F32, 0, 0, x_row_stride, codes_out, 0, 0, codes_row_stride,
-                  N > 0 ? N : 1, 1, 0};
+                  N > 0 ? N : 1, 1, 0, nullptr};
   return run_encode(rm, N, D, codebooks, M, K, prep, prep_bytes, resid_norm, stream,
                     "lap_encode_greedy");
 }
@@ -703,7 +718,29 @@ extern "C" int lap_encode_keys(const void* keys, int key_dtype, int64_t k_sb, in
   const int64_t n = (int64_t)B * Hkv * (t1 - t0);
   LAP_CHECK(n <= (int64_t)1 << 30, "lap_encode_keys: too many rows");
   const RowMap rm{keys, key_dtype, k_sb, k_sh, k_st, codes, c_sb, c_sh, c_st,
-                  t1 > t0 ? t1 - t0 : 1, Hkv, t0};
+                  t1 > t0 ? t1 - t0 : 1, Hkv, t0, nullptr};
   return run_encode(rm, (int)n, D, codebooks, M, K, prep, prep_bytes, resid_norm, stream,
                     "lap_encode_keys");
+}
+
+extern "C" int lap_encode_keys_ranges(const void* keys, int key_dtype, int64_t k_sb,
+                                      int64_t k_sh, int64_t k_st, int B, int Hkv,
+                                      const int32_t* ranges, int max_len, int D,
+                                      const float* codebooks, int M, int K, const void* prep,
+                                      size_t prep_bytes, uint8_t* codes, int64_t c_sb,
+                                      int64_t c_sh, int64_t c_st, lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(keys && codes && ranges, "lap_encode_keys_ranges: null pointer");
+  LAP_CHECK(key_dtype == LAP_DTYPE_F32 || key_dtype == LAP_DTYPE_F16 ||
+                key_dtype == LAP_DTYPE_BF16,
+            "lap_encode_keys_ranges: keys must be f32, f16 or bf16");
+  LAP_CHECK(B > 0 && Hkv > 0 && D > 0 && M > 0 && max_len > 0,
+            "lap_encode_keys_ranges: bad sizes");
+  LAP_CHECK(k_st >= D && c_st >= M, "lap_encode_keys_ranges: token strides smaller than D / M");
+  const int64_t n = (int64_t)B * Hkv * max_len;
+  LAP_CHECK(n <= (int64_t)1 << 30, "lap_encode_keys_ranges: too many rows");
+  const RowMap rm{keys, key_dtype, k_sb, k_sh, k_st, codes, c_sb, c_sh, c_st,
+                  max_len, Hkv, 0, ranges};
+  return run_encode(rm, (int)n, D, codebooks, M, K, prep, prep_bytes, nullptr, stream,
+                    "lap_encode_keys_ranges");
 }

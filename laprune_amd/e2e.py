@@ -14,7 +14,8 @@ codebooks are synthetic N(0, 0.02) [32, 256, 128] per LAPrune layer.
 
 ``--method dense`` decodes every layer with the same GPU's dense split-K
 flash-decode (the comparator); ``both`` runs LAPrune, then dense, on the same
-weights.  Prints one JSON line.
+weights.  Each decode step is one replay of a captured graph (``--eager``:
+host launches).  Prints one JSON line.
 
     python -m laprune_amd.e2e --config c4 --method both
 """
@@ -38,7 +39,7 @@ def log(*a):
 
 
 def run(model, cfg: dict, method: str, lengths: list[int], prompts: list[torch.Tensor],
-        codebooks: dict, layers: int) -> dict:
+        codebooks: dict, layers: int, graph: bool = True) -> dict:
     from .llama import LAPruneLlama, LAPruneSettings
     from .retrieval import RetrievalConfig
     apply = list(range(2, layers)) if method == "laprune" else []
@@ -68,14 +69,17 @@ def run(model, cfg: dict, method: str, lengths: list[int], prompts: list[torch.T
     prefill_s = time.perf_counter() - t0
     del logits
     log(f"  {method}: prefill {prefill_s:.2f} s; decoding {cfg['decode']} tokens")
-    finite = True
-    t0 = time.perf_counter()
+    finite_flags = []
     t_warm = None
     generated = []
     for step in range(cfg["decode"]):
-        logits = lm.decode(tok)
-        finite = finite and bool(torch.isfinite(logits).all())
-        tok = logits.argmax(dim=-1, keepdim=True)
+        if graph:  # one captured graph per step; the greedy token stays on the GPU
+            logits = lm.decode_graph(tok if step == 0 else None)
+            tok = lm.next_tokens().clone()
+        else:
+            logits = lm.decode(tok)
+            tok = logits.argmax(dim=-1, keepdim=True)
+        finite_flags.append(torch.isfinite(logits).all())
         generated.append(tok)
         if step + 1 == cfg["warmup"]:
             torch.cuda.synchronize()
@@ -84,8 +88,10 @@ def run(model, cfg: dict, method: str, lengths: list[int], prompts: list[torch.T
             log(f"  {method}: {step + 1} tokens")
     torch.cuda.synchronize()
     secs = time.perf_counter() - t_warm
+    finite = bool(torch.stack(finite_flags).all())
     measured = cfg["decode"] - cfg["warmup"]
-    out = {"method": method, "prefill_s": round(prefill_s, 3), "decode_s": round(secs, 4),
+    out = {"method": method, "graph": graph, "prefill_s": round(prefill_s, 3),
+           "decode_s": round(secs, 4),
            "tokens_per_s": round(B * measured / secs, 3),
            "ms_per_step": round(secs / measured * 1e3, 3), "finite_logits": finite,
            "first_tokens": torch.cat(generated[:8], dim=1)[0].tolist()}
@@ -103,6 +109,9 @@ def main(argv=None):
                     help="override the context length (uniform across the batch)")
     ap.add_argument("--decode-tokens", type=int, default=0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel from the host instead of replaying one "
+                         "captured graph per decode step")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("e2e needs a GPU", file=sys.stderr)
@@ -128,7 +137,8 @@ def main(argv=None):
     codebooks = {i: (torch.randn(32, 256, 128, generator=g) * 0.02).to(dev)
                  for i in range(2, args.layers)}
     methods = ["laprune", "dense"] if args.method == "both" else [args.method]
-    results = {m: run(model, cfg, m, lengths, prompts, codebooks, args.layers) for m in methods}
+    results = {m: run(model, cfg, m, lengths, prompts, codebooks, args.layers,
+                      graph=not args.eager) for m in methods}
     line = {"config": args.config, "batch": cfg["batch"], "layers": args.layers,
             "context_lengths": lengths if len(set(lengths)) > 1 else lengths[0],
             "decode_tokens": cfg["decode"], "warmup_tokens": cfg["warmup"],

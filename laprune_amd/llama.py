@@ -98,6 +98,9 @@ class LAPruneLlama:
             attn = layer.self_attn
             attn.forward = self._make_forward(i, attn)
         self._row = None  # sequence being prefilled alone (ragged prefill)
+        self._dev_mode = False
+        self._graph = None
+        self._g = None
 
     # ------------------------------------------------------------ attention
     def _make_forward(self, idx: int, attn):
@@ -129,6 +132,14 @@ class LAPruneLlama:
             with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                 o = F.scaled_dot_product_attention(q, kk, vv, is_causal=True,
                                                    scale=1.0 / math.sqrt(D))
+        elif self._dev_mode:  # fixed launches, every per-step value in device memory
+            st.cache.append_at(k, v, self._g_pos, self._g_bidx)
+            if st.sparse is not None:
+                st.cache.encode_ranges(self._g_ranges)
+                o = st.sparse.step_dev(q, st.cache.codes, st.cache.k, st.cache.v,
+                                       self._g_plan_sparse)
+            else:
+                o = st.dense.step_dev(q, st.cache.k, st.cache.v, self._g_plan_dense)
         else:
             if self._row is not None:
                 raise RuntimeError("single-token steps decode the whole batch")
@@ -181,19 +192,133 @@ class LAPruneLlama:
         pos = torch.tensor(self.lengths, device=self.dev)[:, None]
         return self._forward(tokens.reshape(self.B, 1).to(self.dev), pos)
 
+    # ------------------------------------------------------------ captured decode
+    # One decode step of the whole model as one HIP graph.  Per-step values
+    # (positions, the sequences' plans, encode-flush ranges) live in one
+    # device int32 buffer that the host rewrites before each replay; every
+    # kernel of the step reads them there, so the captured launches stay
+    # valid.  The host keeps the lengths and flush bookkeeping.
+
+    def _graph_buffers(self):
+        B, dev = self.B, self.dev
+        flat = torch.zeros(19 * B, dtype=torch.int32, device=dev)
+        self._g_flat = flat
+        self._g_plan_sparse = flat[:8 * B].view(B, 8)
+        self._g_plan_dense = flat[8 * B:16 * B].view(B, 8)
+        self._g_ranges = flat[16 * B:18 * B].view(B, 2)
+        self._g_pos32 = flat[18 * B:].view(B, 1)
+        self._g_pos = torch.zeros((B, 1), dtype=torch.long, device=dev)
+        self._g_bidx = torch.arange(B, device=dev)[:, None]
+        self._g_tok = torch.zeros((B, 1), dtype=torch.long, device=dev)
+        self._g_next = torch.zeros((B, 1), dtype=torch.long, device=dev)
+        self._g_logits = None
+        self._g_host = [torch.zeros(19 * B, dtype=torch.int32).pin_memory() for _ in range(4)]
+        self._g_done = [None] * 4
+        self._g_slot = 0
+        self._g = True
+
+    def _graph_body(self):
+        self._g_pos.copy_(self._g_pos32)
+        self._dev_mode = True
+        try:
+            logits = self._forward(self._g_tok, self._g_pos)
+        finally:
+            self._dev_mode = False
+        if self._g_logits is None:
+            self._g_logits = torch.empty_like(logits)
+        self._g_logits.copy_(logits)
+        self._g_next.copy_(logits.argmax(dim=-1, keepdim=True))
+
+    def _upload_step(self) -> None:
+        """Advance every layer's bookkeeping by one token and upload the
+        step's positions, plans and flush ranges."""
+        B = self.B
+        pos = self.lengths
+        ranges = None
+        for st in self.states:
+            r = st.cache.advance_decode()
+            if st.sparse is not None:
+                ranges = r
+        c0 = next((st for st in self.states if st.sparse is not None), self.states[0])
+        t_total = c0.cache.lengths
+        rows = [0] * (19 * B)
+        if c0.sparse is not None:
+            from .retrieval import PLAN_FIELDS
+            for b, p in enumerate(c0.sparse.row_plans(c0.cache.encoded_lens, t_total)):
+                rows[8 * b:8 * b + 8] = [p[f] for f in PLAN_FIELDS]
+        for b in range(B):
+            t = t_total[b]
+            rows[8 * B + 8 * b:8 * B + 8 * b + 8] = [t, t, 0, 0, 0, 0, 0, t]
+            if ranges is not None:
+                rows[16 * B + 2 * b:16 * B + 2 * b + 2] = list(ranges[b])
+            rows[18 * B + b] = pos[b]
+        i = self._g_slot
+        self._g_slot = (i + 1) % len(self._g_host)
+        if self._g_done[i] is not None:
+            self._g_done[i].synchronize()
+        h = self._g_host[i]
+        h.copy_(torch.tensor(rows, dtype=torch.int32))
+        self._g_flat.copy_(h, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.dev))
+        self._g_done[i] = ev
+
+    @torch.no_grad()
+    def decode_graph(self, tokens: torch.Tensor | None = None) -> torch.Tensor:
+        """One decode step for all sequences as one graph replay.  tokens
+        [B, 1] (device or host); None feeds the previous step's greedy
+        tokens.  Returns the logits [B, V] (a buffer the next step reuses)."""
+        if self._g is None:
+            self._graph_buffers()
+        if tokens is not None:
+            self._g_tok.copy_(tokens.reshape(self.B, 1), non_blocking=True)
+        else:
+            self._g_tok.copy_(self._g_next)
+        self._upload_step()
+        sig = tuple((st.cache.k.data_ptr(), st.cache.v.data_ptr(), st.cache.codes.data_ptr())
+                    for st in self.states)
+        if self._graph is not None and sig != self._graph_sig:
+            self._graph = None  # a cache was reallocated (grown): capture again
+        if self._graph is None:
+            # the first step runs eagerly (it also warms up every kernel), then
+            # the same body is captured for the following steps
+            side = torch.cuda.Stream(self.dev)
+            side.wait_stream(torch.cuda.current_stream(self.dev))
+            with torch.cuda.stream(side):
+                self._graph_body()
+            torch.cuda.current_stream(self.dev).wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._graph_body()
+            self._graph = g
+            self._graph_sig = sig
+        else:
+            self._graph.replay()
+        return self._g_logits
+
+    def next_tokens(self) -> torch.Tensor:
+        """Greedy tokens [B, 1] of the last captured step (device)."""
+        return self._g_next
+
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int,
-                 eos_token_id: int | None = None) -> torch.Tensor:
+                 eos_token_id: int | None = None, graph: bool = False) -> torch.Tensor:
         """Greedy generation as AQGeneration.generate: prefill all prompt
-        tokens but the last, then decode from it.  Returns [B, T + n] ids."""
+        tokens but the last, then decode from it.  Returns [B, T + n] ids.
+        graph=True decodes with captured steps (the cache capacity must hold
+        the whole generation)."""
         self.reset()
         ids = input_ids.to(self.dev)
         if ids.shape[1] > 1:
             self.prefill(ids[:, :-1])
         tok = ids[:, -1:]
         new = []
-        for _ in range(max_new_tokens):
-            tok = self.decode(tok).argmax(dim=-1, keepdim=True)
+        for i in range(max_new_tokens):
+            if graph:
+                self.decode_graph(tok if i == 0 else None)
+                tok = self._g_next.clone()
+            else:
+                tok = self.decode(tok).argmax(dim=-1, keepdim=True)
             new.append(tok)
             if eos_token_id is not None and bool((tok == eos_token_id).all()):
                 break

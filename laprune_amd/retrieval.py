@@ -322,6 +322,57 @@ class SparseDecoder:
                st)
         return self.out.unsqueeze(2)
 
+    @property
+    def k_cols(self) -> int:
+        """Index-row width of device-plan steps: the largest budget any step
+        within max_tokens can have."""
+        return max(self._k_cap(self.T_max), 1)
+
+    @torch.no_grad()
+    def step_dev(self, q: torch.Tensor, codes: torch.Tensor, keys: torch.Tensor,
+                 vals: torch.Tensor, plans: torch.Tensor) -> torch.Tensor:
+        """One decode step driven by device plans (lap_row_plan [B] int32).
+
+        Every launch argument is fixed (columns = the code buffer's
+        capacity, index rows k_cols wide, sink/local bounds from the config),
+        so the same launches serve every step: capture them once in a graph
+        and rewrite ``plans`` before each replay.  Work past a sequence's
+        lengths exits early in each kernel."""
+        if q.dim() == 4:
+            q = q[:, :, 0, :]
+        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
+        T = min(codes.shape[2], self.T_max)
+        st = N.stream_of(q)
+        qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
+        N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
+               N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
+               N.ptr(self.lut), st)
+        k_cols = self.k_cols
+        if self.cfg.select == "group":
+            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
+                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(plans), k_cols,
+                   self.key_mode, None, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
+                   self.ws_sel.numel(), st)
+            H_idx = Hkv
+        else:
+            sc = self.scores
+            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
+                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(plans), 0,
+                   self.key_mode, N.ptr(sc), None, N.I32, N.ptr(self.ws_sel),
+                   self.ws_sel.numel(), st)
+            N.call("lap_topk_select_ragged", N.ptr(sc), T, B * Hq, 1, Hq, T, N.ptr(plans),
+                   k_cols, self.key_mode, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
+                   self.ws_sel.numel(), st)
+            H_idx = Hq
+        self.last_k = k_cols
+        N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
+               N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, keys.shape[2], D, keys.stride(0),
+               keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
+               N.ptr(self.idx), N.I32, H_idx, k_cols, N.ptr(plans), self.cfg.sink_size,
+               max(self.cfg.local_window, 0), 1.0 / math.sqrt(D), N.ptr(self.out),
+               N.ptr(self.ws_attn), self.ws_attn.numel(), st)
+        return self.out.unsqueeze(2)
+
     @torch.no_grad()
     def step_cached(self, q: torch.Tensor, cache) -> torch.Tensor:
         """One decode step over a ``DecodeKVCache``: candidates are the encoded
@@ -377,6 +428,29 @@ class DenseDecoder:
                    max(rows), 1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws),
                    self.ws.numel(), N.stream_of(q))
             return self.out.unsqueeze(2)
+        return self._dense_uniform(q, keys, vals)
+
+    @torch.no_grad()
+    def step_dev(self, q: torch.Tensor, keys: torch.Tensor, vals: torch.Tensor,
+                 plans: torch.Tensor) -> torch.Tensor:
+        """Dense decode with each sequence's length read from device plans
+        (t_total, tail [0, t_total)); fixed launch arguments, as
+        SparseDecoder.step_dev."""
+        if q.dim() == 4:
+            q = q[:, :, 0, :]
+        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
+        T = keys.shape[2]
+        N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1),
+               N.ptr(keys), N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D,
+               keys.stride(0), keys.stride(1), keys.stride(2), vals.stride(0),
+               vals.stride(1), vals.stride(2), None, N.I32, Hkv, 0, N.ptr(plans), 0, T,
+               1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws), self.ws.numel(),
+               N.stream_of(q))
+        return self.out.unsqueeze(2)
+
+    def _dense_uniform(self, q, keys, vals):
+        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
+        T = keys.shape[2]
         N.call("lap_dense_attn_decode", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
                N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D, keys.stride(0),
                keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),

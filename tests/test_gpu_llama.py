@@ -106,3 +106,50 @@ def test_generate_shapes(dev):
     out = lm.generate(ids, max_new_tokens=12)
     assert out.shape == (2, 112) and torch.equal(out[:, :100].cpu(), ids)
     assert lm.lengths == [111, 111]
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_captured_decode_matches_eager(dev, ragged):
+    """Decode steps replayed from one captured graph (device plans, device
+    positions, per-sequence flush ranges) follow the eager steps, across
+    each sequence's 64-token flush."""
+    from laprune_amd.llama import LAPruneLlama, LAPruneSettings, random_model
+    from laprune_amd.retrieval import RetrievalConfig
+    cfg = _tiny()
+    s = LAPruneSettings(apply_layers=[1, 2],
+                        retrieval=RetrievalConfig(topk=32, sink_size=4, local_window=64))
+    cbs = _codebooks([1, 2])
+    B = 3
+    eager = LAPruneLlama(random_model(cfg, dev, seed=8), cbs, s, batch=B, capacity=512)
+    graph = LAPruneLlama(random_model(cfg, dev, seed=8), cbs, s, batch=B, capacity=512)
+    lens = [150, 90, 200] if ragged else [150] * B
+    g = torch.Generator().manual_seed(9)
+    seqs = [torch.randint(0, VOCAB, (1, n + 80), generator=g).to(dev) for n in lens]
+    for lm in (eager, graph):
+        if ragged:
+            for b, n in enumerate(lens):
+                lm.prefill_row(b, seqs[b][:, :n])
+        else:
+            lm.prefill(torch.cat([sq[:, :n] for sq, n in zip(seqs, lens)]))
+    for i in range(80):
+        tok = torch.cat([sq[:, n + i:n + i + 1] for sq, n in zip(seqs, lens)])
+        want = eager.decode(tok)
+        got = graph.decode_graph(tok)
+        assert _rel(got, want) < 3e-2, i
+        assert torch.equal(graph.next_tokens(), got.argmax(dim=-1, keepdim=True))
+    for a, b in zip(eager.states, graph.states):
+        assert a.cache.lengths == b.cache.lengths
+        assert a.cache.encoded_lens == b.cache.encoded_lens
+    assert graph.states[1].cache.encoded_lens == [n + 64 for n in lens]
+
+
+def test_generate_with_captured_steps(dev):
+    from laprune_amd.llama import LAPruneLlama, LAPruneSettings, random_model
+    from laprune_amd.retrieval import RetrievalConfig
+    s = LAPruneSettings(apply_layers=[1, 2], retrieval=RetrievalConfig(topk=16))
+    lm = LAPruneLlama(random_model(_tiny(), dev, seed=6), _codebooks([1, 2]), s, batch=2,
+                      capacity=256)
+    ids = torch.randint(0, VOCAB, (2, 100), generator=torch.Generator().manual_seed(7))
+    out = lm.generate(ids, max_new_tokens=70, graph=True)
+    assert out.shape == (2, 170) and torch.equal(out[:, :100].cpu(), ids)
+    assert lm.lengths == [169, 169] and lm.states[1].cache.encoded_lens == [163, 163]
