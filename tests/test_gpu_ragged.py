@@ -285,3 +285,32 @@ def test_ragged_cache_flushes_per_sequence(dev, orc):
         want, _ = orc.encode(ks[b][0, :, :e].float().reshape(-1, D).numpy(), cb.numpy())
         got = cache.codes[b, :, :e].reshape(-1, M).cpu().numpy()
         assert np.array_equal(got, want), b
+
+
+def test_encode_keys_ranges_per_sequence(dev, orc):
+    """Per-sequence device ranges: codes inside each range are exact, every
+    other code byte is untouched (an empty range and a partial one)."""
+    from laprune_amd import _native as N
+    from laprune_amd.aq_kernels import aq_encode_prepare
+    g = torch.Generator().manual_seed(370)
+    B, H, T, D, M = 3, 2, 300, 128, 32
+    keys = (torch.randn(B, H, T, D, generator=g) * 1.3).bfloat16()
+    cb = torch.randn(M, 256, D, generator=g) * 0.02
+    ranges = torch.tensor([[10, 74], [0, 0], [100, 137]], dtype=torch.int32)
+    kd, cbd = keys.to(dev), cb.to(dev)
+    prep = aq_encode_prepare(cbd)
+    codes = torch.full((B, H, T + 16, M), 0xAB, dtype=torch.uint8, device=dev)
+    rd = ranges.to(dev)
+    N.call("lap_encode_keys_ranges", N.ptr(kd), N.BF16, kd.stride(0), kd.stride(1), kd.stride(2),
+           B, H, N.ptr(rd), 64, D, N.ptr(cbd), M, 256, N.ptr(prep), prep.numel(), N.ptr(codes),
+           codes.stride(0), codes.stride(1), codes.stride(2), N.stream_of(codes))
+    torch.cuda.synchronize()
+    got = codes.cpu().numpy()
+    for b in range(B):
+        t0, t1 = (int(x) for x in ranges[b])
+        for h in range(H):
+            if t1 > t0:
+                want, _ = orc.encode(keys[b, h, t0:t1].float().numpy(), cb.numpy())
+                assert np.array_equal(got[b, h, t0:t1], want), (b, h)
+            outside = np.concatenate([got[b, h, :t0], got[b, h, t1:]])
+            assert np.all(outside == 0xAB), (b, h)
