@@ -19,7 +19,12 @@ so that the 256 MB Infinity Cache cannot serve the step from cache.
                  timed with HIP events around graph replays on the launch
                  stream (inside the timed region's second half).
 ``ms_per_step``  wall time of one full sparse decode step.
-``dense_step_us`` the same GPU's split-K flash-decode over all 131072 tokens.
+``dense_step_us`` the same GPU's split-K flash-decode over all 131072 tokens
+                 (this build's own MFMA kernel, the comparator of record).
+``sdpa_step_us`` torch's scaled_dot_product_attention (flash / efficient
+                 backends only) for the same decode, K/V expanded to the 32
+                 query heads outside the timed region: the stock framework
+                 decode, reported beside the comparator of record.
 ``cpu_baseline`` the reference's fp32 PyTorch scoring + bf16 cast + top-k
                  path (restated in oracle/ref_path.py) on the host cores.
 ``encode``       configs[2] (C3): greedy AQ encode of one 64-token flush of
@@ -166,6 +171,59 @@ def traffic_from_profile() -> dict | None:
     try:
         return json.loads(p.read_text())
     except (OSError, ValueError):
+        return None
+
+
+def sdpa_decode_seconds(args, kv_sets, q_sets) -> float | None:
+    """torch SDPA decode over all T tokens (flash / efficient backends only;
+    the math path is not used), graph-replayed like the other legs.  None when
+    no fused backend serves the shape."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    G = HQ // HKV
+    try:
+        kv = [(k[:, :, :T].repeat_interleave(G, dim=1), v[:, :, :T].repeat_interleave(G, dim=1))
+              for k, v in kv_sets[:2]]
+        qs = q_sets[:2]
+
+        def step(i):
+            k, v = kv[i % 2]
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return F.scaled_dot_product_attention(qs[i % 2], k, v, scale=1.0 / math.sqrt(D))
+
+        for i in range(3):
+            step(i)
+        torch.cuda.synchronize()
+        run = step
+        if not args.eager:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                step(0)
+                step(1)
+            torch.cuda.current_stream().wait_stream(s)
+            graphs = []
+            for j in range(2):
+                gph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gph):
+                    step(j)
+                graphs.append(gph)
+            run = lambda i: graphs[i % 2].replay()  # noqa: E731
+        for i in range(args.warmup):
+            run(i)
+        log(f"timing {args.steps} SDPA decode steps")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            run(i)
+        torch.cuda.synchronize()
+        out = (time.perf_counter() - t0) / args.steps
+        del kv
+        torch.cuda.empty_cache()
+        return out
+    except RuntimeError as e:  # no fused SDPA backend for this shape
+        log(f"SDPA decode not timed: {e}")
         return None
 
 
@@ -390,6 +448,9 @@ def main():
     torch.cuda.synchronize()
     dense_s = (time.perf_counter() - t0) / args.steps
 
+    # ---- stock framework decode: torch SDPA (fused backends only)
+    sdpa_s = sdpa_decode_seconds(args, kv_sets, q_sets)
+
     # ---- scorer kernel duration: HIP events on the launch stream around a
     # graph of back-to-back scorer launches over the rotating code sets.
     log("timing the scorer kernel")
@@ -469,6 +530,8 @@ def main():
         "dense_step_us": round(dense_s * 1e6, 2),
         "speedup_vs_dense": round(dense_s / sparse_s, 3),
         "dense_hbm_gbs": round(2 * HKV * T * D * 2 / dense_s / 1e9, 1),
+        "sdpa_step_us": None if sdpa_s is None else round(sdpa_s * 1e6, 2),
+        "speedup_vs_sdpa": None if sdpa_s is None else round(sdpa_s / sparse_s, 3),
         "score_kernel_us": round(score_us, 3),
         "selection_check": ok,
         "encode": {
