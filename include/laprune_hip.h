@@ -363,12 +363,13 @@ int lap_encode_keys(const void* keys, int key_dtype,
  * captured graph: the token range of sequence b is read from device memory,
  * ranges[2b] .. ranges[2b+1] (empty when the sequence has no full encode
  * buffer this step), at most max_len tokens (the decode group size).  Replaces
- * the same tail encode, aq_evaluation.py:367-405, done per sequence.  Rows past
- * a range are not touched; workgroups with no row in range exit at once.
- * No residual norms. */
+ * the same tail encode, aq_evaluation.py:367-405, done per sequence.  t_cap is
+ * the token capacity of both buffers: a range is clipped to [0, t_cap), so no
+ * range read from memory can address outside them.  Rows past a range are not
+ * touched; workgroups with no row in range exit at once.  No residual norms. */
 int lap_encode_keys_ranges(const void* keys, int key_dtype,
                            int64_t k_sb, int64_t k_sh, int64_t k_st,
-                           int B, int Hkv, const int32_t* ranges, int max_len, int D,
+                           int B, int Hkv, const int32_t* ranges, int max_len, int t_cap, int D,
                            const float* codebooks, int M, int K,
                            const void* prep, size_t prep_bytes,
                            uint8_t* codes, int64_t c_sb, int64_t c_sh, int64_t c_st,

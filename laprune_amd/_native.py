@@ -78,8 +78,8 @@ SIGNATURES = {
     "lap_encode_greedy": [vp, i64, i32, i32, vp, i32, i32, vp, sz, vp, i64, vp, vp],
     "lap_encode_keys": [vp, i32, i64, i64, i64, i32, i32, i32, i32, i32, vp, i32, i32, vp, sz,
                         vp, i64, i64, i64, vp, vp],
-    "lap_encode_keys_ranges": [vp, i32, i64, i64, i64, i32, i32, vp, i32, i32, vp, i32, i32, vp,
-                               sz, vp, i64, i64, i64, vp],
+    "lap_encode_keys_ranges": [vp, i32, i64, i64, i64, i32, i32, vp, i32, i32, i32, vp, i32, i32,
+                               vp, sz, vp, i64, i64, i64, vp],
 }
 
 _lock = threading.Lock()

@@ -250,7 +250,8 @@ class DecodeKVCache:
         k, c = self.k, self.codes
         N.call("lap_encode_keys_ranges", N.ptr(k), N.dtype_code(k.dtype), k.stride(0),
                k.stride(1), k.stride(2), self.B, self.Hkv, N.ptr(ranges), self.group_size,
-               self.D, N.ptr(self.cb), self.M, self.K, N.ptr(self.prep), self.prep.numel(),
+               self.capacity, self.D, N.ptr(self.cb), self.M, self.K, N.ptr(self.prep),
+               self.prep.numel(),
                N.ptr(c), c.stride(0), c.stride(1), c.stride(2), N.stream_of(k))
 
     def keys(self) -> torch.Tensor:

@@ -68,6 +68,7 @@ struct RowMap {
   int64_t c_sb, c_sh, c_st;
   int L, Hs, t0;
   const int32_t* ranges;  // [B][2] or null
+  int t_cap;              // with ranges: rows outside [0, t_cap) are not live
   __device__ __forceinline__ int64_t off(int i, int64_t sb, int64_t sh, int64_t st) const {
     const int sg = i / L, j = i - sg * L;
     const int b = sg / Hs, h = sg - b * Hs;
@@ -76,8 +77,9 @@ struct RowMap {
   }
   __device__ __forceinline__ bool live(int i) const {
     if (!ranges) return true;
-    const int sg = i / L, b = sg / Hs;
-    return i - sg * L < ranges[2 * b + 1] - ranges[2 * b];
+    const int sg = i / L, b = sg / Hs, j = i - sg * L;
+    const int lo = ranges[2 * b], hi = min(ranges[2 * b + 1], t_cap);
+    return lo >= 0 && lo + j < hi;
   }
   __device__ __forceinline__ float xval(int i, int d) const {
     return load_as_f32(x, off(i, x_sb, x_sh, x_st) + d, x_dtype);
@@ -697,7 +699,7 @@ extern "C" int lap_encode_greedy(const float* x, int64_t x_row_stride, int N, in
   LAP_CHECK(N >= 0 && D > 0 && M > 0, "lap_encode_greedy: bad sizes");
   LAP_CHECK(x_row_stride >= D && codes_row_stride >= M, "lap_encode_greedy: bad row strides");
   const RowMap rm{x, LAP_DTYPE_F32, 0, 0, x_row_stride, codes_out, 0, 0, codes_row_stride,
-                  N > 0 ? N : 1, 1, 0, nullptr};
+                  N > 0 ? N : 1, 1, 0, nullptr, 0};
   return run_encode(rm, N, D, codebooks, M, K, prep, prep_bytes, resid_norm, stream,
                     "lap_encode_greedy");
 }
@@ -718,14 +720,14 @@ extern "C" int lap_encode_keys(const void* keys, int key_dtype, int64_t k_sb, in
   const int64_t n = (int64_t)B * Hkv * (t1 - t0);
   LAP_CHECK(n <= (int64_t)1 << 30, "lap_encode_keys: too many rows");
   const RowMap rm{keys, key_dtype, k_sb, k_sh, k_st, codes, c_sb, c_sh, c_st,
-                  t1 > t0 ? t1 - t0 : 1, Hkv, t0, nullptr};
+                  t1 > t0 ? t1 - t0 : 1, Hkv, t0, nullptr, 0};
   return run_encode(rm, (int)n, D, codebooks, M, K, prep, prep_bytes, resid_norm, stream,
                     "lap_encode_keys");
 }
 
 extern "C" int lap_encode_keys_ranges(const void* keys, int key_dtype, int64_t k_sb,
                                       int64_t k_sh, int64_t k_st, int B, int Hkv,
-                                      const int32_t* ranges, int max_len, int D,
+                                      const int32_t* ranges, int max_len, int t_cap, int D,
                                       const float* codebooks, int M, int K, const void* prep,
                                       size_t prep_bytes, uint8_t* codes, int64_t c_sb,
                                       int64_t c_sh, int64_t c_st, lap_stream_t stream) {
@@ -734,13 +736,13 @@ extern "C" int lap_encode_keys_ranges(const void* keys, int key_dtype, int64_t k
   LAP_CHECK(key_dtype == LAP_DTYPE_F32 || key_dtype == LAP_DTYPE_F16 ||
                 key_dtype == LAP_DTYPE_BF16,
             "lap_encode_keys_ranges: keys must be f32, f16 or bf16");
-  LAP_CHECK(B > 0 && Hkv > 0 && D > 0 && M > 0 && max_len > 0,
+  LAP_CHECK(B > 0 && Hkv > 0 && D > 0 && M > 0 && max_len > 0 && t_cap > 0,
             "lap_encode_keys_ranges: bad sizes");
   LAP_CHECK(k_st >= D && c_st >= M, "lap_encode_keys_ranges: token strides smaller than D / M");
   const int64_t n = (int64_t)B * Hkv * max_len;
   LAP_CHECK(n <= (int64_t)1 << 30, "lap_encode_keys_ranges: too many rows");
   const RowMap rm{keys, key_dtype, k_sb, k_sh, k_st, codes, c_sb, c_sh, c_st,
-                  max_len, Hkv, 0, ranges};
+                  max_len, Hkv, 0, ranges, t_cap};
   return run_encode(rm, (int)n, D, codebooks, M, K, prep, prep_bytes, nullptr, stream,
                     "lap_encode_keys_ranges");
 }

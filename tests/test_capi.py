@@ -38,7 +38,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.lap_abi_version() == 4
+    assert lib.lap_abi_version() == 5
 
 
 def _err(lib):

@@ -108,8 +108,8 @@ def test_generate_shapes(dev):
     assert lm.lengths == [111, 111]
 
 
-@pytest.mark.parametrize("ragged", [False, True])
-def test_captured_decode_matches_eager(dev, ragged):
+@pytest.mark.parametrize("ragged,select", [(False, "group"), (True, "group"), (True, "head")])
+def test_captured_decode_matches_eager(dev, ragged, select):
     """Decode steps replayed from one captured graph (device plans, device
     positions, per-sequence flush ranges) follow the eager steps, across
     each sequence's 64-token flush."""
@@ -117,7 +117,8 @@ def test_captured_decode_matches_eager(dev, ragged):
     from laprune_amd.retrieval import RetrievalConfig
     cfg = _tiny()
     s = LAPruneSettings(apply_layers=[1, 2],
-                        retrieval=RetrievalConfig(topk=32, sink_size=4, local_window=64))
+                        retrieval=RetrievalConfig(topk=32, sink_size=4, local_window=64,
+                                                  select=select))
     cbs = _codebooks([1, 2])
     B = 3
     eager = LAPruneLlama(random_model(cfg, dev, seed=8), cbs, s, batch=B, capacity=512)

@@ -296,16 +296,30 @@ def test_encode_keys_ranges_per_sequence(dev, orc):
     B, H, T, D, M = 3, 2, 300, 128, 32
     keys = (torch.randn(B, H, T, D, generator=g) * 1.3).bfloat16()
     cb = torch.randn(M, 256, D, generator=g) * 0.02
+    # the last range runs past the buffers' capacity T + 16 and is clipped there
     ranges = torch.tensor([[10, 74], [0, 0], [100, 137]], dtype=torch.int32)
+    ranges_clip = torch.tensor([[10, 74], [0, 0], [290, 350]], dtype=torch.int32)
     kd, cbd = keys.to(dev), cb.to(dev)
     prep = aq_encode_prepare(cbd)
     codes = torch.full((B, H, T + 16, M), 0xAB, dtype=torch.uint8, device=dev)
     rd = ranges.to(dev)
     N.call("lap_encode_keys_ranges", N.ptr(kd), N.BF16, kd.stride(0), kd.stride(1), kd.stride(2),
-           B, H, N.ptr(rd), 64, D, N.ptr(cbd), M, 256, N.ptr(prep), prep.numel(), N.ptr(codes),
-           codes.stride(0), codes.stride(1), codes.stride(2), N.stream_of(codes))
+           B, H, N.ptr(rd), 64, T, D, N.ptr(cbd), M, 256, N.ptr(prep), prep.numel(),
+           N.ptr(codes), codes.stride(0), codes.stride(1), codes.stride(2), N.stream_of(codes))
     torch.cuda.synchronize()
     got = codes.cpu().numpy()
+    # clipping: keys hold T tokens, so [290, 350) encodes 290..299 only
+    codes2 = torch.full_like(codes, 0xAB)
+    rc = ranges_clip.to(dev)
+    N.call("lap_encode_keys_ranges", N.ptr(kd), N.BF16, kd.stride(0), kd.stride(1), kd.stride(2),
+           B, H, N.ptr(rc), 64, T, D, N.ptr(cbd), M, 256, N.ptr(prep), prep.numel(),
+           N.ptr(codes2), codes2.stride(0), codes2.stride(1), codes2.stride(2),
+           N.stream_of(codes2))
+    torch.cuda.synchronize()
+    got2 = codes2.cpu().numpy()
+    want2, _ = orc.encode(keys[2, 0, 290:300].float().numpy(), cb.numpy())
+    assert np.array_equal(got2[2, 0, 290:300], want2)
+    assert np.all(got2[2, :, 300:] == 0xAB) and np.all(got2[2, :, :290] == 0xAB)
     for b in range(B):
         t0, t1 = (int(x) for x in ranges[b])
         for h in range(H):
