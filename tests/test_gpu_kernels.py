@@ -301,7 +301,11 @@ def test_dense_attn_decode(dev, K, orc, T):
 
 # --------------------------------------------------------------- A6 encode
 
-@pytest.mark.parametrize("N,D", [(512, 128), (37, 64), (3, 256)])
+# 20000 and 40000 rows take the 32- and 64-row workgroup tiles (two and four
+# row groups sharing each codebook fragment) on a 256-CU device; 40003 leaves a
+# partial last tile.
+@pytest.mark.parametrize("N,D", [(512, 128), (37, 64), (3, 256), (20000, 128), (40003, 128),
+                                 (40000, 64)])
 def test_encode_bit_exact(dev, K, orc, N, D):
     g = _gen(100 + N)
     M, Kc = 32, 256
@@ -309,9 +313,15 @@ def test_encode_bit_exact(dev, K, orc, N, D):
     cb = torch.randn(M, Kc, D, generator=g) * 0.02
     codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
     torch.cuda.synchronize()
-    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
-    assert np.array_equal(codes.cpu().numpy(), want_c)
-    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+    # rows are encoded independently: large launches are checked on the first
+    # and last 128 rows (the partial last tile included) and 512 random rows
+    rows = np.arange(N)
+    if N > 4096:
+        pick = torch.randperm(N - 256, generator=g)[:512].numpy() + 128
+        rows = np.unique(np.concatenate([np.arange(128), np.arange(N - 128, N), pick]))
+    want_c, want_r = orc.encode(x.numpy()[rows], cb.numpy())
+    assert np.array_equal(codes.cpu().numpy()[rows], want_c)
+    assert np.array_equal(rn.cpu().numpy()[rows].view(np.uint32), want_r.view(np.uint32))
 
 
 @pytest.mark.parametrize("Kc,D", [(60, 64), (48, 128), (16, 64), (240, 128)])
