@@ -601,6 +601,257 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
     rnorm[row0 + tid] = sqrtf(s.rn[tid]);
 }
 
+// ------------------------------------------------ large launches (prefill)
+// The same stage as enc_stage for 64 rows per workgroup.  A 16-row workgroup
+// holds its stage fragments (64 KiB at K = 256, D = 128) in registers, twice
+// over for the prefetch, so register space caps a CU at 32 rows in flight;
+// and the exact recheck makes every stage a chain of dependent latencies, so
+// throughput follows the rows in flight.  Here 16 waves (4 row groups x 4
+// tile quarters) share one LDS copy of the stage's fragments, the next
+// stage's slice is fetched into registers (64 B per thread) while the
+// current stage runs, and each of the 64 rows keeps its own 16-lane recheck
+// group: 64 rows per CU, each stage costing what it costs a 16-row workgroup.
+constexpr int kTileRows = 64;
+constexpr int kTileThreads = 1024;
+
+template <int D>
+struct TileShared {
+  static constexpr int KS = D / 16;
+  uint2 frag[16 * KS * 64];    // stage fragments [tile][ks][lane], K <= 256
+  float r[kTileRows][D];
+  uint16_t rb[kTileRows][D];   // bf16(r): the MFMA A operand
+  float rn[kTileRows];
+  float u[4][kTileRows];       // per tile quarter: min of G + eps per row
+  uint32_t cnt[kTileRows];
+  uint8_t list[kTileRows][256];
+};
+
+// This thread's slice of stage m's fragments: uint4 i of the stage lies at
+// thread i % 1024, slot i / 1024 (clamped into the stage; at most 4 slots).
+// Four named members, not an array, so that they stay in registers.
+struct TileSlice {
+  uint4 v0, v1, v2, v3;
+};
+template <int D>
+__device__ __forceinline__ TileSlice tile_frag_load(const uint2* __restrict__ frag, int m, int NT,
+                                                    int tid) {
+  constexpr int KS = D / 16;
+  const int n4 = NT * KS * 32;  // uint4 per stage
+  const uint4* src = reinterpret_cast<const uint4*>(frag + (int64_t)m * NT * KS * 64);
+  TileSlice p;
+  p.v0 = src[min(tid, n4 - 1)];
+  p.v1 = src[min(tid + kTileThreads, n4 - 1)];
+  p.v2 = src[min(tid + 2 * kTileThreads, n4 - 1)];
+  p.v3 = src[min(tid + 3 * kTileThreads, n4 - 1)];
+  return p;
+}
+template <int D>
+__device__ __forceinline__ void tile_frag_store(const TileSlice& p, uint2* s_frag, int NT,
+                                                int tid) {
+  constexpr int KS = D / 16;
+  const int n4 = NT * KS * 32;
+  uint4* dst = reinterpret_cast<uint4*>(s_frag);
+  if (tid < n4) dst[tid] = p.v0;
+  if (tid + kTileThreads < n4) dst[tid + kTileThreads] = p.v1;
+  if (tid + 2 * kTileThreads < n4) dst[tid + 2 * kTileThreads] = p.v2;
+  if (tid + 3 * kTileThreads < n4) dst[tid + 3 * kTileThreads] = p.v3;
+}
+
+template <int D>
+__global__ __launch_bounds__(kTileThreads) void encode_tile_kernel(
+    RowMap rm, int N, const float* __restrict__ cb, int M,
+    int K, const uint2* __restrict__ frag, const float* __restrict__ cn,
+    const float* __restrict__ scn, float* __restrict__ rnorm) {
+  constexpr int KS = D / 16, L = D / 16, CAP = 2, TPW = 4;  // CAP 2: fits 128 VGPRs
+  extern __shared__ __attribute__((aligned(16))) char tile_smem[];
+  TileShared<D>& s = *reinterpret_cast<TileShared<D>*>(tile_smem);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = wave >> 2, q = wave & 3;  // row group, tile quarter
+  const int row0 = blockIdx.x * kTileRows;
+  const int NT = K / 16;
+  if (rm.ranges) {  // a workgroup with no live row leaves at once (same test in every thread)
+    bool any = false;
+    for (int r = 0; r < kTileRows; ++r) any = any || (row0 + r < N && rm.live(row0 + r));
+    if (!any) return;
+  }
+  TileSlice pf = tile_frag_load<D>(frag, 0, NT, tid);
+  for (int i = tid; i < kTileRows * D; i += kTileThreads) {
+    const int r = i / D, d = i - r * D;
+    const float v = (row0 + r < N && rm.live(row0 + r)) ? rm.xval(row0 + r, d) : 0.f;
+    s.r[r][d] = v;
+    s.rb[r][d] = __builtin_bit_cast(uint16_t, (__bf16)v);
+  }
+  if (tid < kTileRows) s.cnt[tid] = 0;
+  tile_frag_store<D>(pf, s.frag, NT, tid);
+  __syncthreads();
+  const int grp = wave * 4 + (lane >> 4), j = lane & 15;  // recheck group = row
+  {
+    const float* rr = s.r[grp] + j * L;
+    float a2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < L; ++t) a2 = __builtin_fmaf(rr[t], rr[t], a2);
+    a2 = row_fold16(a2);
+    if (j == 0) s.rn[grp] = a2;
+  }
+  __syncthreads();
+
+  for (int m = 0; m < M; ++m) {
+    // next stage's fragments: in flight for the whole stage (re-requests the
+    // last stage on the last pass, so the loads are unconditional)
+    pf = tile_frag_load<D>(frag, min(m + 1, M - 1), NT, tid);
+    // ---- coarse pass: rows rg*16.., tiles q, q+4, q+8, q+12
+    float cnv[TPW], scv[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = min(q + 4 * i, NT - 1);
+      const int64_t ci = (int64_t)m * K + tile * 16 + (lane & 15);
+      cnv[i] = cn[ci];
+      scv[i] = scn[ci];
+    }
+    bf16x4_t a[KS];
+    {
+      const uint16_t* rr = s.rb[rg * 16 + (lane & 15)] + 4 * (lane >> 4);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        a[ks] = __builtin_bit_cast(bf16x4_t, *reinterpret_cast<const uint2*>(rr + ks * 16));
+    }
+    float g_lo[TPW][4];
+    float umin[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = min(q + 4 * i, NT - 1);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+            a[ks], __builtin_bit_cast(bf16x4_t, s.frag[(tile * KS + ks) * 64 + lane]), acc, 0,
+            0, 0);
+      const bool live = q + 4 * i < NT;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float rn = s.rn[rg * 16 + 4 * (lane >> 4) + e];
+        const float srn = __builtin_amdgcn_sqrtf(rn);
+        const float A = rn + cnv[i];
+        const float dm = acc[e];
+        const float g = A - 2.0f * dm;
+        const float eps = 0x1.02p-6f * (srn * scv[i]) + 0x1p-21f * (fabsf(A) + 2.0f * fabsf(dm)) +
+                          0x1p-116f * (1.0f + srn + scv[i]);
+        g_lo[i][e] = live ? g - eps : INFINITY;
+        umin[e] = fminf(umin[e], live ? g + eps : INFINITY);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) umin[e] = row_min16(umin[e]);
+    if ((lane & 15) == 0)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s.u[q][rg * 16 + 4 * (lane >> 4) + e] = umin[e];
+    lds_barrier();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = rg * 16 + 4 * (lane >> 4) + e;
+      const float U = fminf(fminf(s.u[0][row], s.u[1][row]), fminf(s.u[2][row], s.u[3][row]));
+      uint32_t keep = 0;
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) keep |= (uint32_t)(q + 4 * i < NT && !(g_lo[i][e] > U)) << i;
+      if (keep) {
+        uint32_t slot = atomicAdd(&s.cnt[row], (uint32_t)__builtin_popcount(keep));
+#pragma unroll
+        for (int i = 0; i < TPW; ++i)
+          if (keep & (1u << i)) s.list[row][slot++] = (uint8_t)((q + 4 * i) * 16 + (lane & 15));
+      }
+    }
+    lds_barrier();
+    // ---- exact recheck: group grp owns row grp (same rules as enc_stage)
+    {
+      const int row = grp;
+      float rc[L];
+#pragma unroll
+      for (int t = 0; t < L; t += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&s.r[row][j * L + t]);
+        rc[t] = v.x;
+        rc[t + 1] = v.y;
+        rc[t + 2] = v.z;
+        rc[t + 3] = v.w;
+      }
+      const float rn = s.rn[row];
+      const uint32_t n = s.cnt[row];
+      if (j == 0) s.cnt[row] = 0;
+      float bc[L];
+#pragma unroll
+      for (int t = 0; t < L; ++t) bc[t] = 0.f;
+      float best = 0.f;
+      int bk = -1;
+      for (uint32_t base = 0; base < n; base += CAP) {
+        const uint32_t word = *reinterpret_cast<const uint16_t*>(&s.list[row][base]);
+        int kq[CAP];
+        float c[CAP][L], cnk[CAP];
+#pragma unroll
+        for (int qq = 0; qq < CAP; ++qq) {
+          kq[qq] = base + qq < n ? (int)((word >> (8 * qq)) & 0xffu) : (int)(word & 0xffu);
+          const float* cr = cb + ((int64_t)m * K + kq[qq]) * D + j * L;
+#pragma unroll
+          for (int t = 0; t < L; t += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(cr + t);
+            c[qq][t] = v.x;
+            c[qq][t + 1] = v.y;
+            c[qq][t + 2] = v.z;
+            c[qq][t + 3] = v.w;
+          }
+          cnk[qq] = cn[(int64_t)m * K + kq[qq]];
+        }
+#pragma unroll
+        for (int qq = 0; qq < CAP; ++qq) {
+          float dot = 0.f;
+#pragma unroll
+          for (int t = 0; t < L; ++t) dot = __builtin_fmaf(rc[t], c[qq][t], dot);
+          dot = row_fold16(dot);
+          const float E = (rn + cnk[qq]) - 2.0f * dot;
+          const int k = kq[qq];
+          if (base + qq < n && !(E != E) && E != INFINITY &&
+              (bk < 0 || E < best || (E == best && k < bk))) {
+            best = E;
+            bk = k;
+#pragma unroll
+            for (int t = 0; t < L; ++t) bc[t] = c[qq][t];
+          }
+        }
+      }
+      const int code = bk < 0 ? 0 : bk;
+      if (bk < 0) {
+        const float* cr = cb + (int64_t)m * K * D + j * L;
+#pragma unroll
+        for (int t = 0; t < L; ++t) bc[t] = cr[t];
+      }
+      float a2 = 0.f;
+#pragma unroll
+      for (int t = 0; t < L; t += 4) {
+        float4 r4;
+        r4.x = rc[t] - bc[t];
+        r4.y = rc[t + 1] - bc[t + 1];
+        r4.z = rc[t + 2] - bc[t + 2];
+        r4.w = rc[t + 3] - bc[t + 3];
+        *reinterpret_cast<float4*>(&s.r[row][j * L + t]) = r4;
+        *reinterpret_cast<uint2*>(&s.rb[row][j * L + t]) = bf16x4_bits(r4);
+        a2 = __builtin_fmaf(r4.x, r4.x, a2);
+        a2 = __builtin_fmaf(r4.y, r4.y, a2);
+        a2 = __builtin_fmaf(r4.z, r4.z, a2);
+        a2 = __builtin_fmaf(r4.w, r4.w, a2);
+      }
+      a2 = row_fold16(a2);
+      if (j == 0) {
+        s.rn[row] = a2;
+        if (row0 + row < N && rm.live(row0 + row)) rm.crow(row0 + row)[m] = (uint8_t)code;
+      }
+    }
+    // every wave has read this stage's fragments (before the first barrier):
+    // the next stage's may replace them
+    tile_frag_store<D>(pf, s.frag, NT, tid);
+    lds_barrier();
+  }
+  if (tid < kTileRows && rnorm && row0 + tid < N && rm.live(row0 + tid))
+    rnorm[row0 + tid] = sqrtf(s.rn[tid]);
+}
+
 }  // namespace
 }  // namespace lap
 
@@ -649,6 +900,22 @@ extern "C" int lap_encode_prepare(const float* codebooks, int M, int K, int D, v
   return LAP_OK;
 }
 
+// The 64-row workgroups pay off once every CU gets several of them; smaller
+// launches (a decode flush) keep 16-row workgroups for their parallelism.
+// D = 256 and K > 256 stay on the 16-row kernel.  LAPRUNE_ENCODE_TILE=0|1
+// forces the choice.
+static bool encode_use_tile(int N, int D, int K) {
+  if (!(D == 64 || D == 128) || K > 256) return false;
+  static const int forced = [] {
+    const char* e = getenv("LAPRUNE_ENCODE_TILE");
+    return e ? atoi(e) : -1;
+  }();
+  if (forced == 0 || forced == 1) return forced == 1;
+  DevInfo di;
+  const int cus = device_info(&di) == LAP_OK ? di.cu_count : 256;
+  return (int64_t)N >= (int64_t)kTileRows * 2 * cus;
+}
+
 // Shared checks and launch of both encode entry points.
 static int run_encode(const RowMap& rm, int N, int D, const float* codebooks, int M, int K,
                       const void* prep, size_t prep_bytes, float* resid_norm,
@@ -665,6 +932,20 @@ static int run_encode(const RowMap& rm, int N, int D, const float* codebooks, in
   LAP_CHECK((reinterpret_cast<uintptr_t>(p.ct) & 15) == 0, "%s: prep misaligned", who);
   if (N == 0) return LAP_OK;
   hipStream_t st = as_stream(stream);
+  if (K % 16 == 0 && encode_impl_mfma() && encode_use_tile(N, D, K)) {
+    dim3 grid((N + kTileRows - 1) / kTileRows);
+    const uint2* fr = reinterpret_cast<const uint2*>(p.frag);
+    if (D == 64)
+      hipLaunchKernelGGL(encode_tile_kernel<64>, grid, dim3(kTileThreads),
+                         sizeof(TileShared<64>), st, rm, N, codebooks, M, K, fr, p.cn, p.scn,
+                         resid_norm);
+    else
+      hipLaunchKernelGGL(encode_tile_kernel<128>, grid, dim3(kTileThreads),
+                         sizeof(TileShared<128>), st, rm, N, codebooks, M, K, fr, p.cn, p.scn,
+                         resid_norm);
+    LAP_LAUNCH_CHECK("encode_tile_kernel");
+    return LAP_OK;
+  }
   if (K % 16 == 0 && encode_impl_mfma()) {
     dim3 g16((N + 15) / 16);
     const uint2* fr = reinterpret_cast<const uint2*>(p.frag);
