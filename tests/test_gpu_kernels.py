@@ -48,6 +48,8 @@ def test_lut_build_bit_exact(dev, K, orc, qdt, layout):
 
 @pytest.mark.parametrize("Hq,D,M,Kc,G,layout", [
     (512, 128, 32, 256, 4, "gmkg"),   # batch 16 x 32 heads: 64-head tiles
+    (520, 128, 32, 256, 4, "gmkg"),   # ... with a partial last head tile
+    (200, 64, 32, 256, 4, "hmk"),     # ... D = 64, reference layout
     (40, 128, 32, 256, 4, "gmkg"),    # partial head tile
     (24, 128, 5, 100, 2, "gmkg"),     # G = 2, M*K not a multiple of the row tile
     (64, 256, 8, 64, 4, "hmk"),       # D = 256
