@@ -24,6 +24,10 @@
 // linear copy.
 #include "common.h"
 
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
 namespace lap {
 namespace {
 
@@ -245,6 +249,130 @@ __global__ __launch_bounds__(kThreads) void lut_dpp_kernel(
   }
 }
 
+// ---- fp32 MFMA form.  v_mfma_f32_16x16x4f32 accumulates its four k terms
+// into each output as four fused multiply-adds in ascending k: measured on
+// gfx950 bit for bit against a per-element fmaf chain (random, mixed-exponent,
+// cancelling, subnormal and signed-zero operands, K up to 512), and checked
+// here by every LUT test against the CPU oracle.  So a chain of these MFMAs
+// over k-blocks 0, 4, 8, ... from a zero accumulator is the contract's fmaf
+// chain over d, on the matrix cores.
+//   A = q (16 heads: lane l supplies head l % 16, d = 4 j + l / 16)
+//   B = C^T (16 codebook rows: lane l supplies row l % 16, d = 4 j + l / 16)
+//   D: lane l holds heads 4 (l / 16) + e, row l % 16: the four heads of one
+//      KV group for one row, 8 contiguous bytes of the interleaved layout.
+// In LDS each head or row keeps its d in the order (d % 4, d / 4): lane group
+// l / 16 then finds the operands of four consecutive k-blocks in 16
+// contiguous bytes, one ds_read_b128 per four MFMAs.  Pitch D + 4 floats:
+// the 16 lanes of one pass land on 64 distinct banks.
+// A workgroup (4 waves) owns 16 HT heads x 16 RTW (4 / HT) rows; wave w takes
+// head tile w % HT and RTW row tiles, reusing each q value RTW times.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__host__ __device__ constexpr int mfma_rows(int HT, int RTW) { return 16 * RTW * (4 / HT); }
+
+// Staging of n rows of D values (row i from src at min(base + i, last) *
+// stride) in the (d % 4, d / 4) order: a thread moves 16 consecutive d per
+// unit.  The loads and the LDS writes are separate steps so that a caller can
+// issue every global load before its first LDS access.
+template <int D, int N>
+struct MfmaStage {
+  static constexpr int UPR = D / 16, NU = N * UPR, PER = (NU + kThreads - 1) / kThreads;
+  float4 v[PER][4];
+
+  template <int DT>
+  __device__ __forceinline__ void load(const void* __restrict__ src, int64_t stride, int base,
+                                       int last, int tid) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int u = min(tid + k * kThreads, NU - 1);
+      const int r = u / UPR, d0 = (u % UPR) * 16;
+      const int64_t off = (int64_t)min(base + r, last) * stride + d0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[k][i] = load4<DT>(src, off + 4 * i);
+    }
+  }
+
+  __device__ __forceinline__ void store(float* __restrict__ dst, int tid) const {
+    constexpr int P = c_pitch(D);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int u = min(tid + k * kThreads, NU - 1);
+      const int r = u / UPR, j0 = (u % UPR) * 4;
+      float* row = dst + r * P + j0;
+      *reinterpret_cast<float4*>(row) = make_float4(v[k][0].x, v[k][1].x, v[k][2].x, v[k][3].x);
+      *reinterpret_cast<float4*>(row + D / 4) =
+          make_float4(v[k][0].y, v[k][1].y, v[k][2].y, v[k][3].y);
+      *reinterpret_cast<float4*>(row + D / 2) =
+          make_float4(v[k][0].z, v[k][1].z, v[k][2].z, v[k][3].z);
+      *reinterpret_cast<float4*>(row + 3 * D / 4) =
+          make_float4(v[k][0].w, v[k][1].w, v[k][2].w, v[k][3].w);
+    }
+  }
+};
+
+template <int QDT, int CDT, int HT, int RTW, int D>
+__global__ __launch_bounds__(kThreads) void lut_mfma_kernel(
+    const void* __restrict__ q, int64_t q_row_stride,
+    const void* __restrict__ cb, int Hq, int MK, int G, int layout,
+    uint16_t* __restrict__ out, int head_tiles) {
+  constexpr int ROWS = mfma_rows(HT, RTW), HEADS = 16 * HT, P = c_pitch(D);
+  // Each wave keeps its 16 heads' q (D / 4 floats per lane) in registers.
+  // With 64 x 64 tiles one LDS region holds the q tile, then the codebook tile
+  // (half the LDS, so four workgroups fit per CU); smaller tiles stage both at
+  // once in two regions.
+  constexpr bool kShare = HT == 4;
+  extern __shared__ __attribute__((aligned(16))) float mfma_smem[];
+  float* const s_q = kShare ? mfma_smem : mfma_smem + ROWS * P;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const TileId ti = tile_of(blockIdx.x, gridDim.x, head_tiles, 1);
+  const int row0 = ti.row_tile * ROWS, head0 = ti.head_tile * HEADS;
+  MfmaStage<D, ROWS> sc;
+  MfmaStage<D, HEADS> sq;
+  sc.template load<CDT>(cb, D, row0, MK - 1, tid);
+  sq.template load<QDT>(q, q_row_stride, head0, Hq - 1, tid);
+  sq.store(s_q, tid);
+  if (!kShare) sc.store(mfma_smem, tid);
+  __syncthreads();
+
+  const int ht = wave % HT, rt0 = (wave / HT) * RTW;
+  const int hl = lane & 15, kj = lane >> 4;
+  float4 a[D / 16];
+  {
+    const float* qp = s_q + (ht * 16 + hl) * P + kj * (D / 4);
+#pragma unroll
+    for (int jb = 0; jb < D / 16; ++jb) a[jb] = *reinterpret_cast<const float4*>(qp + 4 * jb);
+  }
+  if (kShare) {
+    __syncthreads();
+    sc.store(mfma_smem, tid);
+    __syncthreads();
+  }
+
+  const float* cp = mfma_smem + (rt0 * 16 + hl) * P + kj * (D / 4);
+  f32x4_t acc[RTW];
+#pragma unroll
+  for (int i = 0; i < RTW; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int jb = 0; jb < D / 16; ++jb) {
+#pragma unroll
+    for (int i = 0; i < RTW; ++i) {
+      const float4 b = *reinterpret_cast<const float4*>(cp + i * 16 * P + 4 * jb);
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].x, b.x, acc[i], 0, 0, 0);
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].y, b.y, acc[i], 0, 0, 0);
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].z, b.z, acc[i], 0, 0, 0);
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].w, b.w, acc[i], 0, 0, 0);
+    }
+  }
+  const int hA = head0 + ht * 16 + 4 * kj;
+#pragma unroll
+  for (int i = 0; i < RTW; ++i) {
+    const int row = row0 + (rt0 + i) * 16 + hl;
+    if (row >= MK) continue;
+    const float r4[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+    write_row<4>(r4, hA, row, Hq, MK, G, layout, out);
+  }
+}
+
 template <int QDT, int CDT, int HPT>
 __global__ __launch_bounds__(kThreads) void lut_tile_kernel(
     const void* __restrict__ q, int64_t q_row_stride,
@@ -317,6 +445,49 @@ int lut_tiles_per_wg(int Hq, int MK, int hpt, const DevInfo& di) {
   return t < 1 ? 1 : (int)t;
 }
 
+// LAPRUNE_LUT_IMPL=dpp selects the VALU kernels (measurements, cross-checks);
+// the fp32-MFMA kernel is the default.  Read at every call, so that one
+// process can run both.
+bool lut_impl_mfma() {
+  const char* e = getenv("LAPRUNE_LUT_IMPL");
+  return !(e && strcmp(e, "dpp") == 0);
+}
+
+// fp32-MFMA LUT (D = 64 or 128): 64 x 64 tiles (four row tiles per wave)
+// once there are two of them per CU, else 32 x 32 tiles (one per wave).
+bool lut_mfma_ok(int D) { return lut_impl_mfma() && (D == 64 || D == 128); }
+
+constexpr size_t lut_mfma_smem_bytes(int D, int HT, int RTW) {
+  const int rows = HT == 4 ? std::max(mfma_rows(HT, RTW), 16 * HT) : mfma_rows(HT, RTW) + 16 * HT;
+  return (size_t)rows * c_pitch(D) * sizeof(float);
+}
+
+template <int QDT, int CDT, int D>
+void launch_lut_mfma_d(const void* q, int64_t qs, const void* cb, int Hq, int MK, int G,
+                       int layout, uint16_t* out, int cus, hipStream_t st) {
+  const int64_t big_tiles = (int64_t)((MK + 63) / 64) * ((Hq + 63) / 64);
+  if (Hq >= 64 && big_tiles >= 2 * cus) {
+    const int htl = (Hq + 63) / 64;
+    const dim3 g((unsigned)(((MK + 63) / 64) * htl));
+    hipLaunchKernelGGL((lut_mfma_kernel<QDT, CDT, 4, 4, D>), g, dim3(kThreads),
+                       lut_mfma_smem_bytes(D, 4, 4), st, q, qs, cb,
+                       Hq, MK, G, layout, out, htl);
+  } else {
+    const int htl = (Hq + 31) / 32;
+    const dim3 g((unsigned)(((MK + 31) / 32) * htl));
+    hipLaunchKernelGGL((lut_mfma_kernel<QDT, CDT, 2, 1, D>), g, dim3(kThreads),
+                       lut_mfma_smem_bytes(D, 2, 1), st, q, qs, cb,
+                       Hq, MK, G, layout, out, htl);
+  }
+}
+
+template <int QDT, int CDT>
+void launch_lut_mfma(const void* q, int64_t qs, const void* cb, int Hq, int D, int MK, int G,
+                     int layout, uint16_t* out, int cus, hipStream_t st) {
+  if (D == 64) launch_lut_mfma_d<QDT, CDT, 64>(q, qs, cb, Hq, MK, G, layout, out, cus, st);
+  else launch_lut_mfma_d<QDT, CDT, 128>(q, qs, cb, Hq, MK, G, layout, out, cus, st);
+}
+
 template <int QDT, int CDT, int HPT>
 void launch_hpt(const void* q, int64_t qs, const void* cb, int Hq, int D, int MK, int G,
                 int layout, uint16_t* out, int tpw, hipStream_t st) {
@@ -338,8 +509,15 @@ void launch_hpt(const void* q, int64_t qs, const void* cb, int Hq, int D, int MK
 
 template <int QDT>
 hipError_t launch_lut(const void* q, int64_t qs, const void* cb, int cb_dtype, int Hq, int D,
-                      int MK, int G, int layout, uint16_t* out, int hpt, int tpw,
+                      int MK, int G, int layout, uint16_t* out, int hpt, int tpw, int cus,
                       hipStream_t st) {
+  if (lut_mfma_ok(D)) {
+    if (cb_dtype == LAP_DTYPE_F32)
+      launch_lut_mfma<QDT, LAP_DTYPE_F32>(q, qs, cb, Hq, D, MK, G, layout, out, cus, st);
+    else
+      launch_lut_mfma<QDT, LAP_DTYPE_F16>(q, qs, cb, Hq, D, MK, G, layout, out, cus, st);
+    return hipGetLastError();
+  }
   if (cb_dtype == LAP_DTYPE_F32) {
     if (hpt == 8) launch_hpt<QDT, LAP_DTYPE_F32, 8>(q, qs, cb, Hq, D, MK, G, layout, out, tpw, st);
     else launch_hpt<QDT, LAP_DTYPE_F32, 4>(q, qs, cb, Hq, D, MK, G, layout, out, tpw, st);
@@ -386,15 +564,15 @@ extern "C" int lap_lut_build(const void* q, int q_dtype, int64_t q_row_stride,
   switch (q_dtype) {
     case LAP_DTYPE_F32:
       e = launch_lut<LAP_DTYPE_F32>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout,
-                                    out, hpt, tpw, st);
+                                    out, hpt, tpw, di.cu_count, st);
       break;
     case LAP_DTYPE_F16:
       e = launch_lut<LAP_DTYPE_F16>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout,
-                                    out, hpt, tpw, st);
+                                    out, hpt, tpw, di.cu_count, st);
       break;
     default:
       e = launch_lut<LAP_DTYPE_BF16>(q, q_row_stride, codebooks, cb_dtype, Hq, D, MK, G, layout,
-                                     out, hpt, tpw, st);
+                                     out, hpt, tpw, di.cu_count, st);
       break;
   }
   LAP_HIP(e, "lap_lut_build launch");

@@ -30,9 +30,17 @@ def K(dev):
 
 # ------------------------------------------------------------------ A1 LUT
 
+@pytest.fixture(params=["mfma", "dpp"])
+def lut_impl(request, monkeypatch):
+    """The LUT builder's two forms for D = 64 and 128: fp32 MFMA (default) and
+    DPP-broadcast VALU (LAPRUNE_LUT_IMPL=dpp, read at every call)."""
+    monkeypatch.setenv("LAPRUNE_LUT_IMPL", request.param)
+    return request.param
+
+
 @pytest.mark.parametrize("qdt", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("layout", ["hmk", "gmkg"])
-def test_lut_build_bit_exact(dev, K, orc, qdt, layout):
+def test_lut_build_bit_exact(dev, K, orc, qdt, layout, lut_impl):
     g = _gen(1)
     q = torch.randn(32, 128, generator=g).to(qdt)
     cb = torch.randn(32, 256, 128, generator=g) * 0.02
@@ -54,7 +62,7 @@ def test_lut_build_bit_exact(dev, K, orc, qdt, layout):
     (24, 128, 5, 100, 2, "gmkg"),     # G = 2, M*K not a multiple of the row tile
     (64, 256, 8, 64, 4, "hmk"),       # D = 256
 ])
-def test_lut_build_tiles(dev, K, orc, Hq, D, M, Kc, G, layout):
+def test_lut_build_tiles(dev, K, orc, Hq, D, M, Kc, G, layout, lut_impl):
     from laprune_amd import _native as N
     print("device info (CUs, LDS per block, wave):", N.device_info(), flush=True)
     g = _gen(3 + Hq + D)
@@ -65,6 +73,35 @@ def test_lut_build_tiles(dev, K, orc, Hq, D, M, Kc, G, layout):
     want = orc.lut_build(q.float().numpy(), cb.numpy())
     if layout == "gmkg":
         want = orc.lut_to_gmkg(want, G)
+    assert np.array_equal(_np_u16(lut), want)
+
+
+@pytest.mark.parametrize("cdt", [torch.float32, torch.float16])
+def test_lut_build_wide_range(dev, K, orc, lut_impl, cdt):
+    """Operands spread over many binades, exact zeros, signed zeros and
+    products below the fp32 normal range: the per-d rounding order shows in
+    the fp16 outputs (many land near a rounding boundary or in overflow)."""
+    g = _gen(11)
+    Hq, D, M, Kc = 64, 128, 4, 64
+
+    def spread(*shape):  # per-element spread of 8 binades
+        return torch.randn(*shape, generator=g) * torch.exp2(
+            torch.randint(-8, 1, shape, generator=g).float())
+    # per-head and per-row scales: sums from far below fp16's subnormals
+    # (fp32-subnormal products) through overflow to inf
+    head_e = torch.cat([torch.linspace(-95, -60, 16), torch.linspace(-45, 14, Hq - 16)]).round()
+    row_e = torch.randint(-35, 5, (M, Kc, 1), generator=g).float()
+    q = spread(Hq, D) * torch.exp2(head_e)[:, None]
+    q[:, ::7] = 0.0
+    q[::5, 3::11] = -0.0
+    q = q.bfloat16()
+    cb = spread(M, Kc, D) * torch.exp2(row_e)
+    if cdt == torch.float16:
+        cb = (spread(M, Kc, D) * torch.exp2(row_e.clamp(min=-14) / 2)).to(cdt).float()
+    cb_dev = cb.to(cdt).to(dev)
+    lut = K.aq_lut_build(q.to(dev), cb_dev, G=4, layout="gmkg")
+    torch.cuda.synchronize()
+    want = orc.lut_to_gmkg(orc.lut_build(q.float().numpy(), cb.numpy()), 4)
     assert np.array_equal(_np_u16(lut), want)
 
 
