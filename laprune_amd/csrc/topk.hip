@@ -20,6 +20,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 namespace lap {
 
@@ -350,55 +351,53 @@ int run_levels(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int 
 
 // ---- One workgroup per row: level 2 and the compaction in one launch.
 //
-// The row's keys stay in registers (thread t owns columns [t*KPT, (t+1)*KPT),
-// KPT <= 128, so up to 131072 columns), the level-1 histogram is the sum of
-// the scorer's chunk histograms, the level-2 histogram is built from the
-// registers, and the ordered compaction is two block-wide scans.  Same
-// result as run_levels (threshold tau, then the `need` lowest-column ties).
+// Wave w owns the columns [w * 64 * KPT, (w + 1) * 64 * KPT) of the row
+// (KPT <= 32, so up to 32768 columns); its lane l holds column
+// w * 64 * KPT + 64 e + l as key e, so for every e the wave's 64 lanes cover
+// 64 consecutive columns and a ballot orders them.  The level-1 histogram is
+// the sum of the scorer's chunk histograms; its threshold bin b1 leaves few
+// candidates (the keys of bins >= b1: fewer than k plus one bin), which every
+// wave packs in column order into its own LDS segment.  The level-2
+// histogram, the tie ranks and the ordered output then run over those
+// segments only.  Same result as run_levels (threshold tau, then the `need`
+// lowest-column ties).
 constexpr int kRowThreads = 1024;
 constexpr int kRowWaves = kRowThreads / 64;
+constexpr int kRowMaxKpt = 32;
 
-// Exclusive prefix sum over the 1024 threads of the block; *total = sum.
-__device__ __forceinline__ uint32_t row_exclusive_scan(uint32_t x, uint32_t* s_wsum,
-                                                       uint32_t* total) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t inc = x;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t y = __shfl_up(inc, d, 64);
-    if (lane >= d) inc += y;
-  }
-  if (lane == 63) s_wsum[wave] = inc;
-  __syncthreads();
-  uint32_t before = 0, all = 0;
-#pragma unroll
-  for (int w = 0; w < kRowWaves; ++w) {
-    const uint32_t v = s_wsum[w];
-    before += w < wave ? v : 0u;
-    all += v;
-  }
-  __syncthreads();
-  *total = all;
-  return before + inc - x;
+// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then the
+// row broadcasts of lanes 15 and 31).
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
 }
 
-// select_bin for a 1024-thread block: threads 0..255 scan, all synchronise.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// select_bin for a 1024-thread block: waves 0..3 scan the 256 bins from the
+// top, all threads synchronise.  s_res = {bin, count above the bin}.
 __device__ void row_select_bin(const uint32_t* s_h, uint32_t target, uint32_t* s_wsum,
                                uint32_t* s_res) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t x = tid < 256 ? s_h[255 - tid] : 0u;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
+  uint32_t x = 0, h = 0;
+  if (wave < 4) {
+    h = s_h[255 - tid];
+    x = wave_inclusive_scan(h);
+    if (lane == 63) s_wsum[wave] = x;
   }
-  if (tid < 256 && lane == 63) s_wsum[wave] = x;
   __syncthreads();
-  if (tid < 256) {
+  if (wave < 4) {
     uint32_t add = 0;
     for (int w = 0; w < wave; ++w) add += s_wsum[w];
-    const uint32_t S_i = x + add;                  // S(255 - tid)
-    const uint32_t S_next = S_i - s_h[255 - tid];  // S(256 - tid)
+    const uint32_t S_i = x + add;  // keys in bins >= 255 - tid
+    const uint32_t S_next = S_i - h;
     if (S_i >= target && S_next < target) {
       s_res[0] = 255 - tid;
       s_res[1] = S_next;
@@ -407,14 +406,19 @@ __device__ void row_select_bin(const uint32_t* s_h, uint32_t target, uint32_t* s
   __syncthreads();
 }
 
+// Dynamic LDS of topk_row_kernel<KPT>: the candidate segments.
+constexpr size_t row_kernel_lds(int kpt) { return (size_t)kRowThreads * kpt * sizeof(uint32_t); }
+
 template <int KPT, typename OUT_T>
 __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(
     const uint16_t* __restrict__ keys, int64_t key_stride, int T,
     const uint32_t* __restrict__ hist1, int C1, SelSpec sp, OUT_T* __restrict__ out,
     int64_t out_stride) {
-  static_assert(KPT % 8 == 0, "KPT must be a multiple of 8");
+  static_assert(KPT % 8 == 0 && KPT <= kRowMaxKpt, "KPT must be 8, 16, 24 or 32");
+  extern __shared__ uint32_t s_seg[];  // wave w: [w * 64 * KPT, +count), (key << 16) | column
   __shared__ uint32_t s_h[4][256], s_h2[256], s_wsum[kRowWaves], s_res[2];
-  const int r = blockIdx.x, tid = threadIdx.x;
+  __shared__ uint32_t s_wgt[kRowWaves], s_wtie[kRowWaves];
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const SelRow sr = sp.row(r);
   OUT_T* orow = out + (int64_t)r * out_stride;
   if (sp.plans)  // ragged rows: pad past the row's k with -1
@@ -422,31 +426,27 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(
   if (sr.k == 0) return;
   const int c0 = sr.cs, c1 = sr.cs + sr.n;
 
-  // Keys of columns [tid*KPT, +KPT), 8 per 16-byte load; granules past the
-  // row's T columns load the last granule and are masked by the window.
-  uint32_t kw[KPT / 2];
-  const uint16_t* kr = keys + (int64_t)r * key_stride;
-#pragma unroll
-  for (int i = 0; i < KPT / 8; ++i) {
-    const int col = min(tid * KPT + 8 * i, T - 8);
-    const uint4 v = *reinterpret_cast<const uint4*>(kr + col);
-    kw[4 * i] = v.x;
-    kw[4 * i + 1] = v.y;
-    kw[4 * i + 2] = v.z;
-    kw[4 * i + 3] = v.w;
-  }
-  auto key_at = [&](int e) -> uint32_t { return (kw[e >> 1] >> ((e & 1) * 16)) & 0xffffu; };
-  auto live = [&](int e) -> bool {
-    const int col = tid * KPT + e;
-    return col >= c0 && col < c1;
-  };
-
   // Level 1: the scorer's chunk histograms summed per bin (4 partial sums).
+  // Their loads go out first (loads retire in order), four at a time.
+  const int bin = tid & 255, part = tid >> 8;
+  const uint32_t* hp = hist1 + (int64_t)r * C1 * 256 + bin;
+  uint32_t hv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) hv[u] = hp[(int64_t)min(part + 4 * u, C1 - 1) * 256];
+
+  // Keys, one 2-byte load each (64 lanes read 128 contiguous bytes); columns
+  // past T load column T - 1 and fall outside the window.
+  const int wcol = wave * 64 * KPT;
+  const uint16_t* kr = keys + (int64_t)r * key_stride;
+  uint32_t kv[KPT];
+#pragma unroll
+  for (int e = 0; e < KPT; ++e) kv[e] = kr[min(wcol + 64 * e + lane, T - 1)];
+
   {
-    const int bin = tid & 255, part = tid >> 8;
-    const uint32_t* hp = hist1 + (int64_t)r * C1 * 256 + bin;
     uint32_t a = 0;
-    for (int c = part; c < C1; c += 4) a += hp[(int64_t)c * 256];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a += part + 4 * u < C1 ? hv[u] : 0u;
+    for (int c = part + 16; c < C1; c += 4) a += hp[(int64_t)c * 256];
     s_h[part][bin] = a;
     if (tid < 256) s_h2[tid] = 0;
   }
@@ -456,11 +456,34 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(
   row_select_bin(s_h[0], (uint32_t)sr.k, s_wsum, s_res);
   const uint32_t b1 = s_res[0], gt1 = s_res[1];
 
-  // Level 2 over the keys of bin b1.
+  // Candidates (window keys in bins >= b1) into the wave's segment, in
+  // column order.
+  const uint32_t lo = b1 << 8;
+  uint32_t* seg = s_seg + wcol;
+  uint32_t cnt = 0;  // wave-uniform
+  auto pack = [&](auto windowed) {
 #pragma unroll
-  for (int e = 0; e < KPT; ++e) {
-    const uint32_t key = key_at(e);
-    if ((key >> 8) == b1 && live(e)) atomicAdd(&s_h2[key & 255u], 1u);
+    for (int e = 0; e < KPT; ++e) {
+      const int col = wcol + 64 * e + lane;
+      const bool c = kv[e] >= lo && (!decltype(windowed)::value || (col >= c0 && col < c1));
+      const uint64_t m = __ballot(c);
+      if (c) seg[cnt + lanes_below(m)] = (kv[e] << 16) | (uint32_t)col;
+      cnt += (uint32_t)__popcll(m);
+    }
+  };
+  // Wave-uniform: columns all inside the window (no per-key window test),
+  // all outside (no candidates), or straddling an edge.
+  const int wend = wcol + 64 * KPT;
+  if (wcol >= c0 && wend <= c1) pack(std::false_type{});
+  else if (wend > c0 && wcol < c1) pack(std::true_type{});
+  // Level 2 over this segment's keys of bin b1 (each lane reads what other
+  // lanes of its wave wrote: a wavefront-scope fence orders them).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (uint32_t i = lane; i < cnt; i += 64) {
+    const uint32_t key = seg[i] >> 16;
+    if ((key >> 8) == b1) atomicAdd(&s_h2[key & 255u], 1u);
   }
   __syncthreads();
   const uint32_t k2 = (uint32_t)sr.k - gt1;
@@ -468,47 +491,53 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(
   const uint32_t tau = (b1 << 8) | s_res[0];
   const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
 
-  // Ordered compaction: keys > tau, then the `need` lowest-column ties.
+  // Keys above tau and ties at tau per segment, then each wave's output
+  // offset: the selections of the segments before it.
   uint32_t ngt = 0, ntie = 0;
-#pragma unroll
-  for (int e = 0; e < KPT; ++e) {
-    const uint32_t key = key_at(e);
-    const bool ok = live(e);
-    ngt += (ok && key > tau) ? 1u : 0u;
-    ntie += (ok && key == tau) ? 1u : 0u;
+  for (uint32_t i0 = 0; i0 < cnt; i0 += 64) {
+    const uint32_t i = i0 + lane;
+    const uint32_t key = i < cnt ? seg[i] >> 16 : 0u;
+    ngt += (uint32_t)__popcll(__ballot(i < cnt && key > tau));
+    ntie += (uint32_t)__popcll(__ballot(i < cnt && key == tau));
   }
-  uint32_t all;
-  const uint32_t tie0 = row_exclusive_scan(ntie, s_wsum, &all);
-  const uint32_t take = tie0 >= need ? 0u : min(ntie, need - tie0);
-  uint32_t pos = row_exclusive_scan(ngt + take, s_wsum, &all);
-  uint32_t taken = 0;
-#pragma unroll
-  for (int e = 0; e < KPT; ++e) {
-    const uint32_t key = key_at(e);
-    if (!live(e)) continue;
-    bool sel = key > tau;
-    if (key == tau && taken < take) {
-      sel = true;
-      ++taken;
-    }
-    if (sel) orow[pos++] = (OUT_T)(tid * KPT + e);
+  if (lane == 0) {
+    s_wgt[wave] = ngt;
+    s_wtie[wave] = ntie;
+  }
+  __syncthreads();
+  uint32_t gt_before = 0, tie_before = 0;
+  for (int w = 0; w < wave; ++w) {
+    gt_before += s_wgt[w];
+    tie_before += s_wtie[w];
+  }
+  uint32_t pos = gt_before + min(tie_before, need);
+  uint32_t tie_rank = tie_before;
+  for (uint32_t i0 = 0; i0 < cnt; i0 += 64) {
+    const uint32_t i = i0 + lane;
+    const uint32_t v = i < cnt ? seg[i] : 0u;
+    const uint32_t key = v >> 16;
+    const bool is_tie = i < cnt && key == tau;
+    const uint64_t mt = __ballot(is_tie);
+    const bool sel = (i < cnt && key > tau) || (is_tie && tie_rank + lanes_below(mt) < need);
+    const uint64_t ms = __ballot(sel);
+    if (sel) orow[pos + lanes_below(ms)] = (OUT_T)(v & 0xffffu);
+    pos += (uint32_t)__popcll(ms);
+    tie_rank += (uint32_t)__popcll(mt);
   }
 }
 
 // Keys per thread of topk_row_kernel for a row of T columns, or 0 for the
 // two-kernel path.  One workgroup per row pays off up to 32 keys per thread
-// (T <= 32768: batched decode rows); longer rows want the parallelism of the
-// chunked levels (at 128 keys per thread the row kernel spills and runs 8
-// workgroups for a batch-1 step).  LAPRUNE_TOPK=levels|row forces a path.
+// (T <= 32768: batched decode rows); longer rows take the chunked levels.
+// LAPRUNE_TOPK=levels|row forces a path (row: whenever T fits).
 int row_kernel_kpt(int T) {
   static const int mode = [] {
     const char* e = getenv("LAPRUNE_TOPK");
     if (!e) return 0;
     return strcmp(e, "levels") == 0 ? 1 : strcmp(e, "row") == 0 ? 2 : 0;
   }();
-  if (mode == 1 || T % 8 != 0) return 0;
-  const int max_kpt = mode == 2 ? 128 : 32;
-  for (int kpt = 8; kpt <= max_kpt; kpt *= 2)
+  if (mode == 1 || T < 1) return 0;
+  for (int kpt = 8; kpt <= kRowMaxKpt; kpt *= 2)
     if ((int64_t)kpt * kRowThreads >= T) return kpt;
   return 0;
 }
@@ -518,12 +547,13 @@ void launch_row_kernel(int kpt, const uint16_t* keys, int64_t key_stride, int T,
                        const uint32_t* hist1, int C1, const SelSpec& sp, int R, OUT_T* out,
                        int64_t out_stride, hipStream_t st) {
   switch (kpt) {
-#define LAP_ROWK(K)                                                                       \
-  case K:                                                                                 \
-    hipLaunchKernelGGL((topk_row_kernel<K, OUT_T>), dim3(R), dim3(kRowThreads), 0, st, keys, \
-                       key_stride, T, hist1, C1, sp, out, out_stride);                    \
+#define LAP_ROWK(K)                                                                      \
+  case K:                                                                                \
+    hipLaunchKernelGGL((topk_row_kernel<K, OUT_T>), dim3(R), dim3(kRowThreads),          \
+                       row_kernel_lds(K), st, keys, key_stride, T, hist1, C1, sp, out,   \
+                       out_stride);                                                      \
     break;
-    LAP_ROWK(8) LAP_ROWK(16) LAP_ROWK(32) LAP_ROWK(64) LAP_ROWK(128)
+    LAP_ROWK(8) LAP_ROWK(16) LAP_ROWK(32)
 #undef LAP_ROWK
   }
 }

@@ -237,6 +237,25 @@ def test_topk_all_equal_and_int32(dev, K, orc):
     assert np.array_equal(idx.cpu().numpy(), np.tile(np.arange(7, 107), (2, 1)))
 
 
+@pytest.mark.parametrize("T,k", [(32768, 1024), (3001, 2933), (20000, 1), (9000, 8000)])
+def test_retrieve_topk_all_equal(dev, K, orc, T, k):
+    """Every token scores the same: each key of the window is a candidate
+    (the selection's candidate lists run full) and all of them tie, so the
+    result is the k lowest columns of the window."""
+    Hkv, cap = 8, 64
+    g = _gen(61)
+    q = torch.randn(32, 128, generator=g).bfloat16()
+    cb = torch.randn(32, 256, 128, generator=g) * 0.02
+    codes = torch.full((1, Hkv, T + cap, 32), 17, dtype=torch.uint8, device=dev)[:, :, :T, :]
+    lut = K.aq_lut_build(q.to(dev), cb.to(dev), G=4, layout="gmkg")
+    cs, ce = orc.candidate_window(T, T, 4, 64)
+    k = min(k, ce - cs)
+    idx = K.aq_retrieve_topk(lut, codes, k, cs, ce)
+    torch.cuda.synchronize()
+    want = np.tile(np.arange(cs, cs + k), (Hkv, 1))
+    assert np.array_equal(idx[0].cpu().numpy().astype(np.int64), want)
+
+
 @pytest.mark.parametrize("T,k,key_dt", [(8192, 2048, torch.float16), (131072, 2048, torch.float16),
                                         (131072, 2621, torch.bfloat16), (4096, 5000, torch.float16)])
 def test_retrieve_topk_fused(dev, K, orc, T, k, key_dt):
