@@ -274,9 +274,9 @@ __host__ __device__ constexpr int mfma_rows(int HT, int RTW) { return 16 * RTW *
 // stride) in the (d % 4, d / 4) order: a thread moves 16 consecutive d per
 // unit.  The loads and the LDS writes are separate steps so that a caller can
 // issue every global load before its first LDS access.
-template <int D, int N>
+template <int D, int N, int TH = kThreads>
 struct MfmaStage {
-  static constexpr int UPR = D / 16, NU = N * UPR, PER = (NU + kThreads - 1) / kThreads;
+  static constexpr int UPR = D / 16, NU = N * UPR, PER = (NU + TH - 1) / TH;
   float4 v[PER][4];
 
   template <int DT>
@@ -284,7 +284,7 @@ struct MfmaStage {
                                        int last, int tid) {
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      const int u = min(tid + k * kThreads, NU - 1);
+      const int u = min(tid + k * TH, NU - 1);
       const int r = u / UPR, d0 = (u % UPR) * 16;
       const int64_t off = (int64_t)min(base + r, last) * stride + d0;
 #pragma unroll
@@ -296,7 +296,7 @@ struct MfmaStage {
     constexpr int P = c_pitch(D);
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      const int u = min(tid + k * kThreads, NU - 1);
+      const int u = min(tid + k * TH, NU - 1);
       const int r = u / UPR, j0 = (u % UPR) * 4;
       float* row = dst + r * P + j0;
       *reinterpret_cast<float4*>(row) = make_float4(v[k][0].x, v[k][1].x, v[k][2].x, v[k][3].x);
@@ -309,6 +309,39 @@ struct MfmaStage {
     }
   }
 };
+
+// acc[t] += q-tile x rows 16 t .. 16 t + 15 of the staged tile, over all D:
+// for each block of 16 d, four ds_read_b128 (one per row tile) then sixteen
+// MFMAs.  The operands of block jb + 1 are read before the MFMAs of block jb
+// issue, so the LDS latency hides behind the matrix pipe even with one wave
+// per SIMD; the scheduling barriers keep the compiler from regrouping them.
+template <int D, int NT>
+__device__ __forceinline__ void mfma_tile_chain(const float4 (&a)[D / 16], const float* cp,
+                                                f32x4_t (&acc)[NT]) {
+  constexpr int P = c_pitch(D);
+  float4 bc[NT], bn[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) bc[t] = *reinterpret_cast<const float4*>(cp + t * 16 * P);
+#pragma unroll
+  for (int jb = 0; jb < D / 16; ++jb) {
+    if (jb + 1 < D / 16) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        bn[t] = *reinterpret_cast<const float4*>(cp + t * 16 * P + 4 * (jb + 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].x, bc[t].x, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].y, bc[t].y, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].z, bc[t].z, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].w, bc[t].w, acc[t], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) bc[t] = bn[t];
+  }
+}
 
 template <int QDT, int CDT, int HT, int RTW, int D>
 __global__ __launch_bounds__(kThreads) void lut_mfma_kernel(
@@ -352,17 +385,7 @@ __global__ __launch_bounds__(kThreads) void lut_mfma_kernel(
   f32x4_t acc[RTW];
 #pragma unroll
   for (int i = 0; i < RTW; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int jb = 0; jb < D / 16; ++jb) {
-#pragma unroll
-    for (int i = 0; i < RTW; ++i) {
-      const float4 b = *reinterpret_cast<const float4*>(cp + i * 16 * P + 4 * jb);
-      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].x, b.x, acc[i], 0, 0, 0);
-      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].y, b.y, acc[i], 0, 0, 0);
-      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].z, b.z, acc[i], 0, 0, 0);
-      acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jb].w, b.w, acc[i], 0, 0, 0);
-    }
-  }
+  mfma_tile_chain<D, RTW>(a, cp, acc);
   const int hA = head0 + ht * 16 + 4 * kj;
 #pragma unroll
   for (int i = 0; i < RTW; ++i) {
@@ -470,8 +493,7 @@ void launch_lut_mfma_d(const void* q, int64_t qs, const void* cb, int Hq, int MK
     const int htl = (Hq + 63) / 64;
     const dim3 g((unsigned)(((MK + 63) / 64) * htl));
     hipLaunchKernelGGL((lut_mfma_kernel<QDT, CDT, 4, 4, D>), g, dim3(kThreads),
-                       lut_mfma_smem_bytes(D, 4, 4), st, q, qs, cb,
-                       Hq, MK, G, layout, out, htl);
+                       lut_mfma_smem_bytes(D, 4, 4), st, q, qs, cb, Hq, MK, G, layout, out, htl);
   } else {
     const int htl = (Hq + 31) / 32;
     const dim3 g((unsigned)(((MK + 31) / 32) * htl));

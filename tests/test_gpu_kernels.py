@@ -54,21 +54,27 @@ def test_lut_build_bit_exact(dev, K, orc, qdt, layout, lut_impl):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("Hq,D,M,Kc,G,layout", [
-    (512, 128, 32, 256, 4, "gmkg"),   # batch 16 x 32 heads: 64-head tiles
-    (520, 128, 32, 256, 4, "gmkg"),   # ... with a partial last head tile
-    (200, 64, 32, 256, 4, "hmk"),     # ... D = 64, reference layout
-    (40, 128, 32, 256, 4, "gmkg"),    # partial head tile
-    (24, 128, 5, 100, 2, "gmkg"),     # G = 2, M*K not a multiple of the row tile
-    (64, 256, 8, 64, 4, "hmk"),       # D = 256
+@pytest.mark.parametrize("Hq,D,M,Kc,G,layout,cdt", [
+    (512, 128, 32, 256, 4, "gmkg", "f32"),  # batch 16 x 32 heads: pipelined 64-head tiles
+    (512, 128, 32, 256, 4, "gmkg", "f16"),  # ... fp16 codebooks
+    (520, 128, 32, 256, 4, "gmkg", "f32"),  # ... with a partial last head tile
+    (448, 128, 40, 206, 4, "gmkg", "f32"),  # ... last workgroup: one partial row tile
+    (200, 64, 32, 256, 4, "hmk", "f32"),    # ... D = 64, reference layout
+    (40, 128, 32, 256, 4, "gmkg", "f32"),   # partial head tile
+    (24, 128, 5, 100, 2, "gmkg", "f32"),    # G = 2, M*K not a multiple of the row tile
+    (64, 256, 8, 64, 4, "hmk", "f32"),      # D = 256
 ])
-def test_lut_build_tiles(dev, K, orc, Hq, D, M, Kc, G, layout, lut_impl):
+def test_lut_build_tiles(dev, K, orc, Hq, D, M, Kc, G, layout, cdt, lut_impl):
     from laprune_amd import _native as N
     print("device info (CUs, LDS per block, wave):", N.device_info(), flush=True)
     g = _gen(3 + Hq + D)
     q = torch.randn(Hq, D, generator=g).bfloat16()
     cb = torch.randn(M, Kc, D, generator=g) * 0.05
-    lut = K.aq_lut_build(q.to(dev), cb.to(dev), G=G, layout=layout)
+    cb_dev = cb.to(dev)
+    if cdt == "f16":
+        cb_dev = cb_dev.half()
+        cb = cb.half().float()
+    lut = K.aq_lut_build(q.to(dev), cb_dev, G=G, layout=layout)
     torch.cuda.synchronize()
     want = orc.lut_build(q.float().numpy(), cb.numpy())
     if layout == "gmkg":
