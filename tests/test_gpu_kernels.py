@@ -326,7 +326,7 @@ def _rel(a, b):
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("per_head", [False, True])
-@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("D", [128, 64, 256])
 def test_sparse_attn_decode(dev, K, orc, dt, per_head, D):
     g = _gen(80 + D)
     B, Hq, Hkv, T, n = 2, 8, 2, 3000, 300
