@@ -31,6 +31,10 @@ so that the 256 MB Infinity Cache cannot serve the step from cache.
                  post-RoPE keys (8 KV heads x 64 tokens = 512 rows, 32x256
                  codebooks), MFMA coarse search + exact recheck, next to the
                  reference's fp32 greedy path on the host cores.
+``reference_mode`` the same C2 step with the reference's own selection: top-k
+                 per query head on bf16-cast scores, budget 131004 -
+                 int(0.98 * 131004) = 2621, each head attending over its own
+                 keep set.
 ``ragged``       one attention layer of configs[4] (C5): batch 16, per-sequence
                  lengths uniform in [16384, 32768] (seeded), top-1024 per KV
                  group + 4 sink + 64 local, the newest < 64 keys of each
@@ -77,6 +81,8 @@ def parse():
                     help="budget for the CPU baseline sample")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
     ap.add_argument("--no-ragged", action="store_true", help="skip the C5 ragged-batch leg")
+    ap.add_argument("--no-reference-mode", action="store_true",
+                    help="skip the per-query-head (reference selection) C2 leg")
     ap.add_argument("--only-ragged", action="store_true",
                     help="run only the C5 ragged-batch leg (for profiling); prints its JSON")
     ap.add_argument("--counters", action="store_true",
@@ -225,6 +231,69 @@ def sdpa_decode_seconds(args, kv_sets, q_sets) -> float | None:
     except RuntimeError as e:  # no fused SDPA backend for this shape
         log(f"SDPA decode not timed: {e}")
         return None
+
+
+def reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets, dense_s) -> dict:
+    """The reference's own selection at C2: top-k per query head (not per KV
+    group) on scores cast to bf16, budget n - int(0.98 n) = 2621 of n = 131004
+    candidates (aq_evaluation.py:166, 185-199), then attention over each
+    head's own keep set.  Same inputs and timing as the group-mode step."""
+    import torch
+    from laprune_amd.retrieval import (RetrievalConfig, SparseDecoder, budget_k,
+                                       candidate_window)
+    cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=None, select="head",
+                          score_dtype=torch.bfloat16)
+    dec = SparseDecoder(cb, 1, HQ, HKV, D, T, cfg)
+    cs, ce = candidate_window(T, T, SINK, LOCAL)
+    k = budget_k(ce - cs, cfg.mask_out, cfg.min_remain)
+
+    def step(i):
+        kk, vv = kv_sets[i % N_KV_SETS]
+        c = codes_sets[i % N_CODE_SETS]
+        return dec.step(q_sets[i % N_CODE_SETS], c[:, :, :T], kk[:, :, :T], vv[:, :, :T])
+
+    log("reference-mode leg: per-head selection")
+    for i in range(2):
+        step(i)
+    torch.cuda.synchronize()
+    if args.eager:
+        run = step
+    else:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(2):
+                step(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graphs = []
+        for j in range(N_CODE_SETS):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                step(j)
+            graphs.append(gph)
+        run = lambda i: graphs[i % N_CODE_SETS].replay()  # noqa: E731
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run(i)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+    step(0)
+    torch.cuda.synchronize()
+    sel = dec.selected()
+    ok = bool(sel.shape[-1] == k and sel.shape[-2] == HQ and int(sel.min()) >= cs
+              and int(sel.max()) < ce)
+    return {
+        "selection": (f"top-{k} per query head on bf16-cast scores (reference budget rule, "
+                      f"mask_out 0.98) + {SINK} sink + {LOCAL} local"),
+        "k": k,
+        "sparse_step_us": round(step_s * 1e6, 2),
+        "speedup_vs_dense": round(dense_s / step_s, 3),
+        "selection_check": ok,
+    }
 
 
 def ragged_leg(args, dev, cb) -> dict:
@@ -552,6 +621,9 @@ def main():
             "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
         },
     }
+    if not args.no_reference_mode:
+        result["reference_mode"] = reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets,
+                                                      dense_s)
     if not args.no_ragged:
         result["ragged"] = ragged_leg(args, dev, cb)
     if not args.no_cpu_baseline:

@@ -53,6 +53,12 @@ typedef void* lap_stream_t;
 /* ---- top-k key modes ---------------------------------------------------- */
 #define LAP_KEY_F16   0   /* rank the fp16 score itself                     */
 #define LAP_KEY_BF16  1   /* rank bf16(fp16 score): the model-dtype cast    */
+/* OR-ed into the key_mode of lap_retrieve_score / _topk / _topk_ragged: one
+ * top-k per query head (the reference's selection, aq_evaluation.py:198-201)
+ * instead of one per KV group on the group max.  Selection rows are then
+ * B*Hkv*4, row b*Hq + h; size the workspace with
+ * lap_retrieve_workspace_size(B*Hkv*4, T). */
+#define LAP_SELECT_PER_HEAD 0x10
 
 /* ---- per-sequence plan of one decode step (ragged batches) ---------------
  * The reference decodes a batch with one shared length
@@ -191,6 +197,12 @@ int lap_retrieve_score(const void* lut_gmkg, const uint8_t* codes,
 int lap_retrieve_select(int B, int Hkv, int T, int cand_start, int cand_end, int k,
                         void* out_idx, int out_dtype, void* workspace,
                         size_t workspace_bytes, lap_stream_t stream);
+/* lap_retrieve_select after a lap_retrieve_score with LAP_SELECT_PER_HEAD:
+ * one top-k per query head, out_idx [B][Hkv*4][k] (replaces the per-head
+ * torch.topk, aq_evaluation.py:198-201). */
+int lap_retrieve_select_heads(int B, int Hkv, int T, int cand_start, int cand_end, int k,
+                              void* out_idx, int out_dtype, void* workspace,
+                              size_t workspace_bytes, lap_stream_t stream);
 int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
                       int64_t codes_stride_b, int64_t codes_stride_h,
                       int64_t codes_stride_t, int B, int Hkv, int T,

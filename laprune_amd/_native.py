@@ -28,6 +28,7 @@ LAP_ERR_WORKSPACE = 4
 F32, F16, BF16, U8, I8, I32, I64 = range(7)
 LUT_HMK, LUT_GMKG = 0, 1
 KEY_F16, KEY_BF16 = 0, 1
+SELECT_PER_HEAD = 0x10  # key_mode flag: one top-k per query head
 
 _TORCH_DTYPE = {
     torch.float32: F32,
@@ -59,6 +60,7 @@ SIGNATURES = {
                           i32, vp, sz, vp],
     "lap_retrieve_score": [vp, vp, i64, i64, i64, i32, i32, i32, i32, i32, i32, vp, vp, sz, vp],
     "lap_retrieve_select": [i32, i32, i32, i32, i32, i32, vp, i32, vp, sz, vp],
+    "lap_retrieve_select_heads": [i32, i32, i32, i32, i32, i32, vp, i32, vp, sz, vp],
     "lap_retrieve_topk_ragged": [vp, vp, i64, i64, i64, i32, i32, i32, vp, i32, i32, vp, vp, i32,
                                  vp, sz, vp],
     "lap_topk_select_ragged": [vp, i64, i32, i32, i32, i32, vp, i32, i32, vp, i32, vp, sz, vp],

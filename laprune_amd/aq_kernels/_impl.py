@@ -245,13 +245,16 @@ def aq_topk(scores: torch.Tensor, k: int, group: int = 1, cand_start: int = 0,
 
 def aq_retrieve_topk(lut_gmkg: torch.Tensor, codes: torch.Tensor, k: int, cand_start: int = 0,
                      cand_end: int | None = None, key_dtype: torch.dtype = torch.float16,
-                     index_dtype: torch.dtype = torch.int32, return_scores: bool = False):
-    """Fused LUT scoring + group-max top-k for G=4, M=32, K=256.
+                     index_dtype: torch.dtype = torch.int32, return_scores: bool = False,
+                     per_head: bool = False):
+    """Fused LUT scoring + top-k for G=4, M=32, K=256.
 
     ``lut_gmkg`` [B*Hkv, 32, 256, 4] fp16 (from ``aq_lut_build(..., layout="gmkg")``),
     ``codes`` u8 [B, Hkv, T, 32] (any T/H/B strides, M contiguous).  Returns
-    indices [B, Hkv, min(k, n)] (ascending) and optionally the per-head fp16
-    scores [B, Hkv*4, T].
+    indices [B, Hkv, min(k, n)] (ascending; one top-k per KV group on the max
+    of its 4 query-head scores) or, with ``per_head``, [B, Hkv*4, min(k, n)]
+    (one top-k per query head, the reference's selection), and optionally the
+    per-head fp16 scores [B, Hkv*4, T].
     """
     N.require_cuda(lut_gmkg, codes)
     _check(lut_gmkg.dtype == torch.float16 and codes.dtype == torch.uint8,
@@ -265,16 +268,18 @@ def aq_retrieve_topk(lut_gmkg: torch.Tensor, codes: torch.Tensor, k: int, cand_s
     _check(0 <= cand_start <= ce <= T, "candidate window outside [0, T)")
     ke = min(int(k), ce - cand_start)
     _check(k >= 0, "k must be non-negative")
-    out = torch.empty((B, Hkv, ke), dtype=index_dtype, device=codes.device)
+    rows = Hkv * 4 if per_head else Hkv
+    out = torch.empty((B, rows, ke), dtype=index_dtype, device=codes.device)
     scores = (torch.empty((B, Hkv * 4, T), dtype=torch.float16, device=codes.device)
               if return_scores else None)
-    ws_bytes = N.size_query("lap_retrieve_workspace_size", B * Hkv, T)
+    ws_bytes = N.size_query("lap_retrieve_workspace_size", B * rows, T)
     ws = _workspace(codes.device, ws_bytes)
+    mode = _key_mode(key_dtype) | (N.SELECT_PER_HEAD if per_head else 0)
     with _device_guard(codes):
         N.call("lap_retrieve_topk", N.ptr(lut_gmkg), N.ptr(codes), codes.stride(0),
-               codes.stride(1), codes.stride(2), B, Hkv, T, cand_start, ce, ke,
-               _key_mode(key_dtype), N.ptr(scores), N.ptr(out), N.dtype_code(index_dtype),
-               N.ptr(ws), ws.numel(), N.stream_of(codes))
+               codes.stride(1), codes.stride(2), B, Hkv, T, cand_start, ce, ke, mode,
+               N.ptr(scores), N.ptr(out), N.dtype_code(index_dtype), N.ptr(ws), ws.numel(),
+               N.stream_of(codes))
     return (out, scores) if return_scores else out
 
 

@@ -43,12 +43,16 @@ constexpr int kLutBytes = kG * kM * kK * 2;  // 65536
 
 struct ScoreOut {
   uint16_t* heads;   // [R*4][T] fp16 or null
-  uint16_t* keys;    // [R][T] u16 or null
-  uint32_t* hist;    // [R][nchunk][256] or null
+  uint16_t* keys;    // [R][T] u16 (group max), [R*4][T] with per_head; or null
+  uint32_t* hist;    // [R][nchunk][256], [R*4][nchunk][256] with per_head; or null
   int key_mode;
   int cand_start, cand_end;
   const int32_t* plans;  // lap_row_plan[B] (ragged batches) or null
+  int per_head;          // keys and histograms per query head instead of per KV row
 };
+
+// Selection rows a KV row feeds: its four query heads, or itself.
+__device__ __forceinline__ int key_rows(const ScoreOut& so) { return so.per_head ? kG : 1; }
 
 // Columns a row scores, [0, t_end), and its histogram window [cs, ce): the
 // call's scalars, or the sequence's plan clamped to the T scored columns.
@@ -61,13 +65,49 @@ __device__ __forceinline__ RowCols row_cols(const ScoreOut& so, int b, int T) {
   return RowCols{min(max(p[0], 0), T), p[2], p[3]};
 }
 
-// A workgroup whose chunk lies past its row's columns: empty histogram.
+// Copy the workgroup's level-1 histograms (one per selection row of KV row
+// r) to [row][nchunk][256]; with s_hist null, zeros (a chunk past the row's
+// columns).
+__device__ __forceinline__ void write_hists(const ScoreOut& so, uint32_t (*s_hist)[256],
+                                            int r, int R, int chunk, int tid, int threads) {
+  if (!so.hist) return;
+  const int nchunk = gridDim.x / R, rows = key_rows(so);
+  for (int i = tid; i < rows * 256; i += threads) {
+    const int g = i >> 8, bin = i & 255;
+    so.hist[(((int64_t)r * rows + g) * nchunk + chunk) * 256 + bin] = s_hist ? s_hist[g][bin] : 0u;
+  }
+}
 __device__ __forceinline__ void write_empty_hist(const ScoreOut& so, int r, int R, int chunk,
                                                  int tid, int threads) {
-  if (!so.hist) return;
-  const int nchunk = gridDim.x / R;
-  uint32_t* dst = so.hist + ((int64_t)r * nchunk + chunk) * 256;
-  for (int i = tid; i < 256; i += threads) dst[i] = 0u;
+  write_hists(so, nullptr, r, R, chunk, tid, threads);
+}
+
+// Selection keys of token t of KV row r and their level-1 histogram counts
+// (inside the candidate window): the group max of the four fp16 head scores
+// (fp16 rounding is monotone, so fp16(max) == max of the fp16 scores), or
+// with per_head each head's own key.
+__device__ __forceinline__ void emit_keys(const ScoreOut& so, const RowCols& rc, int r, int T,
+                                          int t, float e0, float e1, float e2, float e3,
+                                          uint32_t (*s_hist)[256]) {
+  if (!so.keys && !so.hist) return;
+  const bool counted = so.hist && t >= rc.cs && t < rc.ce;
+  auto key_of = [&](float e) {
+    const uint16_t h = f2h(e);
+    return so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(h) : f16_key(h);
+  };
+  if (so.per_head) {
+    const float e[kG] = {e0, e1, e2, e3};
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      const uint32_t key = key_of(e[g]);
+      if (so.keys) so.keys[((int64_t)r * kG + g) * T + t] = (uint16_t)key;
+      if (counted) atomicAdd(&s_hist[g][key >> 8], 1u);
+    }
+  } else {
+    const uint32_t key = key_of(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
+    if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
+    if (counted) atomicAdd(&s_hist[0][key >> 8], 1u);
+  }
 }
 
 // Accumulate one token's 32 lookups into four fp32 head sums.
@@ -92,7 +132,7 @@ __global__ __launch_bounds__(THREADS) void score_g4_kernel(
     int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, int chunk_tokens, ScoreOut so,
     _Float16 one) {
   __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
-  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_hist[kG][256];
 
   const int r = blockIdx.x % R;
   const int chunk = blockIdx.x / R;
@@ -122,7 +162,7 @@ __global__ __launch_bounds__(THREADS) void score_g4_kernel(
     }
   }
   if (so.hist) {
-    for (int i = tid; i < 256; i += THREADS) s_hist[i] = 0;
+    for (int i = tid; i < key_rows(so) * 256; i += THREADS) s_hist[i >> 8][i & 255] = 0;
   }
   __syncthreads();
 
@@ -162,21 +202,13 @@ __global__ __launch_bounds__(THREADS) void score_g4_kernel(
         hp[2 * (int64_t)T] = f2h(e2);
         hp[3 * (int64_t)T] = f2h(e3);
       }
-      if (so.keys || so.hist) {
-        // fp16 rounding is monotone, so fp16(max) == max of the fp16 scores.
-        const uint16_t hm = f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
-        const uint32_t key = so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(hm) : f16_key(hm);
-        if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
-        if (so.hist && t >= rc.cs && t < rc.ce) atomicAdd(&s_hist[key >> 8], 1u);
-      }
+      emit_keys(so, rc, r, T, t, e0, e1, e2, e3, s_hist);
     }
   }
 
   if (so.hist) {
     __syncthreads();
-    const int nchunk = gridDim.x / R;
-    uint32_t* dst = so.hist + ((int64_t)r * nchunk + chunk) * 256;
-    for (int i = tid; i < 256; i += THREADS) dst[i] = s_hist[i];
+    write_hists(so, s_hist, r, R, chunk, tid, THREADS);
   }
 }
 
@@ -247,7 +279,7 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
   static_assert(kFill * THREADS * 16 == kLutBytes && THREADS >= 256, "bad THREADS");
   static_assert(kFill + 2 * kAhead <= 23 && 2 * kAhead <= 16, "vmcnt range");
   __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
-  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_hist[kG][256];
 
   const int r = blockIdx.x % R;
   const int chunk = blockIdx.x / R;
@@ -284,7 +316,7 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
     vm_wait(kFill - 1 - i + 2 * kAhead, f[i]);
     s_lut[i * THREADS + tid] = as_uint4(f[i]);
   }
-  if (tid < 256) s_hist[tid] = 0;
+  for (int i = tid; i < key_rows(so) * 256; i += THREADS) s_hist[i >> 8][i & 255] = 0;
   lds_barrier();
 
   const char* lds = reinterpret_cast<const char*>(s_lut);
@@ -305,20 +337,12 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
       hp[2 * (int64_t)T] = f2h(e2);
       hp[3 * (int64_t)T] = f2h(e3);
     }
-    if (so.keys || so.hist) {
-      // fp16 rounding is monotone, so fp16(max) == max of the fp16 scores.
-      const uint16_t hm = f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
-      const uint32_t key = so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(hm) : f16_key(hm);
-      if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
-      if (so.hist && t >= rc.cs && t < rc.ce) atomicAdd(&s_hist[key >> 8], 1u);
-    }
+    emit_keys(so, rc, r, T, t, e0, e1, e2, e3, s_hist);
   }
 
   if (so.hist) {
     __syncthreads();
-    const int nchunk = gridDim.x / R;
-    uint32_t* dst = so.hist + ((int64_t)r * nchunk + chunk) * 256;
-    for (int i = tid; i < 256; i += THREADS) dst[i] = s_hist[i];
+    write_hists(so, s_hist, r, R, chunk, tid, THREADS);
   }
 }
 
@@ -542,13 +566,14 @@ static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, const uin
 // Launch the fast G=4 scorer.  Exposed to the fused retrieval entry point.
 int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int64_t cs_b,
                     int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, uint16_t* heads,
-                    uint16_t* keys, uint32_t* hist, int key_mode, int cand_start,
-                    int cand_end, const int32_t* plans, int* nchunk_out, hipStream_t st) {
+                    uint16_t* keys, uint32_t* hist, int key_mode, bool per_head,
+                    int cand_start, int cand_end, const int32_t* plans, int* nchunk_out,
+                    hipStream_t st) {
   const int R = B * Hkv;
   G4Plan pl;
   int s = g4_plan(R, T, lut_il, &pl);
   if (s != LAP_OK) return s;
-  ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end, plans};
+  ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end, plans, per_head ? 1 : 0};
   dim3 grid((unsigned)(R * pl.nchunk));
   if (pl.kind == 0) {
     if (lut_il)
@@ -619,7 +644,7 @@ extern "C" int lap_lut_score_grouped(const void* lut, int lut_layout, const uint
   if (G == 4 && M == kM && K == kK && score_g4_supported(codes, 0, codes_stride_h, codes_stride_t)) {
     return launch_score_g4(L, lut_layout == LAP_LUT_GMKG, codes, 0, codes_stride_h,
                            codes_stride_t, 1, Hkv, T, static_cast<uint16_t*>(out), nullptr,
-                           nullptr, LAP_KEY_F16, 0, 0, nullptr, nullptr, st);
+                           nullptr, LAP_KEY_F16, false, 0, 0, nullptr, nullptr, st);
   }
   DevInfo di;
   int s = device_info(&di);

@@ -26,8 +26,9 @@ namespace lap {
 
 int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int64_t cs_b,
                     int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, uint16_t* heads,
-                    uint16_t* keys, uint32_t* hist, int key_mode, int cand_start, int cand_end,
-                    const int32_t* plans, int* nchunk_out, hipStream_t st);
+                    uint16_t* keys, uint32_t* hist, int key_mode, bool per_head,
+                    int cand_start, int cand_end, const int32_t* plans, int* nchunk_out,
+                    hipStream_t st);
 bool score_g4_supported(const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t);
 int score_g4_nchunk(int R, int T);
 
@@ -684,21 +685,26 @@ static int retrieve_checks(const void* lut_gmkg, const uint8_t* codes, int64_t c
                            const char* who) {
   LAP_CHECK(lut_gmkg && codes, "%s: null pointer", who);
   LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "%s: bad sizes", who);
-  LAP_CHECK(key_mode == LAP_KEY_F16 || key_mode == LAP_KEY_BF16, "%s: bad key mode", who);
+  const int km = key_mode & ~LAP_SELECT_PER_HEAD;
+  LAP_CHECK(km == LAP_KEY_F16 || km == LAP_KEY_BF16, "%s: bad key mode", who);
   LAP_CHECK(cs_t >= 32, "%s: codes token stride < M=32", who);
   LAP_CHECK_CODE(score_g4_supported(codes, cs_b, cs_h, cs_t), LAP_ERR_UNSUPPORTED,
                  "%s: codes base and strides must be 16-byte aligned", who);
   return LAP_OK;
 }
 
-// The fused scorer: per-head scores (optional), column-indexed group keys
-// and level-1 histograms in the workspace.
+// Selection rows per KV row: 4 (one per query head) with LAP_SELECT_PER_HEAD,
+// else 1 (the group max).
+static int rows_per_kv(int key_mode) { return (key_mode & LAP_SELECT_PER_HEAD) ? 4 : 1; }
+
+// The fused scorer: per-head scores (optional), column-indexed selection
+// keys and level-1 histograms in the workspace (B * Hkv * rows_per_kv rows).
 static int retrieve_score_impl(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b,
                                int64_t cs_h, int64_t cs_t, int B, int Hkv, int T, int cand_start,
                                int cand_end, const lap_row_plan* plans, int key_mode,
                                void* scores_out, void* workspace, size_t workspace_bytes,
                                const char* who, hipStream_t st) {
-  const int R = B * Hkv;
+  const int R = B * Hkv * rows_per_kv(key_mode);
   const int C2 = (T + kChunk - 1) / kChunk;
   Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
   LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
@@ -706,25 +712,27 @@ static int retrieve_score_impl(const void* lut_gmkg, const uint8_t* codes, int64
   int C1 = 0;
   int s = launch_score_g4(static_cast<const uint16_t*>(lut_gmkg), true, codes, cs_b, cs_h, cs_t,
                           B, Hkv, T, static_cast<uint16_t*>(scores_out), w.keys, w.hist1,
-                          key_mode, cand_start, cand_end,
-                          reinterpret_cast<const int32_t*>(plans), &C1, st);
+                          key_mode & ~LAP_SELECT_PER_HEAD, rows_per_kv(key_mode) == 4,
+                          cand_start, cand_end, reinterpret_cast<const int32_t*>(plans), &C1,
+                          st);
   if (s != LAP_OK) return s;
   LAP_CHECK_CODE(C1 <= retrieve_chunk_bound(T), LAP_ERR_INVALID,
                  "%s: internal chunk bound exceeded", who);
   return LAP_OK;
 }
 
-// Levels over the keys and histograms retrieve_score_impl left.
-static int retrieve_select_impl(int B, int Hkv, int T, const SelSpec& sp, int n_max,
+// Levels over the keys and histograms retrieve_score_impl left, for the
+// B * Hkv * rpk selection rows (rpk as the scorer ran: 1 or 4).
+static int retrieve_select_impl(int B, int Hkv, int rpk, int T, const SelSpec& sp, int n_max,
                                 void* out_idx, int out_dtype, int64_t out_stride,
                                 void* workspace, size_t workspace_bytes, const char* who,
                                 hipStream_t st) {
-  const int R = B * Hkv;
+  const int R = B * Hkv * rpk;
   const int C2 = (T + kChunk - 1) / kChunk;
   Ws w = carve(workspace, R, T, retrieve_chunk_bound(T), C2);
   LAP_CHECK_CODE(workspace && workspace_bytes >= w.bytes, LAP_ERR_WORKSPACE,
                  "%s: workspace of %zu bytes needed", who, w.bytes);
-  const int C1 = score_g4_nchunk(R, T);
+  const int C1 = score_g4_nchunk(B * Hkv, T);  // the scorer's chunks per KV row
   LAP_CHECK_CODE(C1 > 0 && C1 <= retrieve_chunk_bound(T), LAP_ERR_HIP,
                  "%s: device query failed", who);
   const int kpt = row_kernel_kpt(T);
@@ -760,24 +768,39 @@ extern "C" int lap_retrieve_score(const void* lut_gmkg, const uint8_t* codes,
                              workspace, workspace_bytes, "lap_retrieve_score", as_stream(stream));
 }
 
+static int retrieve_select_uniform(int B, int Hkv, int rpk, int T, int cand_start, int cand_end,
+                                   int k, void* out_idx, int out_dtype, void* workspace,
+                                   size_t workspace_bytes, const char* who, hipStream_t st) {
+  LAP_CHECK(out_idx, "%s: null output", who);
+  LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "%s: bad sizes", who);
+  LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
+            "%s: candidate window [%d,%d) outside [0,%d)", who, cand_start, cand_end, T);
+  LAP_CHECK(k >= 0, "%s: k must be non-negative", who);
+  LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
+            "%s: out dtype must be int32/int64", who);
+  const int n = cand_end - cand_start;
+  const int ke = std::min(k, n);
+  if (ke == 0) return LAP_OK;
+  return retrieve_select_impl(B, Hkv, rpk, T, uniform_spec(cand_start, n, ke), n, out_idx,
+                              out_dtype, k, workspace, workspace_bytes, who, st);
+}
+
 extern "C" int lap_retrieve_select(int B, int Hkv, int T, int cand_start, int cand_end, int k,
                                    void* out_idx, int out_dtype, void* workspace,
                                    size_t workspace_bytes, lap_stream_t stream) {
   clear_error();
-  LAP_CHECK(out_idx, "lap_retrieve_select: null output");
-  LAP_CHECK(B > 0 && Hkv > 0 && T > 0, "lap_retrieve_select: bad sizes");
-  LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
-            "lap_retrieve_select: candidate window [%d,%d) outside [0,%d)", cand_start, cand_end,
-            T);
-  LAP_CHECK(k >= 0, "lap_retrieve_select: k must be non-negative");
-  LAP_CHECK(out_dtype == LAP_DTYPE_I32 || out_dtype == LAP_DTYPE_I64,
-            "lap_retrieve_select: out dtype must be int32/int64");
-  const int n = cand_end - cand_start;
-  const int ke = std::min(k, n);
-  if (ke == 0) return LAP_OK;
-  return retrieve_select_impl(B, Hkv, T, uniform_spec(cand_start, n, ke), n, out_idx, out_dtype,
-                              k, workspace, workspace_bytes, "lap_retrieve_select",
-                              as_stream(stream));
+  return retrieve_select_uniform(B, Hkv, 1, T, cand_start, cand_end, k, out_idx, out_dtype,
+                                 workspace, workspace_bytes, "lap_retrieve_select",
+                                 as_stream(stream));
+}
+
+extern "C" int lap_retrieve_select_heads(int B, int Hkv, int T, int cand_start, int cand_end,
+                                         int k, void* out_idx, int out_dtype, void* workspace,
+                                         size_t workspace_bytes, lap_stream_t stream) {
+  clear_error();
+  return retrieve_select_uniform(B, Hkv, 4, T, cand_start, cand_end, k, out_idx, out_dtype,
+                                 workspace, workspace_bytes, "lap_retrieve_select_heads",
+                                 as_stream(stream));
 }
 
 extern "C" int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
@@ -793,8 +816,9 @@ extern "C" int lap_retrieve_topk(const void* lut_gmkg, const uint8_t* codes,
                              Hkv, T, cand_start, cand_end, key_mode, scores_out, workspace,
                              workspace_bytes, stream);
   if (s != LAP_OK || k == 0) return s;
-  return lap_retrieve_select(B, Hkv, T, cand_start, cand_end, k, out_idx, out_dtype, workspace,
-                             workspace_bytes, stream);
+  return retrieve_select_uniform(B, Hkv, rows_per_kv(key_mode), T, cand_start, cand_end, k,
+                                 out_idx, out_dtype, workspace, workspace_bytes,
+                                 "lap_retrieve_topk", as_stream(stream));
 }
 
 extern "C" int lap_retrieve_topk_ragged(const void* lut_gmkg, const uint8_t* codes,
@@ -818,6 +842,7 @@ extern "C" int lap_retrieve_topk_ragged(const void* lut_gmkg, const uint8_t* cod
                           T, 0, 0, plans, key_mode, scores_out, workspace, workspace_bytes, who,
                           st);
   if (s != LAP_OK || k_cols == 0) return s;
-  return retrieve_select_impl(B, Hkv, T, ragged_spec(plans, Hkv, k_cols, T), T, out_idx,
-                              out_dtype, k_cols, workspace, workspace_bytes, who, st);
+  const int rpk = rows_per_kv(key_mode);
+  return retrieve_select_impl(B, Hkv, rpk, T, ragged_spec(plans, Hkv * rpk, k_cols, T), T,
+                              out_idx, out_dtype, k_cols, workspace, workspace_bytes, who, st);
 }

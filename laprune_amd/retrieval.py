@@ -167,21 +167,20 @@ class SparseDecoder:
         R = batch * num_kv_heads
         self.lut = torch.empty((R, self.M, self.K, 4), dtype=torch.float16, device=self.dev)
         k_cap = self._k_cap(max_tokens)
+        # selection rows per batch row: KV groups (group max) or query heads
         rows = num_kv_heads if self.cfg.select == "group" else num_q_heads
+        self.H_idx = rows
         self.idx = torch.empty((batch, rows, max(k_cap, 1)), dtype=torch.int32, device=self.dev)
         self.out = torch.empty((batch, num_q_heads, head_dim), dtype=dtype, device=self.dev)
-        self.scores = None
-        if self.cfg.select == "head":
-            self.scores = torch.empty((batch, num_q_heads, max_tokens), dtype=torch.float16,
-                                      device=self.dev)
-        ws_r = N.size_query("lap_retrieve_workspace_size", R, max_tokens)
-        ws_t = N.size_query("lap_topk_workspace_size", batch * num_q_heads, max_tokens)
-        self.ws_sel = torch.empty(max(ws_r, ws_t, 1), dtype=torch.uint8, device=self.dev)
+        ws_r = N.size_query("lap_retrieve_workspace_size", batch * rows, max_tokens)
+        self.ws_sel = torch.empty(max(ws_r, 1), dtype=torch.uint8, device=self.dev)
         max_keep = k_cap + self.cfg.sink_size + max(self.cfg.local_window, 0)
         ws_a = N.size_query("lap_attn_decode_workspace_size", batch, num_q_heads, head_dim,
                             max(max_keep, 1))
         self.ws_attn = torch.zeros(max(ws_a, 1), dtype=torch.uint8, device=self.dev)  # counters start at 0
         self.key_mode = N.KEY_BF16 if self.cfg.score_dtype == torch.bfloat16 else N.KEY_F16
+        if self.cfg.select == "head":  # the scorer emits one key row per query head
+            self.key_mode |= N.SELECT_PER_HEAD
         self.last_k = 0
         self._plans = None
         self._plan_key = None
@@ -244,26 +243,12 @@ class SparseDecoder:
                N.ptr(self.lut), st)
         k = p["k"] if t_codes > 0 else 0
         self.last_k = k
-        if k == 0:
-            H_idx = Hkv if self.cfg.select == "group" else Hq  # sink + local only
-        elif self.cfg.select == "group":
+        H_idx = self.H_idx
+        if k > 0:  # else sink + local only
             N.call("lap_retrieve_topk", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
                    codes.stride(1), codes.stride(2), B, Hkv, t_codes, p["cand_start"],
                    p["cand_end"], k, self.key_mode, None, N.ptr(self.idx), N.I32,
                    N.ptr(self.ws_sel), self.ws_sel.numel(), st)
-            H_idx = Hkv
-        else:
-            # The scorer writes the head scores as [B*Hq][t_codes] rows; the
-            # per-head selection reads them with that row stride.
-            sc = self.scores
-            N.call("lap_retrieve_topk", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
-                   codes.stride(1), codes.stride(2), B, Hkv, t_codes, p["cand_start"],
-                   p["cand_end"], 0, self.key_mode, N.ptr(sc), N.ptr(self.idx), N.I32,
-                   N.ptr(self.ws_sel), self.ws_sel.numel(), st)
-            N.call("lap_topk_select", N.ptr(sc), t_codes, B * Hq, 1, t_codes, p["cand_start"],
-                   p["cand_end"], k, self.key_mode, N.ptr(self.idx), N.I32,
-                   N.ptr(self.ws_sel), self.ws_sel.numel(), st)
-            H_idx = Hq
         scale = 1.0 / math.sqrt(D)
         N.call("lap_sparse_attn_decode", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
                N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, t_total, D, keys.stride(0),
@@ -296,20 +281,11 @@ class SparseDecoder:
                N.ptr(self.lut), st)
         k_cols = max(p["k"] for p in plans)
         T = max(max(t_codes), 1)
-        H_idx = Hkv if self.cfg.select == "group" else Hq
-        if k_cols > 0 and self.cfg.select == "group":
+        H_idx = self.H_idx
+        if k_cols > 0:
             N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
                    codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(pdev), k_cols,
                    self.key_mode, None, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
-                   self.ws_sel.numel(), st)
-        elif k_cols > 0:
-            sc = self.scores
-            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
-                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(pdev), 0,
-                   self.key_mode, N.ptr(sc), None, N.I32, N.ptr(self.ws_sel),
-                   self.ws_sel.numel(), st)
-            N.call("lap_topk_select_ragged", N.ptr(sc), T, B * Hq, 1, Hq, T, N.ptr(pdev), k_cols,
-                   self.key_mode, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
                    self.ws_sel.numel(), st)
         self.last_k = k_cols
         max_sink = max(p["sink"] for p in plans)
@@ -348,22 +324,11 @@ class SparseDecoder:
                N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
                N.ptr(self.lut), st)
         k_cols = self.k_cols
-        if self.cfg.select == "group":
-            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
-                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(plans), k_cols,
-                   self.key_mode, None, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
-                   self.ws_sel.numel(), st)
-            H_idx = Hkv
-        else:
-            sc = self.scores
-            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
-                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(plans), 0,
-                   self.key_mode, N.ptr(sc), None, N.I32, N.ptr(self.ws_sel),
-                   self.ws_sel.numel(), st)
-            N.call("lap_topk_select_ragged", N.ptr(sc), T, B * Hq, 1, Hq, T, N.ptr(plans),
-                   k_cols, self.key_mode, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
-                   self.ws_sel.numel(), st)
-            H_idx = Hq
+        N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
+               codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(plans), k_cols,
+               self.key_mode, None, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
+               self.ws_sel.numel(), st)
+        H_idx = self.H_idx
         self.last_k = k_cols
         N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
                N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, keys.shape[2], D, keys.stride(0),

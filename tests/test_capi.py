@@ -38,7 +38,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.lap_abi_version() == 5
+    assert lib.lap_abi_version() == 6
 
 
 def _err(lib):

@@ -243,6 +243,47 @@ def test_topk_all_equal_and_int32(dev, K, orc):
     assert np.array_equal(idx.cpu().numpy(), np.tile(np.arange(7, 107), (2, 1)))
 
 
+@pytest.mark.parametrize("B,T,k,key_dt", [(2, 8192, 163, torch.bfloat16),
+                                          (2, 30000, 1024, torch.float16),
+                                          (1, 131072, 2621, torch.bfloat16)])
+def test_retrieve_topk_per_head(dev, K, orc, B, T, k, key_dt):
+    """One top-k per query head from the fused scorer (LAP_SELECT_PER_HEAD):
+    the reference's own selection (k = 2621 of 131004 candidates on bf16-cast
+    scores at 128k).  Rows are b * 32 + h; the split form (score, then
+    lap_retrieve_select_heads) gives the same indices."""
+    from laprune_amd import _native as N
+    g = _gen(70 + T + B)
+    Hkv, Hq, cap = 8, 32, 64
+    q = torch.randn(B * Hq, 128, generator=g).bfloat16()
+    cb = torch.randn(32, 256, 128, generator=g) * 0.02
+    buf = torch.randint(0, 256, (B, Hkv, T + cap, 32), generator=g, dtype=torch.uint8)
+    codes = buf.to(dev)[:, :, :T, :]
+    lut = K.aq_lut_build(q.to(dev), cb.to(dev), G=4, layout="gmkg")
+    cs, ce = orc.candidate_window(T, T, 4, 64)
+    idx, scores = K.aq_retrieve_topk(lut, codes, k, cs, ce, key_dtype=key_dt,
+                                     return_scores=True, per_head=True)
+    # the split form
+    kmode = (N.KEY_BF16 if key_dt == torch.bfloat16 else N.KEY_F16) | N.SELECT_PER_HEAD
+    ws = torch.empty(N.size_query("lap_retrieve_workspace_size", B * Hq, T), dtype=torch.uint8,
+                     device=dev)
+    idx2 = torch.full((B, Hq, k), -3, dtype=torch.int32, device=dev)
+    N.call("lap_retrieve_score", N.ptr(lut), N.ptr(codes), codes.stride(0), codes.stride(1),
+           codes.stride(2), B, Hkv, T, cs, ce, kmode, None, N.ptr(ws), ws.numel(),
+           N.stream_of(idx2))
+    N.call("lap_retrieve_select_heads", B, Hkv, T, cs, ce, k, N.ptr(idx2), N.I32, N.ptr(ws),
+           ws.numel(), N.stream_of(idx2))
+    torch.cuda.synchronize()
+    assert tuple(idx.shape) == (B, Hq, k)
+    assert np.array_equal(idx.cpu().numpy(), idx2.cpu().numpy())
+    lut_hmk = orc.lut_build(q.float().numpy(), cb.numpy())
+    for b in range(B):
+        want_s = orc.score_grouped(lut_hmk[b * Hq:(b + 1) * Hq], buf[b, :, :T, :].numpy(), 4)
+        assert np.array_equal(_np_u16(scores[b]), want_s)
+        want_i = orc.topk(want_s, k, group=1, cand_start=cs, cand_end=ce,
+                          key_bf16=key_dt == torch.bfloat16)
+        assert np.array_equal(idx[b].cpu().numpy().astype(np.int64), want_i), b
+
+
 @pytest.mark.parametrize("T,k", [(32768, 1024), (3001, 2933), (20000, 1), (9000, 8000)])
 def test_retrieve_topk_all_equal(dev, K, orc, T, k):
     """Every token scores the same: each key of the window is a candidate

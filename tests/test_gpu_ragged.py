@@ -57,17 +57,27 @@ def _plans_dev(plans, dev):
                         device=dev)
 
 
-@pytest.mark.parametrize("topk,key_dt", [(2048, torch.float16), (None, torch.bfloat16)])
-def test_retrieve_topk_ragged(dev, orc, topk, key_dt):
+@pytest.mark.parametrize("topk,key_dt,per_head,lengths", [
+    (2048, torch.float16, False, "short"),
+    (None, torch.bfloat16, False, "short"),
+    (2048, torch.float16, True, "short"),    # one top-k per query head (row kernel)
+    (None, torch.bfloat16, True, "long"),    # ... rows past 32768 columns (chunked levels)
+])
+def test_retrieve_topk_ragged(dev, orc, topk, key_dt, per_head, lengths):
     """Per-sequence windows and budgets; short rows pad with -1; a sequence
     with no codes selects nothing."""
     from laprune_amd import _native as N
     from laprune_amd.aq_kernels import aq_lut_build
-    g = _gen(300 + (topk or 0))
+    g = _gen(300 + (topk or 0) + 7 * per_head)
     Hkv, Hq, cap = 8, 32, 64
-    t_codes = [5000, 1300, 9000, 0]
-    t_total = [5000, 1337, 9010, 40]
+    if lengths == "short":
+        t_codes = [5000, 1300, 9000, 0]
+        t_total = [5000, 1337, 9010, 40]
+    else:
+        t_codes = [40000, 33000, 0]
+        t_total = [40030, 33000, 12]
     B, T = len(t_codes), max(t_codes)
+    rows = Hq if per_head else Hkv
     q = torch.randn(B * Hq, 128, generator=g).bfloat16()
     cb = torch.randn(32, 256, 128, generator=g) * 0.02
     buf = torch.randint(0, 256, (B, Hkv, T + cap, 32), generator=g, dtype=torch.uint8)
@@ -75,10 +85,12 @@ def test_retrieve_topk_ragged(dev, orc, topk, key_dt):
     lut = aq_lut_build(q.to(dev), cb.to(dev), G=4, layout="gmkg")
     plans = [_plan(orc, tc, tt, topk) for tc, tt in zip(t_codes, t_total)]
     k_cols = max(p["k"] for p in plans)
-    out = torch.full((B, Hkv, k_cols), -7, dtype=torch.int32, device=dev)
-    ws = torch.empty(N.size_query("lap_retrieve_workspace_size", B * Hkv, T), dtype=torch.uint8,
+    out = torch.full((B, rows, k_cols), -7, dtype=torch.int32, device=dev)
+    ws = torch.empty(N.size_query("lap_retrieve_workspace_size", B * rows, T), dtype=torch.uint8,
                      device=dev)
     kmode = N.KEY_BF16 if key_dt == torch.bfloat16 else N.KEY_F16
+    if per_head:
+        kmode |= N.SELECT_PER_HEAD
     pd = _plans_dev(plans, dev)
     N.call("lap_retrieve_topk_ragged", N.ptr(lut), N.ptr(codes), codes.stride(0), codes.stride(1),
            codes.stride(2), B, Hkv, T, N.ptr(pd), k_cols, kmode, None, N.ptr(out), N.I32,
@@ -92,7 +104,7 @@ def test_retrieve_topk_ragged(dev, orc, topk, key_dt):
         if kb == 0:
             continue
         s = orc.score_grouped(lut_hmk[b * Hq:(b + 1) * Hq], buf[b, :, :p["t_codes"]].numpy(), 4)
-        want = orc.topk(s, kb, 4, p["cand_start"], p["cand_end"],
+        want = orc.topk(s, kb, 1 if per_head else 4, p["cand_start"], p["cand_end"],
                         key_bf16=key_dt == torch.bfloat16)
         assert np.array_equal(got[b, :, :kb].astype(np.int64), want), b
 
