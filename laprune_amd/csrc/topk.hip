@@ -34,33 +34,49 @@ int score_g4_nchunk(int R, int T);
 
 namespace {
 
-constexpr int kChunk = 2048;
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+constexpr int kChunk = 2048;   // prep chunk; the smallest level chunk (workspace sizing)
+constexpr int kThreads = 256;  // prep and small-level workgroups
+constexpr int kPer = 8;        // keys per thread in the level kernels, contiguous
 
-// Inclusive suffix sums S(i) = sum_{j>=i} h[j] over 256 LDS bins, then the
-// unique bin b with S(b) >= target > S(b+1).  Returns b and S(b+1) to every
-// thread.  target must satisfy 1 <= target <= S(0).
+// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then the
+// row broadcasts of lanes 15 and 31).
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Suffix sums S(i) = sum_{j>=i} h[j] over 256 LDS bins (waves 0..3 scan the
+// reversed bins), then the unique bin b with S(b) >= target > S(b+1).
+// s_res = {b, S(b+1)}; every thread of the block synchronises.  target must
+// satisfy 1 <= target <= S(0); the block has at least 256 threads.
 __device__ void select_bin(const uint32_t* s_h, uint32_t target, uint32_t* s_wsum,
                            uint32_t* s_res) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  // Scan the reversed bins: x_tid = h[255 - tid]; P(tid) = S(255 - tid).
-  uint32_t x = s_h[255 - tid];
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    uint32_t y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t x = 0, h = 0;
+  if (wave < 4) {
+    h = s_h[255 - tid];
+    x = wave_inclusive_scan(h);
+    if (lane == 63) s_wsum[wave] = x;
   }
-  if (lane == 63) s_wsum[wave] = x;
   __syncthreads();
-  uint32_t add = 0;
-  for (int w = 0; w < wave; ++w) add += s_wsum[w];
-  const uint32_t S_i = x + add;                    // S(255 - tid)
-  const uint32_t S_next = S_i - s_h[255 - tid];    // S(256 - tid)
-  if (S_i >= target && S_next < target) {
-    s_res[0] = 255 - tid;
-    s_res[1] = S_next;
+  if (wave < 4) {
+    uint32_t add = 0;
+    for (int w = 0; w < wave; ++w) add += s_wsum[w];
+    const uint32_t S_i = x + add;  // keys in bins >= 255 - tid
+    const uint32_t S_next = S_i - h;
+    if (S_i >= target && S_next < target) {
+      s_res[0] = 255 - tid;
+      s_res[1] = S_next;
+    }
   }
   __syncthreads();
 }
@@ -129,47 +145,70 @@ struct KeySrc {
   }
 };
 
-// Sum of n values p[0], p[stride], ... with 32 independent loads in flight
-// (the chunk histograms live in L2; latency, not bandwidth, is the cost).
-__device__ __forceinline__ void sum_strided2(const uint32_t* __restrict__ p, int n,
-                                             int64_t stride, int split, uint32_t& tot,
-                                             uint32_t& pre) {
+// Sum of n values p[0], p[stride], ... (and of those with index < split),
+// NB independent loads in flight per round (the chunk histograms live in
+// L2: latency, not bandwidth, is the cost).
+template <int NB>
+__device__ __forceinline__ void sum_strided(const uint32_t* __restrict__ p, int n,
+                                            int64_t stride, int split, uint32_t& tot,
+                                            uint32_t& pre) {
   tot = 0;
   pre = 0;
-  int i = 0;
-  for (; i + 32 <= n; i += 32) {
-    uint32_t v[32];
+  for (int i0 = 0; i0 < n; i0 += NB) {
+    uint32_t v[NB];
 #pragma unroll
-    for (int u = 0; u < 32; ++u) v[u] = p[(int64_t)(i + u) * stride];
+    for (int u = 0; u < NB; ++u) v[u] = p[(int64_t)min(i0 + u, n - 1) * stride];
 #pragma unroll
-    for (int u = 0; u < 32; ++u) {
-      tot += v[u];
-      pre += (i + u) < split ? v[u] : 0u;
+    for (int u = 0; u < NB; ++u) {
+      const bool ok = i0 + u < n;
+      tot += ok ? v[u] : 0u;
+      pre += ok && i0 + u < split ? v[u] : 0u;
     }
-  }
-  for (; i < n; ++i) {
-    const uint32_t v = p[(int64_t)i * stride];
-    tot += v;
-    pre += i < split ? v : 0u;
   }
 }
 
-// Exclusive prefix sum over the 256 threads of the block; returns the
+// Per-bin sums of a row's chunk histograms h[c][256] over c < C (tot) and
+// c < split (pre): TH / 256 threads per bin, thread t taking chunks
+// t / 256, t / 256 + TH / 256, ...; the partial sums meet in s_tot[0] and
+// s_pre[0] (s_pre may be null).
+template <int TH>
+__device__ __forceinline__ void sum_chunk_hists(const uint32_t* __restrict__ h, int C, int split,
+                                                uint32_t (*s_tot)[256], uint32_t (*s_pre)[256]) {
+  constexpr int P = TH / 256;
+  const int tid = threadIdx.x, bin = tid & 255, part = tid >> 8;
+  uint32_t tot, pre;
+  // 32 loads per round for one thread per bin (up to 64 chunks), 8 when four
+  // threads share a bin's chunks
+  sum_strided<P == 1 ? 32 : 8>(h + (int64_t)part * 256 + bin,
+                               part < C ? (C - part + P - 1) / P : 0, P * 256,
+                               split > part ? (split - part + P - 1) / P : 0, tot, pre);
+  s_tot[part][bin] = tot;
+  if (s_pre) s_pre[part][bin] = pre;
+  __syncthreads();
+  if (P > 1) {
+    if (tid < 256) {
+#pragma unroll
+      for (int q = 1; q < P; ++q) {
+        s_tot[0][tid] += s_tot[q][tid];
+        if (s_pre) s_pre[0][tid] += s_pre[q][tid];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Exclusive prefix sum over the TH threads of the block; returns the
 // thread's prefix and writes the block total to *total.
+template <int TH>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t x, uint32_t* s_wsum,
                                                          uint32_t* total) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t inc = x;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t y = __shfl_up(inc, d, 64);
-    if (lane >= d) inc += y;
-  }
+  const uint32_t inc = wave_inclusive_scan(x);
   if (lane == 63) s_wsum[wave] = inc;
   __syncthreads();
   uint32_t before = 0, all = 0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < TH / 64; ++w) {
     const uint32_t v = s_wsum[w];
     before += w < wave ? v : 0u;
     all += v;
@@ -179,36 +218,34 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t x, uint32_t* s
   return before + inc - x;
 }
 
-constexpr int kPer = kChunk / kThreads;  // keys per thread, contiguous
-
-__global__ __launch_bounds__(kThreads) void topk_level2_kernel(
+// Level 2 over chunks of kPer * TH candidates (TH = 256 or 1024): the
+// threshold bin b1 from the row's level-1 histograms, then the low-byte
+// histogram of this chunk's keys in b1 and its count of keys above b1.
+template <int TH>
+__global__ __launch_bounds__(TH) void topk_level2_kernel(
     KeySrc ks, int R, SelSpec sp, const uint32_t* __restrict__ hist1, int C1, int C,
     uint32_t* __restrict__ hist2, uint32_t* __restrict__ gtc, uint32_t* __restrict__ info) {
-  __shared__ uint32_t s_h[256], s_h2[256], s_wsum[kWaves], s_res[2], s_gt;
+  constexpr int CH = kPer * TH;
+  __shared__ uint32_t s_h[TH / 256][256], s_h2[256], s_wsum[TH / 64], s_res[2], s_gt;
   const int r = blockIdx.x % R, c = blockIdx.x / R;
   const int tid = threadIdx.x;
   const SelRow sr = sp.row(r);
-  const int e0 = c * kChunk, e1 = min(sr.n, e0 + kChunk);
+  const int e0 = c * CH, e1 = min(sr.n, e0 + CH);
   if (sr.k == 0 || e0 >= e1) {  // nothing of this row here (ragged rows only)
-    hist2[((int64_t)r * C + c) * 256 + tid] = 0u;
+    if (tid < 256) hist2[((int64_t)r * C + c) * 256 + tid] = 0u;
     if (tid == 0) gtc[(int64_t)r * C + c] = 0u;
     return;
   }
-  // this thread's keys first, so their latency overlaps the histogram sum
+  // this thread's keys first (unconditional, clamped), so their latency
+  // overlaps the histogram sum
   const uint16_t* kr = ks.row(r, sr);
   uint32_t kv[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int e = e0 + tid * kPer + i;
-    kv[i] = e < e1 ? (uint32_t)kr[e] : 0xffffffffu;
-  }
-  uint32_t tot, unused;
-  sum_strided2(hist1 + (int64_t)r * C1 * 256 + tid, C1, 256, 0, tot, unused);
-  s_h[tid] = tot;
-  s_h2[tid] = 0;
+  for (int i = 0; i < kPer; ++i) kv[i] = kr[min(e0 + tid * kPer + i, e1 - 1)];
+  if (tid < 256) s_h2[tid] = 0;
   if (tid == 0) s_gt = 0;
-  __syncthreads();
-  select_bin(s_h, (uint32_t)sr.k, s_wsum, s_res);
+  sum_chunk_hists<TH>(hist1 + (int64_t)r * C1 * 256, C1, 0, s_h, nullptr);
+  select_bin(s_h[0], (uint32_t)sr.k, s_wsum, s_res);
   const uint32_t b1 = s_res[0];
   if (c == 0 && tid == 0) {
     info[r * 4 + 0] = b1;
@@ -217,61 +254,58 @@ __global__ __launch_bounds__(kThreads) void topk_level2_kernel(
   uint32_t gt = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    if (kv[i] == 0xffffffffu) continue;
+    if (e0 + tid * kPer + i >= e1) continue;
     const uint32_t hi = kv[i] >> 8;
     if (hi == b1) atomicAdd(&s_h2[kv[i] & 255u], 1u);
     gt += hi > b1;
   }
   if (gt) atomicAdd(&s_gt, gt);
   __syncthreads();
-  hist2[((int64_t)r * C + c) * 256 + tid] = s_h2[tid];
+  if (tid < 256) hist2[((int64_t)r * C + c) * 256 + tid] = s_h2[tid];
   if (tid == 0) gtc[(int64_t)r * C + c] = s_gt;
 }
 
-template <typename OUT_T>
-__global__ __launch_bounds__(kThreads) void topk_select_kernel(
+// Threshold tau and the ordered compaction of one chunk: keys above tau,
+// then the `need` lowest-column ties, at the chunk's output offset.
+template <int TH, typename OUT_T>
+__global__ __launch_bounds__(TH) void topk_select_kernel(
     KeySrc ks, int R, SelSpec sp, int C, const uint32_t* __restrict__ hist2,
     const uint32_t* __restrict__ gtc, const uint32_t* __restrict__ info,
     OUT_T* __restrict__ out, int64_t out_stride) {
-  __shared__ uint32_t s_tot[256], s_pre[256], s_wsum[kWaves], s_res[2], s_red[kWaves];
+  constexpr int CH = kPer * TH, W = TH / 64;
+  __shared__ uint32_t s_tot[TH / 256][256], s_pre[TH / 256][256], s_wsum[W], s_res[2], s_red[W];
   const int r = blockIdx.x % R, c = blockIdx.x / R;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const SelRow sr = sp.row(r);
   OUT_T* orow = out + (int64_t)r * out_stride;
   if (sp.plans && c == 0)  // ragged rows: pad past the row's k with -1
-    for (int i = sr.k + tid; i < sp.k_cols; i += kThreads) orow[i] = (OUT_T)-1;
-  const int e0 = c * kChunk, e1 = min(sr.n, e0 + kChunk);
+    for (int i = sr.k + tid; i < sp.k_cols; i += TH) orow[i] = (OUT_T)-1;
+  const int e0 = c * CH, e1 = min(sr.n, e0 + CH);
   if (sr.k == 0 || e0 >= e1) return;
   const uint16_t* kr = ks.row(r, sr);
   uint32_t kv[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int e = e0 + tid * kPer + i;
-    kv[i] = e < e1 ? (uint32_t)kr[e] : 0u;
-  }
+  for (int i = 0; i < kPer; ++i) kv[i] = kr[min(e0 + tid * kPer + i, e1 - 1)];
   const uint32_t b1 = info[r * 4 + 0], gt1 = info[r * 4 + 1];
-  uint32_t tot, pre;
-  sum_strided2(hist2 + (int64_t)r * C * 256 + tid, C, 256, c, tot, pre);
-  s_tot[tid] = tot;
-  s_pre[tid] = pre;
-  // Selected-above-threshold count of earlier chunks: gtc prefix.
-  uint32_t g = 0;
-  for (int cc = tid; cc < c; cc += kThreads) g += gtc[(int64_t)r * C + cc];
-  __syncthreads();
+  // Selected-above-threshold count of earlier chunks (gtc prefix): the first
+  // TH counts are requested before the histogram loads and added after them.
+  uint32_t g = tid < c ? gtc[(int64_t)r * C + tid] : 0u;
+  sum_chunk_hists<TH>(hist2 + (int64_t)r * C * 256, C, c, s_tot, s_pre);
+  for (int cc = tid + TH; cc < c; cc += TH) g += gtc[(int64_t)r * C + cc];
   const uint32_t k2 = (uint32_t)sr.k - gt1;
-  select_bin(s_tot, k2, s_wsum, s_res);
+  select_bin(s_tot[0], k2, s_wsum, s_res);
   const uint32_t b2 = s_res[0];
   const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
   const uint32_t tau = (b1 << 8) | b2;
-  const uint32_t ties_before = s_pre[b2];
+  const uint32_t ties_before = s_pre[0][b2];
   // base = gtc prefix + level-2 keys above b2 in earlier chunks + ties taken.
-  uint32_t part = g + (tid > (int)b2 ? s_pre[tid] : 0u);
+  uint32_t acc = g + (tid < 256 && tid > (int)b2 ? s_pre[0][tid] : 0u);
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) part += __shfl_xor(part, d, 64);
-  if (lane == 0) s_red[wave] = part;
+  for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, 64);
+  if (lane == 0) s_red[wave] = acc;
   __syncthreads();
   uint32_t base = 0;
-  for (int w = 0; w < kWaves; ++w) base += s_red[w];
+  for (int w = 0; w < W; ++w) base += s_red[w];
   base += min(need, ties_before);
 
   // Ordered compaction: each thread owns kPer consecutive candidates.
@@ -283,11 +317,11 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
     ngt += (valid && kv[i] > tau) ? 1u : 0u;
   }
   uint32_t all_ties;
-  const uint32_t tie_rank0 = ties_before + block_exclusive_scan(ntie, s_wsum, &all_ties);
+  const uint32_t tie_rank0 = ties_before + block_exclusive_scan<TH>(ntie, s_wsum, &all_ties);
   // ties this thread may take: ranks [tie_rank0, tie_rank0 + ntie) below need
   const uint32_t take = tie_rank0 >= need ? 0u : min(ntie, need - tie_rank0);
   uint32_t all_sel;
-  uint32_t pos = base + block_exclusive_scan(ngt + take, s_wsum, &all_sel);
+  uint32_t pos = base + block_exclusive_scan<TH>(ngt + take, s_wsum, &all_sel);
   uint32_t taken = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -331,23 +365,35 @@ Ws carve(void* base, int R, int64_t key_cols, int C1, int C2) {
   return w;
 }
 
-// Level 2 and the compaction over C2 chunks of kChunk candidates; n_max is
-// the widest row's window.
-int run_levels(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int C1,
-               void* out, int out_dtype, int64_t out_stride, hipStream_t st) {
-  const int C2 = (n_max + kChunk - 1) / kChunk;
+// Level 2 and the compaction over chunks of candidates; n_max is the widest
+// row's window.  Each workgroup re-sums its row's chunk histograms, so when
+// 2048-key chunks would make more than 1024 workgroups (many long rows: one
+// top-k per query head at 128k), 8192-key chunks on 1024-thread workgroups
+// cut that repeated reading fourfold.
+template <int TH>
+int run_levels_th(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int C1,
+                  void* out, int out_dtype, int64_t out_stride, hipStream_t st) {
+  const int C2 = (n_max + kPer * TH - 1) / (kPer * TH);
   if (C2 == 0) return LAP_OK;
-  hipLaunchKernelGGL(topk_level2_kernel, dim3(R * C2), dim3(kThreads), 0, st, ks, R, sp,
-                     w.hist1, C1, C2, w.hist2, w.gtc, w.info);
+  hipLaunchKernelGGL(topk_level2_kernel<TH>, dim3(R * C2), dim3(TH), 0, st, ks, R, sp, w.hist1,
+                     C1, C2, w.hist2, w.gtc, w.info);
   LAP_LAUNCH_CHECK("topk_level2_kernel");
   if (out_dtype == LAP_DTYPE_I64)
-    hipLaunchKernelGGL(topk_select_kernel<int64_t>, dim3(R * C2), dim3(kThreads), 0, st, ks, R,
+    hipLaunchKernelGGL((topk_select_kernel<TH, int64_t>), dim3(R * C2), dim3(TH), 0, st, ks, R,
                        sp, C2, w.hist2, w.gtc, w.info, static_cast<int64_t*>(out), out_stride);
   else
-    hipLaunchKernelGGL(topk_select_kernel<int32_t>, dim3(R * C2), dim3(kThreads), 0, st, ks, R,
+    hipLaunchKernelGGL((topk_select_kernel<TH, int32_t>), dim3(R * C2), dim3(TH), 0, st, ks, R,
                        sp, C2, w.hist2, w.gtc, w.info, static_cast<int32_t*>(out), out_stride);
   LAP_LAUNCH_CHECK("topk_select_kernel");
   return LAP_OK;
+}
+
+int run_levels(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int C1,
+               void* out, int out_dtype, int64_t out_stride, hipStream_t st) {
+  const int64_t small_wgs = (int64_t)R * ((n_max + kChunk - 1) / kChunk);
+  if (small_wgs > 1024)
+    return run_levels_th<1024>(w, ks, R, sp, n_max, C1, out, out_dtype, out_stride, st);
+  return run_levels_th<kThreads>(w, ks, R, sp, n_max, C1, out, out_dtype, out_stride, st);
 }
 
 // ---- One workgroup per row: level 2 and the compaction in one launch.
@@ -365,47 +411,6 @@ int run_levels(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int 
 constexpr int kRowThreads = 1024;
 constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kRowMaxKpt = 32;
-
-// Inclusive prefix sum over the 64 lanes of a wave (DPP row shifts, then the
-// row broadcasts of lanes 15 and 31).
-__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x) {
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31
-  return x;
-}
-
-__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-}
-
-// select_bin for a 1024-thread block: waves 0..3 scan the 256 bins from the
-// top, all threads synchronise.  s_res = {bin, count above the bin}.
-__device__ void row_select_bin(const uint32_t* s_h, uint32_t target, uint32_t* s_wsum,
-                               uint32_t* s_res) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t x = 0, h = 0;
-  if (wave < 4) {
-    h = s_h[255 - tid];
-    x = wave_inclusive_scan(h);
-    if (lane == 63) s_wsum[wave] = x;
-  }
-  __syncthreads();
-  if (wave < 4) {
-    uint32_t add = 0;
-    for (int w = 0; w < wave; ++w) add += s_wsum[w];
-    const uint32_t S_i = x + add;  // keys in bins >= 255 - tid
-    const uint32_t S_next = S_i - h;
-    if (S_i >= target && S_next < target) {
-      s_res[0] = 255 - tid;
-      s_res[1] = S_next;
-    }
-  }
-  __syncthreads();
-}
 
 // Dynamic LDS of topk_row_kernel<KPT>: the candidate segments.
 constexpr size_t row_kernel_lds(int kpt) { return (size_t)kRowThreads * kpt * sizeof(uint32_t); }
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(
   __syncthreads();
   if (tid < 256) s_h[0][tid] += s_h[1][tid] + s_h[2][tid] + s_h[3][tid];
   __syncthreads();
-  row_select_bin(s_h[0], (uint32_t)sr.k, s_wsum, s_res);
+  select_bin(s_h[0], (uint32_t)sr.k, s_wsum, s_res);
   const uint32_t b1 = s_res[0], gt1 = s_res[1];
 
   // Candidates (window keys in bins >= b1) into the wave's segment, in
@@ -488,7 +493,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(
   }
   __syncthreads();
   const uint32_t k2 = (uint32_t)sr.k - gt1;
-  row_select_bin(s_h2, k2, s_wsum, s_res);
+  select_bin(s_h2, k2, s_wsum, s_res);
   const uint32_t tau = (b1 << 8) | s_res[0];
   const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
 
