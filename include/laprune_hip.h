@@ -272,12 +272,9 @@ int lap_gqa_gather_kv(const void* keys, const void* vals, int dtype,
  *           n_idx == 0)
  *   out   [B][Hq][D] contiguous, q dtype
  * ======================================================================= */
-/* Workspace of the two decode entry points: a 256-byte-aligned block of
- * per-row arrival counters followed by fp32 split partials (m, l, o).  The
- * counter block (the leading lap_attn_decode_workspace_size bytes' first
- * align256(B * Hq * 4) bytes) must be zero before the first call on a
- * workspace (zero it once at allocation); every call leaves it zero.  Calls
- * that share a workspace must be ordered (same stream). */
+/* Workspace of the two decode entry points: the fp32 split partials
+ * (m, l, o) the combine kernel merges.  Calls that share a workspace must be
+ * ordered (same stream). */
 int lap_attn_decode_workspace_size(int B, int Hq, int D, int max_keys, size_t* bytes);
 int lap_sparse_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                            const void* keys, const void* vals, int dtype,

@@ -34,21 +34,6 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         return buf
 
 
-_zws_cache: dict = {}
-
-
-def _zeroed_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Attention-decode scratch: its leading block of arrival counters must be
-    zero before the first call; the kernels leave it zero after every call."""
-    key = (device.type, device.index)
-    with _ws_lock:
-        buf = _zws_cache.get(key)
-        if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _zws_cache[key] = buf
-        return buf
-
-
 def _device_guard(t: torch.Tensor):
     return torch.cuda.device(t.device)
 
@@ -389,7 +374,7 @@ def sparse_attn_decode(q: torch.Tensor, keys: torch.Tensor, vals: torch.Tensor,
     out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     L = n_idx + sink + tail_count
     ws_bytes = N.size_query("lap_attn_decode_workspace_size", B, Hq, D, max(L, 1))
-    ws = _zeroed_workspace(q.device, ws_bytes)
+    ws = _workspace(q.device, ws_bytes)
     with _device_guard(q):
         N.call("lap_sparse_attn_decode", N.ptr(q3), q3.stride(0), q3.stride(1), N.ptr(keys),
                N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D, keys.stride(0),
@@ -412,7 +397,7 @@ def dense_attn_decode(q: torch.Tensor, keys: torch.Tensor, vals: torch.Tensor,
     sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
     out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
     ws_bytes = N.size_query("lap_attn_decode_workspace_size", B, Hq, D, max(T, 1))
-    ws = _zeroed_workspace(q.device, ws_bytes)
+    ws = _workspace(q.device, ws_bytes)
     with _device_guard(q):
         N.call("lap_dense_attn_decode", N.ptr(q3), q3.stride(0), q3.stride(1), N.ptr(keys),
                N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D, keys.stride(0),

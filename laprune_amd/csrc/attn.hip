@@ -20,7 +20,7 @@
 // step's keep-list positions are read two steps ahead and its K/V rows one
 // step ahead, and nothing in the loop waits on the whole workgroup.  The
 // waves' states merge through LDS at the end; splits are merged by a combine
-// kernel (or, on request, in-kernel by the last-arriving workgroup of a row).
+// kernel.
 #include "common.h"
 
 #include <cstdlib>
@@ -32,7 +32,6 @@ namespace {
 constexpr int kTile = 64;     // keys per workgroup step (4 waves x 16)
 constexpr int kKeys = 16;     // keys per wave step
 constexpr int kThreads = 256;
-constexpr int kMaxInKernelSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int DT>
@@ -57,7 +56,6 @@ struct AttnArgs {
   int per_split, nsplit;
   uint16_t* out;     // [B][Hq][D]
   float* part;       // [B][Hq][nsplit][D + 2] (m, l, o...)
-  unsigned* ctr;     // [B * H_idx] arrival counters (zero between calls), or null
   const int32_t* plans;  // lap_row_plan[B] (ragged batches) or null
 };
 
@@ -236,8 +234,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   static_assert(D % 64 == 0 && HPR <= 8, "D must be a multiple of 64, HPR <= 8");
   __shared__ float s_m[4][HPR], s_l[4][HPR];
   __shared__ __attribute__((aligned(16))) float s_o[4][HPR][D];
-  __shared__ float s_w[HPR][kMaxInKernelSplits];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = blockIdx.x % a.nsplit;
@@ -347,50 +343,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
       pp[2 + d] = o;
     }
   }
-  if (a.nsplit == 1 || !a.ctr) return;
-
-  // The last workgroup of the row to finish merges the splits.  One thread
-  // publishes (device-scope release after the workgroup barrier) and counts;
-  // a per-row counter keeps the atomics short.  The merging workgroup
-  // acquires before reading the other splits and leaves the counter at zero.
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    s_last = atomicAdd(&a.ctr[br], 1u) == (unsigned)(a.nsplit - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  if (tid == 0) __threadfence();
-  __syncthreads();
-  for (int i = tid; i < HPR * a.nsplit; i += kThreads) {
-    const int g = i / a.nsplit, sp = i - g * a.nsplit;
-    s_w[g][sp] = a.part[(((int64_t)b * a.Hq + h0 + g) * a.nsplit + sp) * (D + 2)];
-  }
-  __syncthreads();
-  if (tid < HPR) {
-    float M = -INFINITY;
-    for (int sp = 0; sp < a.nsplit; ++sp) M = fmaxf(M, s_w[tid][sp]);
-    const float* pp = a.part + ((int64_t)b * a.Hq + h0 + tid) * a.nsplit * (D + 2);
-    float l = 0.f;
-    for (int sp = 0; sp < a.nsplit; ++sp) {
-      const float ms = s_w[tid][sp];
-      const float wt = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
-      s_w[tid][sp] = wt;
-      l += pp[(int64_t)sp * (D + 2) + 1] * wt;
-    }
-    s_l[0][tid] = l;
-  }
-  __syncthreads();
-  for (int i = tid; i < HPR * D; i += kThreads) {
-    const int g = i / D, d = i - g * D;
-    const float* pp = a.part + ((int64_t)b * a.Hq + h0 + g) * a.nsplit * (D + 2) + 2 + d;
-    float o = 0.f;
-#pragma unroll 4
-    for (int sp = 0; sp < a.nsplit; ++sp) o = __builtin_fmaf(pp[(int64_t)sp * (D + 2)], s_w[g][sp], o);
-    const float l = s_l[0][g];
-    a.out[((int64_t)b * a.Hq + h0 + g) * D + d] = st16<DT>(l > 0.f ? o / l : 0.f);
-  }
-  if (tid == 0) a.ctr[br] = 0u;  // ready for the next call
 }
 
 // Merge split partials: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
@@ -483,16 +435,6 @@ hipError_t launch_attn_dt(const AttnArgs& a, int hpr, int D, hipStream_t st) {
   }
 }
 
-// LAPRUNE_ATTN_MERGE=kernel merges splits in the attention kernel (last
-// workgroup of a row); default: a separate combine kernel.
-bool attn_merge_in_kernel() {
-  static const bool v = [] {
-    const char* e = getenv("LAPRUNE_ATTN_MERGE");
-    return e && strcmp(e, "kernel") == 0;
-  }();
-  return v;
-}
-
 int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_t ws_bytes,
              hipStream_t st) {
   const int L = a.n_idx + a.sink + a.tail_count;
@@ -504,17 +446,12 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
   a.per_split = (a.per_split + kTile - 1) / kTile * kTile;
   if (a.per_split < kTile) a.per_split = kTile;
   a.nsplit = L > 0 ? (L + a.per_split - 1) / a.per_split : 1;
-  // Workspace: [B * H_idx arrival counters, 256-byte block][split partials
-  // [B][Hq][nsplit][D + 2]].  Up to 64 splits merge in-kernel (the counters
-  // must be zero before a call and are left zero); more use a combine kernel.
-  const size_t ctr_bytes = align_up((size_t)a.B * a.H_idx * sizeof(unsigned), 256);
-  const bool merge_in_kernel = a.nsplit <= kMaxInKernelSplits && attn_merge_in_kernel();
+  // Workspace: the split partials [B][Hq][nsplit][D + 2] (m, l, o...).
   if (a.nsplit > 1) {
-    const size_t need = ctr_bytes + (size_t)a.B * a.Hq * a.nsplit * (D + 2) * sizeof(float);
+    const size_t need = (size_t)a.B * a.Hq * a.nsplit * (D + 2) * sizeof(float);
     LAP_CHECK_CODE(workspace && ws_bytes >= need, LAP_ERR_WORKSPACE,
                    "attention decode: workspace of %zu bytes needed", need);
-    a.ctr = merge_in_kernel ? static_cast<unsigned*>(workspace) : nullptr;
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ctr_bytes);
+    a.part = static_cast<float*>(workspace);
   }
   hipError_t e;
   const bool i64 = idx_dtype == LAP_DTYPE_I64;
@@ -525,7 +462,7 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
     e = i64 ? launch_attn_dt<LAP_DTYPE_BF16, int64_t>(a, hpr, D, st)
             : launch_attn_dt<LAP_DTYPE_BF16, int32_t>(a, hpr, D, st);
   LAP_HIP(e, "attn_decode_kernel launch");
-  if (a.nsplit > 1 && !merge_in_kernel) {
+  if (a.nsplit > 1) {
     if (dtype == LAP_DTYPE_F16)
       hipLaunchKernelGGL(attn_combine_kernel<LAP_DTYPE_F16>, dim3(a.B * a.Hq), dim3(256), 0, st,
                          a.part, a.nsplit, D, a.out);
@@ -568,10 +505,8 @@ extern "C" int lap_attn_decode_workspace_size(int B, int Hq, int D, int max_keys
   int ns = (max_keys + kTile - 1) / kTile;
   if (ns > 1024) ns = 1024;
   if (ns < 1) ns = 1;
-  // arrival counters (one per selection row; at most one per query head)
-  // followed by the split partials
-  *bytes = align_up((size_t)B * Hq * sizeof(unsigned), 256) +
-           (size_t)B * Hq * ns * (D + 2) * sizeof(float);
+  // the split partials
+  *bytes = (size_t)B * Hq * ns * (D + 2) * sizeof(float);
   return LAP_OK;
 }
 

@@ -491,9 +491,13 @@ struct G4Plan {
   int kind, threads, tok, pref, chunk_tokens, nchunk;
 };
 
-// LAPRUNE_SCORE_CFG overrides the choice for measurements: "legacy" or
-// "<threads>x<tok>p<pref>" (threads in {256, 512, 1024}, tok in {1, 2, 4, 8},
-// pref in {1, 2, tok}).
+// Launch shapes of score_g4p_kernel, largest chunk first: {threads, tokens
+// per thread, stages in flight}.
+static const int kG4Shapes[][3] = {{1024, 4, 1}, {512, 4, 1}, {512, 2, 1}, {256, 2, 1},
+                                   {256, 1, 1}};
+
+// LAPRUNE_SCORE_CFG overrides the choice for measurements: "legacy" or one
+// of the shapes above as "<threads>x<tok>p<pref>".
 static bool score_cfg_override(int* threads, int* tok, int* pref, bool* legacy) {
   static const char* e = getenv("LAPRUNE_SCORE_CFG");
   if (!e || !*e) return false;
@@ -503,9 +507,9 @@ static bool score_cfg_override(int* threads, int* tok, int* pref, bool* legacy) 
   }
   int th = 0, tk = 0, pf = 0;
   if (sscanf(e, "%dx%dp%d", &th, &tk, &pf) != 3) return false;
-  if (!(th == 256 || th == 512 || th == 1024) || !(tk == 1 || tk == 2 || tk == 4 || tk == 8))
-    return false;
-  if (!(pf == 1 || pf == 2 || pf == tk)) return false;
+  bool known = false;
+  for (const auto& sh : kG4Shapes) known |= sh[0] == th && sh[1] == tk && sh[2] == pf;
+  if (!known) return false;
   *threads = th;
   *tok = tk;
   *pref = pf;
@@ -535,12 +539,10 @@ static int g4_plan(int R, int T, bool lut_il, G4Plan* p) {
   if (!forced) {
     // Largest chunk that still gives every CU a workgroup; the smallest
     // shape when even that cannot.
-    static const int kShapes[][3] = {{1024, 4, 1}, {512, 4, 1}, {512, 2, 1}, {256, 2, 1},
-                                     {256, 1, 1}};
     th = 256;
     tk = 1;
     pf = 1;
-    for (const auto& sh : kShapes) {
+    for (const auto& sh : kG4Shapes) {
       const int ct = sh[0] * sh[1];
       if ((int64_t)R * ((T + ct - 1) / ct) >= di.cu_count) {
         th = sh[0];
@@ -589,11 +591,7 @@ int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int6
   case (TH * 16 + TK) * 16 + PF:                                                          \
     launch_g4p<TH, TK, PF>(grid, st, lut, codes, cs_b, cs_h, cs_t, Hkv, R, T, so);        \
     break;
-      LAP_G4P(1024, 4, 1) LAP_G4P(1024, 4, 2) LAP_G4P(1024, 4, 4)
-      LAP_G4P(1024, 2, 1) LAP_G4P(1024, 2, 2) LAP_G4P(1024, 8, 1) LAP_G4P(1024, 8, 2)
-      LAP_G4P(512, 8, 1) LAP_G4P(512, 8, 2) LAP_G4P(512, 4, 1) LAP_G4P(512, 4, 2)
-      LAP_G4P(512, 4, 4) LAP_G4P(512, 2, 1) LAP_G4P(512, 2, 2)
-      LAP_G4P(256, 8, 1) LAP_G4P(256, 8, 2) LAP_G4P(256, 4, 1) LAP_G4P(256, 2, 1)
+      LAP_G4P(1024, 4, 1) LAP_G4P(512, 4, 1) LAP_G4P(512, 2, 1) LAP_G4P(256, 2, 1)
       LAP_G4P(256, 1, 1)
 #undef LAP_G4P
       default:

@@ -177,7 +177,7 @@ class SparseDecoder:
         max_keep = k_cap + self.cfg.sink_size + max(self.cfg.local_window, 0)
         ws_a = N.size_query("lap_attn_decode_workspace_size", batch, num_q_heads, head_dim,
                             max(max_keep, 1))
-        self.ws_attn = torch.zeros(max(ws_a, 1), dtype=torch.uint8, device=self.dev)  # counters start at 0
+        self.ws_attn = torch.empty(max(ws_a, 1), dtype=torch.uint8, device=self.dev)
         self.key_mode = N.KEY_BF16 if self.cfg.score_dtype == torch.bfloat16 else N.KEY_F16
         if self.cfg.select == "head":  # the scorer emits one key row per query head
             self.key_mode |= N.SELECT_PER_HEAD
@@ -363,7 +363,7 @@ class DenseDecoder:
         self.out = torch.empty((batch, num_q_heads, head_dim), dtype=dtype, device=device)
         ws = N.size_query("lap_attn_decode_workspace_size", batch, num_q_heads, head_dim,
                           max(max_tokens, 1))
-        self.ws = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)  # counters start at 0
+        self.ws = torch.empty(max(ws, 1), dtype=torch.uint8, device=device)
         self._plans = None
         self._plan_key = None
 
