@@ -12,27 +12,18 @@
 // with the fp32 add).  The grid is 1-D with the KV row in the low bits of the
 // block id: workgroups are dealt round-robin to the 8 XCDs, so with 8 KV rows
 // each XCD scores one KV group and its 64 KiB table stays in that XCD's L2.
-// Optionally the kernel also emits the group-max selection key (the max of
-// the four fp16 head scores, as an orderable 16-bit key) and a per-workgroup
-// 256-bin histogram of the key's high byte over the candidate window, which
-// is the first radix level of the top-k (topk.hip).
+// The table comes from either LUT layout: the interleaved [Hkv][M][K][G]
+// is copied, the reference's [Hkv*G][M][K] is interleaved while it is
+// loaded.  Optionally the kernel also emits selection keys (the group max of
+// the four fp16 head scores, or each head's own score, as orderable 16-bit
+// keys) and per-workgroup 256-bin histograms of the keys' high byte over the
+// candidate window, the first radix level of the top-k (topk.hip).
 #include "common.h"
 
 #include <cstdlib>
 #include <cstring>
 
 namespace lap {
-
-// Tunables of the fast scorer (read once from the environment; documented in
-// the design notes):  LAPRUNE_SCORE_WG_PER_CU  (default 2 workgroups per CU).
-static int score_wg_per_cu() {
-  static int v = [] {
-    const char* e = getenv("LAPRUNE_SCORE_WG_PER_CU");
-    int x = e ? atoi(e) : 2;
-    return x > 0 && x <= 16 ? x : 2;
-  }();
-  return v;
-}
 
 namespace {
 
@@ -126,93 +117,7 @@ __device__ __forceinline__ void score_token(const char* __restrict__ lds, const 
   }
 }
 
-template <int THREADS, bool LUT_IL>
-__global__ __launch_bounds__(THREADS) void score_g4_kernel(
-    const uint16_t* __restrict__ lut, const uint8_t* __restrict__ codes, int64_t cs_b,
-    int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, int chunk_tokens, ScoreOut so,
-    _Float16 one) {
-  __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
-  __shared__ uint32_t s_hist[kG][256];
-
-  const int r = blockIdx.x % R;
-  const int chunk = blockIdx.x / R;
-  const int tid = threadIdx.x;
-  const int b = r / Hkv, hkv = r - b * Hkv;
-  const RowCols rc = row_cols(so, b, T);
-  const int t0 = chunk * chunk_tokens;
-  const int t1 = min(rc.t_end, t0 + chunk_tokens);
-  if (t0 >= t1) {
-    write_empty_hist(so, r, R, chunk, tid, THREADS);
-    return;
-  }
-
-  // Fill the [M][K][G] table.
-  if (LUT_IL) {
-    const uint4* src = reinterpret_cast<const uint4*>(lut + (int64_t)r * (kG * kM * kK));
-#pragma unroll 4
-    for (int i = tid; i < kLutBytes / 16; i += THREADS) s_lut[i] = src[i];
-  } else {
-    // Reference layout [R*4][M][K]: gather the four heads of each (m,k).
-    const uint16_t* src = lut + (int64_t)r * (kG * kM * kK);
-    uint2* dst = reinterpret_cast<uint2*>(s_lut);
-    for (int mk = tid; mk < kM * kK; mk += THREADS) {
-      const uint32_t h0 = src[mk], h1 = src[kM * kK + mk];
-      const uint32_t h2 = src[2 * kM * kK + mk], h3 = src[3 * kM * kK + mk];
-      dst[mk] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
-    }
-  }
-  if (so.hist) {
-    for (int i = tid; i < key_rows(so) * 256; i += THREADS) s_hist[i >> 8][i & 255] = 0;
-  }
-  __syncthreads();
-
-  const char* lds = reinterpret_cast<const char*>(s_lut);
-  const uint8_t* crow = codes + (int64_t)b * cs_b + (int64_t)hkv * cs_h;
-
-  for (int base = t0; base < t1; base += 2 * THREADS) {
-    const int ta = base + tid, tb = base + THREADS + tid;
-    const bool va = ta < t1, vb = tb < t1;
-    uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0, b0 = a0, b1 = a0;
-    if (va) {
-      const uint4* p = reinterpret_cast<const uint4*>(crow + (int64_t)ta * cs_t);
-      a0 = p[0];
-      a1 = p[1];
-    }
-    if (vb) {
-      const uint4* p = reinterpret_cast<const uint4*>(crow + (int64_t)tb * cs_t);
-      b0 = p[0];
-      b1 = p[1];
-    }
-    float x0 = 0.f, x1 = 0.f, x2 = 0.f, x3 = 0.f;
-    float y0 = 0.f, y1 = 0.f, y2 = 0.f, y3 = 0.f;
-    score_token(lds, a0, a1, one, x0, x1, x2, x3);
-    score_token(lds, b0, b1, one, y0, y1, y2, y3);
-
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const bool v = s == 0 ? va : vb;
-      if (!v) continue;
-      const int t = s == 0 ? ta : tb;
-      const float e0 = s == 0 ? x0 : y0, e1 = s == 0 ? x1 : y1;
-      const float e2 = s == 0 ? x2 : y2, e3 = s == 0 ? x3 : y3;
-      if (so.heads) {
-        uint16_t* hp = so.heads + (int64_t)(r * kG) * T + t;
-        hp[0] = f2h(e0);
-        hp[(int64_t)T] = f2h(e1);
-        hp[2 * (int64_t)T] = f2h(e2);
-        hp[3 * (int64_t)T] = f2h(e3);
-      }
-      emit_keys(so, rc, r, T, t, e0, e1, e2, e3, s_hist);
-    }
-  }
-
-  if (so.hist) {
-    __syncthreads();
-    write_hists(so, s_hist, r, R, chunk, tid, THREADS);
-  }
-}
-
-// Pipelined fused scorer (GMKG table only).  A workgroup owns THREADS * TOK
+// Pipelined fused scorer (either table layout).  A workgroup owns THREADS * TOK
 // consecutive tokens of one KV row; thread tid scores tokens
 // t0 + j * THREADS + tid, j < TOK, as TOK stages.  Every CU of the chip
 // starts at once, so requesting all code rows up front lets the memory
@@ -268,15 +173,48 @@ __device__ __forceinline__ void vm_wait(int n, u32x4& a, u32x4& b) {
   }
 }
 
+template <int N>
+__device__ __forceinline__ void vmw4(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
+}
+__device__ __forceinline__ void vm_wait(int n, u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  switch (n) {
+#define LAP_VW(N) case N: vmw4<N>(a, b, c, d); break;
+    LAP_VW(0) LAP_VW(1) LAP_VW(2) LAP_VW(3) LAP_VW(4) LAP_VW(5) LAP_VW(6) LAP_VW(7)
+    LAP_VW(8) LAP_VW(9) LAP_VW(10) LAP_VW(11) LAP_VW(12) LAP_VW(13) LAP_VW(14) LAP_VW(15)
+    LAP_VW(16) LAP_VW(17) LAP_VW(18) LAP_VW(19) LAP_VW(20) LAP_VW(21) LAP_VW(22) LAP_VW(23)
+#undef LAP_VW
+    default: vmw4<0>(a, b, c, d);
+  }
+}
+
 __device__ __forceinline__ uint4 as_uint4(const u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
 
-template <int THREADS, int TOK, int PREF>
+// Entries k0 .. k0+7 of one (m, k-block) for the four heads of a KV group,
+// from the reference layout (one u32x4 of 8 fp16 per head), as the four
+// uint4 of the [M][K][4] table: entry k = (h0, h1 | h2, h3) in 8 bytes.
+__device__ __forceinline__ void interleave_heads(const u32x4& h0, const u32x4& h1,
+                                                 const u32x4& h2, const u32x4& h3,
+                                                 uint4* __restrict__ dst) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t a = h0[q], b = h1[q], c = h2[q], d = h3[q];
+    // even entry: low halves; odd entry: high halves
+    dst[q] = make_uint4(__builtin_amdgcn_perm(b, a, 0x05040100u),
+                        __builtin_amdgcn_perm(d, c, 0x05040100u),
+                        __builtin_amdgcn_perm(b, a, 0x07060302u),
+                        __builtin_amdgcn_perm(d, c, 0x07060302u));
+  }
+}
+
+template <int THREADS, int TOK, int PREF, bool IL>
 __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
     const uint16_t* __restrict__ lut, const uint8_t* __restrict__ codes, int64_t cs_b,
     int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, ScoreOut so, _Float16 one) {
   constexpr int kFill = kLutBytes / 16 / THREADS;  // table uint4s per thread
   constexpr int kAhead = PREF < TOK ? PREF : TOK;  // stages requested up front
-  static_assert(kFill * THREADS * 16 == kLutBytes && THREADS >= 256, "bad THREADS");
+  static_assert(kFill * THREADS * 16 == kLutBytes && THREADS >= 256 && kFill % 4 == 0,
+                "bad THREADS");
   static_assert(kFill + 2 * kAhead <= 23 && 2 * kAhead <= 16, "vmcnt range");
   __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
   __shared__ uint32_t s_hist[kG][256];
@@ -294,9 +232,22 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
   }
 
   const uint4* src = reinterpret_cast<const uint4*>(lut + (int64_t)r * (kG * kM * kK));
+  // The table: the interleaved layout is copied as is; the reference layout
+  // [4][M][K] is read as 8 consecutive entries of each head per group of
+  // four loads and interleaved in registers.
   u32x4 f[kFill];
+  if constexpr (IL) {
 #pragma unroll
-  for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * THREADS + tid);
+    for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * THREADS + tid);
+  } else {
+    const uint16_t* hsrc = lut + (int64_t)r * (kG * kM * kK);
+#pragma unroll
+    for (int j = 0; j < kFill / 4; ++j) {
+      const int e0 = (j * THREADS + tid) * 8;
+#pragma unroll
+      for (int g = 0; g < kG; ++g) f[4 * j + g] = gload16_ordered(hsrc + g * (kM * kK) + e0);
+    }
+  }
 
   // Rows past the chunk end load the chunk's last row (always in bounds) and
   // are discarded after scoring.
@@ -311,10 +262,19 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
 #pragma unroll
   for (int j = 0; j < kAhead; ++j) request(j);
 
+  if constexpr (IL) {
 #pragma unroll
-  for (int i = 0; i < kFill; ++i) {
-    vm_wait(kFill - 1 - i + 2 * kAhead, f[i]);
-    s_lut[i * THREADS + tid] = as_uint4(f[i]);
+    for (int i = 0; i < kFill; ++i) {
+      vm_wait(kFill - 1 - i + 2 * kAhead, f[i]);
+      s_lut[i * THREADS + tid] = as_uint4(f[i]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kFill / 4; ++j) {
+      vm_wait(kFill - 4 - 4 * j + 2 * kAhead, f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
+      interleave_heads(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3],
+                       &s_lut[(j * THREADS + tid) * 4]);
+    }
   }
   for (int i = tid; i < key_rows(so) * 256; i += THREADS) s_hist[i >> 8][i & 255] = 0;
   lds_barrier();
@@ -485,10 +445,9 @@ inline _Float16 f16_one() { return (_Float16)1.0f; }
 
 }  // namespace
 
-// Launch plan of the fast G=4 scorer.  kind 0: score_g4_kernel (any table
-// layout); kind 1: the pipelined score_g4p_kernel<threads, tok> (GMKG table).
+// Launch plan of the fast G=4 scorer, score_g4p_kernel<threads, tok, pref>.
 struct G4Plan {
-  int kind, threads, tok, pref, chunk_tokens, nchunk;
+  int threads, tok, pref, chunk_tokens, nchunk;
 };
 
 // Launch shapes of score_g4p_kernel, largest chunk first: {threads, tokens
@@ -496,15 +455,11 @@ struct G4Plan {
 static const int kG4Shapes[][3] = {{1024, 4, 1}, {512, 4, 1}, {512, 2, 1}, {256, 2, 1},
                                    {256, 1, 1}};
 
-// LAPRUNE_SCORE_CFG overrides the choice for measurements: "legacy" or one
-// of the shapes above as "<threads>x<tok>p<pref>".
-static bool score_cfg_override(int* threads, int* tok, int* pref, bool* legacy) {
+// LAPRUNE_SCORE_CFG overrides the choice for measurements: one of the
+// shapes above as "<threads>x<tok>p<pref>".
+static bool score_cfg_override(int* threads, int* tok, int* pref) {
   static const char* e = getenv("LAPRUNE_SCORE_CFG");
   if (!e || !*e) return false;
-  if (strcmp(e, "legacy") == 0) {
-    *legacy = true;
-    return true;
-  }
   int th = 0, tk = 0, pf = 0;
   if (sscanf(e, "%dx%dp%d", &th, &tk, &pf) != 3) return false;
   bool known = false;
@@ -513,29 +468,15 @@ static bool score_cfg_override(int* threads, int* tok, int* pref, bool* legacy) 
   *threads = th;
   *tok = tk;
   *pref = pf;
-  *legacy = false;
   return true;
 }
 
-static int g4_plan(int R, int T, bool lut_il, G4Plan* p) {
+static int g4_plan(int R, int T, G4Plan* p) {
   DevInfo di;
   int s = device_info(&di);
   if (s != LAP_OK) return s;
   int th = 0, tk = 0, pf = 1;
-  bool legacy = !lut_il;
-  const bool forced = score_cfg_override(&th, &tk, &pf, &legacy);
-  if (legacy || !lut_il) {
-    constexpr int THREADS = 512;
-    const int target_wgs = di.cu_count * score_wg_per_cu();
-    int nchunk = (target_wgs + R - 1) / R;
-    // Tokens per workgroup rounded up to whole passes of the token loop.
-    int chunk_tokens = (T + nchunk - 1) / nchunk;
-    chunk_tokens = (chunk_tokens + 2 * THREADS - 1) / (2 * THREADS) * (2 * THREADS);
-    if (chunk_tokens < 2 * THREADS) chunk_tokens = 2 * THREADS;
-    nchunk = (T + chunk_tokens - 1) / chunk_tokens;
-    *p = G4Plan{0, THREADS, 0, 0, chunk_tokens, nchunk < 1 ? 1 : nchunk};
-    return LAP_OK;
-  }
+  const bool forced = score_cfg_override(&th, &tk, &pf);
   if (!forced) {
     // Largest chunk that still gives every CU a workgroup; the smallest
     // shape when even that cannot.
@@ -553,16 +494,20 @@ static int g4_plan(int R, int T, bool lut_il, G4Plan* p) {
     }
   }
   const int ct = th * tk;
-  *p = G4Plan{1, th, tk, pf, ct, (T + ct - 1) / ct};
+  *p = G4Plan{th, tk, pf, ct, (T + ct - 1) / ct};
   return LAP_OK;
 }
 
 template <int TH, int TK, int PF>
-static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, const uint8_t* codes,
-                       int64_t cs_b, int64_t cs_h, int64_t cs_t, int Hkv, int R, int T,
-                       const ScoreOut& so) {
-  hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF>), grid, dim3(TH), 0, st, lut, codes, cs_b,
-                     cs_h, cs_t, Hkv, R, T, so, f16_one());
+static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, bool lut_il,
+                       const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t, int Hkv,
+                       int R, int T, const ScoreOut& so) {
+  if (lut_il)
+    hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, true>), grid, dim3(TH), 0, st, lut, codes,
+                       cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one());
+  else
+    hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, false>), grid, dim3(TH), 0, st, lut, codes,
+                       cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one());
 }
 
 // Launch the fast G=4 scorer.  Exposed to the fused retrieval entry point.
@@ -573,23 +518,16 @@ int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int6
                     hipStream_t st) {
   const int R = B * Hkv;
   G4Plan pl;
-  int s = g4_plan(R, T, lut_il, &pl);
+  int s = g4_plan(R, T, &pl);
   if (s != LAP_OK) return s;
   ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end, plans, per_head ? 1 : 0};
   dim3 grid((unsigned)(R * pl.nchunk));
-  if (pl.kind == 0) {
-    if (lut_il)
-      hipLaunchKernelGGL((score_g4_kernel<512, true>), grid, dim3(512), 0, st, lut, codes, cs_b,
-                         cs_h, cs_t, Hkv, R, T, pl.chunk_tokens, so, f16_one());
-    else
-      hipLaunchKernelGGL((score_g4_kernel<512, false>), grid, dim3(512), 0, st, lut, codes, cs_b,
-                         cs_h, cs_t, Hkv, R, T, pl.chunk_tokens, so, f16_one());
-  } else {
+  {
     const int key = (pl.threads * 16 + pl.tok) * 16 + pl.pref;
     switch (key) {
 #define LAP_G4P(TH, TK, PF)                                                               \
   case (TH * 16 + TK) * 16 + PF:                                                          \
-    launch_g4p<TH, TK, PF>(grid, st, lut, codes, cs_b, cs_h, cs_t, Hkv, R, T, so);        \
+    launch_g4p<TH, TK, PF>(grid, st, lut, lut_il, codes, cs_b, cs_h, cs_t, Hkv, R, T, so); \
     break;
       LAP_G4P(1024, 4, 1) LAP_G4P(512, 4, 1) LAP_G4P(512, 2, 1) LAP_G4P(256, 2, 1)
       LAP_G4P(256, 1, 1)
@@ -600,7 +538,7 @@ int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int6
         return LAP_ERR_INVALID;
     }
   }
-  LAP_LAUNCH_CHECK("score_g4_kernel");
+  LAP_LAUNCH_CHECK("score_g4p_kernel");
   if (nchunk_out) *nchunk_out = pl.nchunk;
   return LAP_OK;
 }
@@ -609,7 +547,7 @@ int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int6
 // tokens and R rows (the level-1 histogram count of the fused top-k).
 int score_g4_nchunk(int R, int T) {
   G4Plan pl;
-  if (g4_plan(R, T, true, &pl) != LAP_OK) return -1;
+  if (g4_plan(R, T, &pl) != LAP_OK) return -1;
   return pl.nchunk;
 }
 
