@@ -54,7 +54,11 @@ def aq_lut_build(q: torch.Tensor, codebooks: torch.Tensor, G: int = 1,
     M, K, Dc = codebooks.shape
     _check(D == Dc, "q and codebooks last dim must match")
     _check(q.stride(1) == 1, "q rows must be contiguous")
+    if q.data_ptr() % 16 or q.stride(0) % 4:  # the kernels read q four elements at a time
+        q = q.clone(memory_format=torch.contiguous_format)
     cb = codebooks.contiguous()
+    if cb.data_ptr() % 16:
+        cb = cb.clone()
     lay = N.LUT_HMK if layout == "hmk" else N.LUT_GMKG
     if lay == N.LUT_HMK:
         out = torch.empty((Hq, M, K), dtype=torch.float16, device=q.device)

@@ -475,7 +475,8 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
 }
 
 int check_common(const void* q, const void* keys, const void* vals, void* out, int dtype, int B,
-                 int Hq, int Hkv, int T, int D, int64_t q_sh, int64_t k_st, int64_t v_st) {
+                 int Hq, int Hkv, int T, int D, int64_t q_sh, int64_t k_sb, int64_t k_sh,
+                 int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st) {
   LAP_CHECK(q && keys && vals && out, "attention decode: null pointer");
   LAP_CHECK(dtype == LAP_DTYPE_F16 || dtype == LAP_DTYPE_BF16,
             "attention decode supports fp16/bf16");
@@ -487,7 +488,9 @@ int check_common(const void* q, const void* keys, const void* vals, void* out, i
   LAP_CHECK_CODE(D == 64 || D == 128 || D == 256, LAP_ERR_UNSUPPORTED,
                  "attention decode: head dim %d unsupported (64/128/256)", D);
   LAP_CHECK(q_sh >= D && k_st >= D && v_st >= D, "attention decode: strides smaller than D");
-  LAP_CHECK(k_st % 8 == 0 && v_st % 8 == 0 && (reinterpret_cast<uintptr_t>(keys) & 15) == 0 &&
+  // every K/V row is read as 16-byte vectors: base and all three strides
+  LAP_CHECK(k_st % 8 == 0 && v_st % 8 == 0 && k_sh % 8 == 0 && v_sh % 8 == 0 &&
+                k_sb % 8 == 0 && v_sb % 8 == 0 && (reinterpret_cast<uintptr_t>(keys) & 15) == 0 &&
                 (reinterpret_cast<uintptr_t>(vals) & 15) == 0,
             "attention decode: K/V rows must be 16-byte aligned");
   return LAP_OK;
@@ -519,7 +522,8 @@ extern "C" int lap_sparse_attn_decode(const void* q, int64_t q_sb, int64_t q_sh,
                                       float scale, void* out, void* workspace,
                                       size_t workspace_bytes, lap_stream_t stream) {
   clear_error();
-  int s = check_common(q, keys, vals, out, dtype, B, Hq, Hkv, T, D, q_sh, k_st, v_st);
+  int s = check_common(q, keys, vals, out, dtype, B, Hq, Hkv, T, D, q_sh, k_sb, k_sh, k_st, v_sb,
+                       v_sh, v_st);
   if (s != LAP_OK) return s;
   LAP_CHECK(H_idx == Hq || H_idx == Hkv, "sparse decode: H_idx must be Hq or Hkv");
   LAP_CHECK(n_idx >= 0 && sink_count >= 0 && tail_count >= 0, "sparse decode: negative count");
@@ -551,7 +555,8 @@ extern "C" int lap_sparse_attn_decode_ragged(
     const lap_row_plan* plans, int max_sink, int max_tail, float scale, void* out,
     void* workspace, size_t workspace_bytes, lap_stream_t stream) {
   clear_error();
-  int s = check_common(q, keys, vals, out, dtype, B, Hq, Hkv, T, D, q_sh, k_st, v_st);
+  int s = check_common(q, keys, vals, out, dtype, B, Hq, Hkv, T, D, q_sh, k_sb, k_sh, k_st, v_sb,
+                       v_sh, v_st);
   if (s != LAP_OK) return s;
   LAP_CHECK(plans, "ragged decode: null plans");
   LAP_CHECK(H_idx == Hq || H_idx == Hkv, "ragged decode: H_idx must be Hq or Hkv");
@@ -587,7 +592,8 @@ extern "C" int lap_dense_attn_decode(const void* q, int64_t q_sb, int64_t q_sh, 
                                      void* out, void* workspace, size_t workspace_bytes,
                                      lap_stream_t stream) {
   clear_error();
-  int s = check_common(q, keys, vals, out, dtype, B, Hq, Hkv, T, D, q_sh, k_st, v_st);
+  int s = check_common(q, keys, vals, out, dtype, B, Hq, Hkv, T, D, q_sh, k_sb, k_sh, k_st, v_sb,
+                       v_sh, v_st);
   if (s != LAP_OK) return s;
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);

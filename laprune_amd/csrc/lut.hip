@@ -567,6 +567,14 @@ extern "C" int lap_lut_build(const void* q, int q_dtype, int64_t q_row_stride,
   LAP_CHECK(D % 4 == 0, "lap_lut_build: D must be a multiple of 4 (got %d)", D);
   LAP_CHECK_CODE(D <= 256, LAP_ERR_UNSUPPORTED, "lap_lut_build: D=%d > 256 unsupported", D);
   LAP_CHECK(q_row_stride >= D, "lap_lut_build: q row stride %lld < D", (long long)q_row_stride);
+  // q and codebook rows are read four elements at a time (8 or 16 bytes)
+  const uintptr_t q_align = q_dtype == LAP_DTYPE_F32 ? 16 : 8;
+  const uintptr_t cb_align = cb_dtype == LAP_DTYPE_F32 ? 16 : 8;
+  LAP_CHECK(reinterpret_cast<uintptr_t>(q) % q_align == 0 && q_row_stride % 4 == 0,
+            "lap_lut_build: q must be %d-byte aligned with a row stride that is a multiple of 4",
+            (int)q_align);
+  LAP_CHECK(reinterpret_cast<uintptr_t>(codebooks) % cb_align == 0,
+            "lap_lut_build: codebooks must be %d-byte aligned", (int)cb_align);
   LAP_CHECK(layout == LAP_LUT_HMK || layout == LAP_LUT_GMKG, "lap_lut_build: bad layout");
   if (layout == LAP_LUT_GMKG)
     LAP_CHECK(G > 0 && Hq % G == 0, "lap_lut_build: Hq=%d not divisible by G=%d", Hq, G);

@@ -49,6 +49,13 @@ def test_invalid_arguments_return_status_and_message(lib):
     from laprune_amd import _native as N
     st = lib.lap_lut_build(None, N.BF16, 128, None, N.F32, 32, 128, 32, 256, 4, N.LUT_GMKG, None, None)
     assert st == N.LAP_ERR_INVALID and "null pointer" in _err(lib)
+    al, odd = C.c_void_p(4096), C.c_void_p(4098)  # never dereferenced
+    st = lib.lap_lut_build(odd, N.BF16, 128, al, N.F32, 32, 128, 32, 256, 4, N.LUT_GMKG, al, None)
+    assert st == N.LAP_ERR_INVALID and "aligned" in _err(lib)
+    st = lib.lap_lut_build(al, N.BF16, 130, al, N.F32, 32, 128, 32, 256, 4, N.LUT_GMKG, al, None)
+    assert st == N.LAP_ERR_INVALID and "multiple of 4" in _err(lib)
+    st = lib.lap_lut_build(al, N.F32, 128, odd, N.F32, 32, 128, 32, 256, 4, N.LUT_GMKG, al, None)
+    assert st == N.LAP_ERR_INVALID and "codebooks must be" in _err(lib)
     one = C.c_void_p(16)  # never dereferenced: validation fails first
     st = lib.lap_lut_score_grouped(one, N.LUT_HMK, one, 0, 32, 8, 5, 100, 32, 256, one, None)
     assert st == N.LAP_ERR_INVALID and "G<=4" in _err(lib)
