@@ -435,6 +435,8 @@ def aq_encode_greedy(x: torch.Tensor, codebooks: torch.Tensor,
     N.require_cuda(x, codebooks)
     _check(x.dim() == 2 and codebooks.dim() == 3, "expected x [N, d] and codebooks [M, K, d]")
     cb = codebooks.to(torch.float32).contiguous()
+    if cb.data_ptr() % 16:  # rows are read as 16-byte vectors
+        cb = cb.clone()
     M, K, D = cb.shape
     _check(x.shape[1] == D, "x and codebooks last dim must match")
     _check(K <= 256, "K must be <= 256 for uint8 codes")

@@ -930,6 +930,9 @@ static int run_encode(const RowMap& rm, int N, int D, const float* codebooks, in
   LAP_CHECK_CODE(prep_bytes >= p.bytes, LAP_ERR_WORKSPACE, "%s: prep buffer of %zu bytes needed",
                  who, p.bytes);
   LAP_CHECK((reinterpret_cast<uintptr_t>(p.ct) & 15) == 0, "%s: prep misaligned", who);
+  // exact rechecks read codebook rows as 16-byte vectors
+  LAP_CHECK((reinterpret_cast<uintptr_t>(codebooks) & 15) == 0,
+            "%s: codebooks must be 16-byte aligned", who);
   if (N == 0) return LAP_OK;
   hipStream_t st = as_stream(stream);
   if (K % 16 == 0 && encode_impl_mfma() && encode_use_tile(N, D, K)) {
