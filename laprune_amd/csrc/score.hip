@@ -207,10 +207,14 @@ __device__ __forceinline__ void interleave_heads(const u32x4& h0, const u32x4& h
   }
 }
 
-template <int THREADS, int TOK, int PREF, bool IL>
+// PH: per-head selection keys (a template parameter, so the two key modes
+// are separate kernels in traces and the key code folds).
+template <int THREADS, int TOK, int PREF, bool IL, bool PH>
 __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
     const uint16_t* __restrict__ lut, const uint8_t* __restrict__ codes, int64_t cs_b,
-    int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, ScoreOut so, _Float16 one) {
+    int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, ScoreOut so_arg, _Float16 one) {
+  ScoreOut so = so_arg;
+  so.per_head = PH;
   constexpr int kFill = kLutBytes / 16 / THREADS;  // table uint4s per thread
   constexpr int kAhead = PREF < TOK ? PREF : TOK;  // stages requested up front
   static_assert(kFill * THREADS * 16 == kLutBytes && THREADS >= 256 && kFill % 4 == 0,
@@ -502,12 +506,17 @@ template <int TH, int TK, int PF>
 static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, bool lut_il,
                        const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t, int Hkv,
                        int R, int T, const ScoreOut& so) {
-  if (lut_il)
-    hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, true>), grid, dim3(TH), 0, st, lut, codes,
-                       cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one());
-  else
-    hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, false>), grid, dim3(TH), 0, st, lut, codes,
-                       cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one());
+#define LAP_G4P_LAUNCH(IL, PH)                                                             \
+  hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, IL, PH>), grid, dim3(TH), 0, st, lut, codes, \
+                     cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one())
+  if (lut_il) {
+    if (so.per_head) LAP_G4P_LAUNCH(true, true);
+    else LAP_G4P_LAUNCH(true, false);
+  } else {
+    if (so.per_head) LAP_G4P_LAUNCH(false, true);
+    else LAP_G4P_LAUNCH(false, false);
+  }
+#undef LAP_G4P_LAUNCH
 }
 
 // Launch the fast G=4 scorer.  Exposed to the fused retrieval entry point.
