@@ -56,3 +56,11 @@ def test_gpu_reproduces_golden(dev, gold):
     assert np.array_equal(ig.cpu().numpy(), gold["idx_group"])
     assert np.array_equal(ec.cpu().numpy(), gold["enc_codes"])
     assert np.array_equal(er.cpu().numpy().view(np.uint32), gold["enc_rnorm"].view(np.uint32))
+    # the fused retrieve from the interleaved table: per head and per group
+    lut_il = K.aq_lut_build(q, cb, G=4, layout="gmkg")
+    c4 = codes.unsqueeze(0)
+    fh = K.aq_retrieve_topk(lut_il, c4, k, cs, ce, per_head=True)
+    fg = K.aq_retrieve_topk(lut_il, c4, 64, cs, ce, key_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert np.array_equal(fh[0].cpu().numpy().astype(np.int64), gold["idx_head"])
+    assert np.array_equal(fg[0].cpu().numpy().astype(np.int64), gold["idx_group"])
