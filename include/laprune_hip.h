@@ -384,6 +384,26 @@ int lap_encode_keys_ranges(const void* keys, int key_dtype,
                            uint8_t* codes, int64_t c_sb, int64_t c_sh, int64_t c_st,
                            lap_stream_t stream);
 
+/* Decode-step rotary embedding and cache append, one token per sequence:
+ * HF apply_rotary_pos_emb (rotate_half convention) as aq_evaluation.py:296-305
+ * applies it to the step's q and k, and the cache write of _kv_cache_append
+ * (aq_evaluation.py:65-112), in one launch.  Arithmetic as torch's in the
+ * model dtype: rnd(rnd(x * cos) + rnd(rotate_half(x) * sin)), bit-identical.
+ *   q   [B][Hq][D]  strides (q_sb, q_sh, 1);  k, v [B][Hkv][D] likewise
+ *   cos, sin [B][D] stride cs_sb, same dtype (fp16/bf16)
+ *   pos int64 [B] device positions; cache rows at pos >= t_cap (or < 0) are
+ *       not written
+ * Writes rope(q) to q_out [B][Hq][D] (contiguous), rope(k) to
+ * cache_k[b][h][pos[b]] and v to cache_v[b][h][pos[b]]. */
+int lap_rope_append(const void* q, int64_t q_sb, int64_t q_sh,
+                    const void* k, int64_t k_sb, int64_t k_sh,
+                    const void* v, int64_t v_sb, int64_t v_sh,
+                    const void* cos, const void* sin, int64_t cs_sb, int dtype,
+                    int B, int Hq, int Hkv, int D, const int64_t* pos,
+                    void* cache_k, int64_t ck_sb, int64_t ck_sh, int64_t ck_st,
+                    void* cache_v, int64_t cv_sb, int64_t cv_sh, int64_t cv_st,
+                    int t_cap, void* q_out, lap_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,8 @@ SIGNATURES = {
     "lap_retrieve_score": [vp, vp, i64, i64, i64, i32, i32, i32, i32, i32, i32, vp, vp, sz, vp],
     "lap_retrieve_select": [i32, i32, i32, i32, i32, i32, vp, i32, vp, sz, vp],
     "lap_retrieve_select_heads": [i32, i32, i32, i32, i32, i32, vp, i32, vp, sz, vp],
+    "lap_rope_append": [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, vp, i64, i32, i32, i32,
+                        i32, i32, vp, vp, i64, i64, i64, vp, i64, i64, i64, i32, vp, vp],
     "lap_retrieve_topk_ragged": [vp, vp, i64, i64, i64, i32, i32, i32, vp, i32, i32, vp, vp, i32,
                                  vp, sz, vp],
     "lap_topk_select_ragged": [vp, i64, i32, i32, i32, i32, vp, i32, i32, vp, i32, vp, sz, vp],

@@ -242,6 +242,39 @@ class DecodeKVCache:
         self.k[bidx, :, pos] = k_new.to(self.dtype).permute(0, 2, 1, 3)
         self.v[bidx, :, pos] = v_new.to(self.dtype).permute(0, 2, 1, 3)
 
+    def rope_append(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor, pos: torch.Tensor, q_out: torch.Tensor) -> torch.Tensor:
+        """Rotate one decode token per sequence and append it, in one launch.
+
+        q [B, 1, Hq*D], k and v [B, 1, Hkv*D] (projection outputs, heads
+        contiguous), cos/sin [B, 1, D] (the model's rotary tables in its
+        dtype), pos [B, 1] int64 device positions.  rope(k) and v go to the
+        capacity buffers at pos; rope(q) to q_out [B, Hq, D], returned as
+        [B, Hq, 1, D].  Bit-identical to apply_rotary_pos_emb + append_at."""
+        D, B = self.D, self.B
+        Hq = q.shape[-1] // D
+        if any(t.stride(-1) != 1 for t in (q, k, v, cos, sin)):
+            raise RuntimeError("rope_append: rows must be contiguous")
+        if any(t.dtype != self.dtype for t in (q, k, v, cos, sin)):
+            raise RuntimeError("rope_append: q, k, v, cos and sin must be in the cache dtype")
+        if sin.stride(0) != cos.stride(0) or cos.shape[-1] != D or sin.shape[-1] != D:
+            raise RuntimeError("rope_append: cos and sin must be [B, 1, D] with equal strides")
+        if (q.shape[0] != B or k.shape[0] != B or v.shape[0] != B or cos.shape[0] != B
+                or k.shape[-1] != self.Hkv * D or v.shape[-1] != self.Hkv * D
+                or q.shape[-1] % D != 0):
+            raise RuntimeError("rope_append: q [B,1,Hq*D], k/v [B,1,Hkv*D] expected")
+        if pos.dtype != torch.int64 or pos.numel() != B:
+            raise RuntimeError("rope_append: pos must be int64 with one position per sequence")
+        if q_out.shape != (B, Hq, D) or not q_out.is_contiguous() or q_out.dtype != self.dtype:
+            raise RuntimeError("rope_append: q_out must be a contiguous [B, Hq, D] tensor")
+        N.call("lap_rope_append", N.ptr(q), q.stride(0), D, N.ptr(k), k.stride(0), D, N.ptr(v),
+               v.stride(0), D, N.ptr(cos), N.ptr(sin), cos.stride(0), N.dtype_code(self.dtype),
+               B, Hq, self.Hkv, D, N.ptr(pos), N.ptr(self.k), self.k.stride(0),
+               self.k.stride(1), self.k.stride(2), N.ptr(self.v), self.v.stride(0),
+               self.v.stride(1), self.v.stride(2), self.capacity, N.ptr(q_out),
+               N.stream_of(q_out))
+        return q_out.unsqueeze(2)
+
     def encode_ranges(self, ranges: torch.Tensor) -> None:
         """Encode each sequence's device range ([B, 2] int32, at most
         group_size tokens; empty ranges cost a workgroup exit)."""

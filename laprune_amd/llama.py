@@ -112,12 +112,26 @@ class LAPruneLlama:
     def _attention(self, idx, attn, h, position_embeddings):
         B, T, _ = h.shape
         Hq, Hkv, D = self.Hq, self.Hkv, self.D
+        cos, sin = position_embeddings
+        st = self.states[idx]
+        if T == 1 and self._dev_mode:
+            # fixed launches, every per-step value in device memory; RoPE and
+            # the cache write are one kernel
+            q = st.cache.rope_append(attn.q_proj(h), attn.k_proj(h), attn.v_proj(h), cos, sin,
+                                     self._g_pos, self._q_rope)
+            if st.sparse is not None:
+                if self._g_flush:
+                    st.cache.encode_ranges(self._g_ranges)
+                o = st.sparse.step_dev(q, st.cache.codes, st.cache.k, st.cache.v,
+                                       self._g_plan_sparse)
+            else:
+                o = st.dense.step_dev(q, st.cache.k, st.cache.v, self._g_plan_dense)
+            o = o.transpose(1, 2).reshape(B, T, Hq * D)
+            return attn.o_proj(o), None
         q = attn.q_proj(h).view(B, T, Hq, D).transpose(1, 2)
         k = attn.k_proj(h).view(B, T, Hkv, D).transpose(1, 2)
         v = attn.v_proj(h).view(B, T, Hkv, D).transpose(1, 2)
-        cos, sin = position_embeddings
         q, k = self._rope(q, k, cos, sin)
-        st = self.states[idx]
         if T > 1:  # prefill: causal attention over the prompt, encode all its keys
             if self._row is None:
                 if any(n != 0 for n in st.cache.lengths):
@@ -132,14 +146,6 @@ class LAPruneLlama:
             with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                 o = F.scaled_dot_product_attention(q, kk, vv, is_causal=True,
                                                    scale=1.0 / math.sqrt(D))
-        elif self._dev_mode:  # fixed launches, every per-step value in device memory
-            st.cache.append_at(k, v, self._g_pos, self._g_bidx)
-            if st.sparse is not None:
-                st.cache.encode_ranges(self._g_ranges)
-                o = st.sparse.step_dev(q, st.cache.codes, st.cache.k, st.cache.v,
-                                       self._g_plan_sparse)
-            else:
-                o = st.dense.step_dev(q, st.cache.k, st.cache.v, self._g_plan_dense)
         else:
             if self._row is not None:
                 raise RuntimeError("single-token steps decode the whole batch")
@@ -208,7 +214,8 @@ class LAPruneLlama:
         self._g_ranges = flat[16 * B:18 * B].view(B, 2)
         self._g_pos32 = flat[18 * B:].view(B, 1)
         self._g_pos = torch.zeros((B, 1), dtype=torch.long, device=dev)
-        self._g_bidx = torch.arange(B, device=dev)[:, None]
+        self._q_rope = torch.empty((B, self.Hq, self.D), dtype=self.dtype, device=dev)
+        self._g_flush = False
         self._g_tok = torch.zeros((B, 1), dtype=torch.long, device=dev)
         self._g_next = torch.zeros((B, 1), dtype=torch.long, device=dev)
         self._g_logits = None
@@ -239,6 +246,9 @@ class LAPruneLlama:
             r = st.cache.advance_decode()
             if st.sparse is not None:
                 ranges = r
+        # steps on which no sequence fills its encode buffer replay the graph
+        # without the encode launches
+        self._g_flush = ranges is not None and any(hi > lo for lo, hi in ranges)
         c0 = next((st for st in self.states if st.sparse is not None), self.states[0])
         t_total = c0.cache.lengths
         rows = [0] * (19 * B)
@@ -280,8 +290,13 @@ class LAPruneLlama:
         if self._graph is not None and sig != self._graph_sig:
             self._graph = None  # a cache was reallocated (grown): capture again
         if self._graph is None:
-            # the first step runs eagerly (it also warms up every kernel), then
-            # the same body is captured for the following steps
+            self._graph = {}
+            self._graph_sig = sig
+        g = self._graph.get(self._g_flush)
+        if g is None:
+            # the first step of each variant (with or without encode flushes)
+            # runs eagerly (it also warms up every kernel), then the same body
+            # is captured for the following steps
             side = torch.cuda.Stream(self.dev)
             side.wait_stream(torch.cuda.current_stream(self.dev))
             with torch.cuda.stream(side):
@@ -290,10 +305,9 @@ class LAPruneLlama:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 self._graph_body()
-            self._graph = g
-            self._graph_sig = sig
+            self._graph[self._g_flush] = g
         else:
-            self._graph.replay()
+            g.replay()
         return self._g_logits
 
     def next_tokens(self) -> torch.Tensor:

@@ -587,3 +587,45 @@ def test_decode_step_over_cache(dev, K, orc):
         want = orc.attn_decode_f64(q[:, :, 0].double().numpy(), kk[:, :, :t + 1].double().numpy(),
                                    vv[:, :, :t + 1].double().numpy(), keep)
         assert _rel(out[:, :, 0].double().cpu().numpy(), want) < 1e-2
+
+
+# ------------------------------------------------- decode RoPE + cache append
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_rope_append_matches_hf(dev, dt):
+    """lap_rope_append against HF apply_rotary_pos_emb and an index write:
+    bit-identical rotated q, cache rows written at each sequence's position,
+    nothing else touched, and a position at the capacity bound skipped."""
+    from transformers.models.llama.modeling_llama import (LlamaRotaryEmbedding,
+                                                          apply_rotary_pos_emb)
+    from laprune_amd import _native as N
+    from laprune_amd.llama import llama31_8b_config
+    g = _gen(123)
+    B, Hq, Hkv, D, cap = 4, 32, 8, 128, 96
+    rot = LlamaRotaryEmbedding(llama31_8b_config(num_layers=1)).to(dev)
+    h = (torch.randn(B, 1, (Hq + 2 * Hkv) * D, generator=g) * 3).to(dt).to(dev)
+    q, k, v = h.split([Hq * D, Hkv * D, Hkv * D], dim=-1)   # strided views, like projections
+    pos = torch.tensor([[5], [95], [0], [96]], dtype=torch.long, device=dev)  # 96: past capacity
+    cos, sin = rot(h, torch.tensor([[5], [95], [0], [96]], device=dev))
+    cos, sin = cos.to(dt), sin.to(dt)
+    ck = torch.randn(B, Hkv, cap, D, generator=g).to(dt).to(dev)
+    cv = torch.randn(B, Hkv, cap, D, generator=g).to(dt).to(dev)
+    ck0, cv0 = ck.clone(), cv.clone()
+    q_out = torch.empty(B, Hq, D, dtype=dt, device=dev)
+    N.call("lap_rope_append", N.ptr(q), q.stride(0), D, N.ptr(k), k.stride(0), D, N.ptr(v),
+           v.stride(0), D, N.ptr(cos), N.ptr(sin), cos.stride(0), N.dtype_code(dt), B, Hq, Hkv,
+           D, N.ptr(pos), N.ptr(ck), ck.stride(0), ck.stride(1), ck.stride(2), N.ptr(cv),
+           cv.stride(0), cv.stride(1), cv.stride(2), cap, N.ptr(q_out), N.stream_of(q_out))
+    torch.cuda.synchronize()
+    qh = q.view(B, 1, Hq, D).transpose(1, 2)
+    kh = k.view(B, 1, Hkv, D).transpose(1, 2)
+    qr, kr = apply_rotary_pos_emb(qh, kh, cos, sin)
+    u16 = lambda t: t.contiguous().view(torch.int16).cpu()  # noqa: E731
+    assert torch.equal(u16(q_out), u16(qr[:, :, 0]))
+    want_k, want_v = ck0.clone(), cv0.clone()
+    for b, t in enumerate(pos[:, 0].tolist()):
+        if t < cap:
+            want_k[b, :, t] = kr[b, :, 0]
+            want_v[b, :, t] = v.view(B, Hkv, D)[b]
+    assert torch.equal(u16(ck), u16(want_k))
+    assert torch.equal(u16(cv), u16(want_v))
