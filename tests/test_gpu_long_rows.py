@@ -1,0 +1,144 @@
+"""SparseDecoder steps over rows longer than 32768 code columns, on the GPU.
+
+Such rows take the chunked radix levels (topk_level2_kernel +
+topk_select_kernel) instead of the one-workgroup row kernel.  The indices
+must be bit-exact against the oracle's top-k over the oracle's scores
+(aq_evaluation.py:198-201) and the attention within 1e-2 of float64 SDPA over
+the keep set (:210-251), for group and per-head selection, fp16 and bf16,
+both level shapes, ragged batches and graph replays.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SINK, LOCAL = 4, 64
+Hq, Hkv, D = 32, 8, 128
+
+
+def _rel(a, b):
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-6))
+
+
+def _inputs(seed, B, T, dt, zero_codes=False):
+    g = torch.Generator().manual_seed(seed)
+    cb = torch.randn(32, 256, D, generator=g) * 0.02
+    if zero_codes:  # every score equal: the first k candidates win
+        codes = torch.zeros(B, Hkv, T, 32, dtype=torch.uint8)
+    else:
+        codes = torch.randint(0, 256, (B, Hkv, T, 32), generator=g, dtype=torch.uint8)
+    kk = torch.randn(B, Hkv, T, D, generator=g).to(dt)
+    vv = torch.randn(B, Hkv, T, D, generator=g).to(dt)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(dt)
+    return cb, codes, kk, vv, q
+
+
+def _want_idx(orc, cb, codes_b, q_b, tc, plan, per_head, key_bf16):
+    """Oracle indices of one sequence: rows [Hkv] (group max) or [Hq]."""
+    lut = orc.lut_build(q_b.float().numpy(), cb.numpy())
+    s = orc.score_grouped(lut, codes_b[:, :tc].numpy(), 4)
+    return orc.topk(s, plan["k"], 1 if per_head else 4, plan["cand_start"], plan["cand_end"],
+                    key_bf16=key_bf16)
+
+
+def _check_attn(orc, out, q, kk, vv, sel_b, b, t_total, per_head):
+    G = Hq // Hkv
+
+    def keep(bb, h):
+        row = sel_b[h if per_head else h // G]
+        return orc.keep_list(row[row >= 0], t_total, SINK, LOCAL)
+
+    want = orc.attn_decode_f64(q[b:b + 1, :, 0].double().numpy(), kk[b:b + 1].double().numpy(),
+                               vv[b:b + 1].double().numpy(), keep)
+    got = out[b:b + 1, :, 0].double().cpu().numpy()
+    assert _rel(got, want) < 1e-2, b
+
+
+@pytest.mark.parametrize("select,dt,topk,zero", [
+    ("group", torch.bfloat16, 2048, False),
+    ("group", torch.float16, None, False),
+    ("head", torch.bfloat16, None, False),
+    ("group", torch.bfloat16, 2048, True),   # ties: the first 2048 candidates
+])
+def test_long_rows_uniform(dev, orc, select, dt, topk, zero):
+    from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
+    B, tc, tt = 1, 40000, 40030
+    T = tt + 16
+    cb, codes, kk, vv, q = _inputs(400 + len(select) + (topk or 0) % 7 + zero, B, T, dt, zero)
+    cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=topk, select=select,
+                          score_dtype=dt)
+    dec = SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg, dtype=dt)
+    cd, kd, vd, qd = codes.to(dev), kk.to(dev), vv.to(dev), q.to(dev)
+    out = dec.step(qd, cd[:, :, :tc], kd[:, :, :tt], vd[:, :, :tt]).clone()
+    sel = dec.selected().cpu().numpy()
+    p = dec.plan(tc, tt)
+    per_head = select == "head"
+    assert sel.shape == (B, Hq if per_head else Hkv, p["k"])
+    want = _want_idx(orc, cb, codes[0], q[0, :, 0], tc, p, per_head, dt == torch.bfloat16)
+    assert np.array_equal(sel[0].astype(np.int64), want)
+    _check_attn(orc, out, q, kk, vv, sel[0], 0, tt, per_head)
+
+
+@pytest.mark.parametrize("select", ["group", "head"])
+def test_long_rows_ragged(dev, orc, select):
+    """Ragged batch on the level path; head mode (3 sequences x 32 rows x 20
+    chunks) takes the 1024-thread level shape.  The second sequence has no
+    codes yet (no selection, sink and local rows only)."""
+    from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
+    t_total = [40100, 60, 36000]
+    t_codes = [40064, 0, 35968]
+    B, T = len(t_total), max(t_total) + 8
+    dt = torch.bfloat16
+    cb, codes, kk, vv, q = _inputs(420 + len(select), B, T, dt)
+    cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=None, select=select)
+    dec = SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg)
+    out = dec.step(q.to(dev), codes.to(dev), kk.to(dev), vv.to(dev), t_codes=t_codes,
+                   t_total=t_total).clone()
+    sel = dec.selected().cpu().numpy()
+    per_head = select == "head"
+    for b in range(B):
+        p = dec.plan(t_codes[b], t_total[b])
+        kb = p["k"] if t_codes[b] > 0 else 0
+        if kb:
+            want = _want_idx(orc, cb, codes[b], q[b, :, 0], t_codes[b], p, per_head, False)
+            assert np.array_equal(sel[b, :, :kb].astype(np.int64), want), b
+        assert np.all(sel[b, :, kb:] == -1), b
+        _check_attn(orc, out, q, kk, vv, sel[b], b, t_total[b], per_head)
+
+
+def test_long_rows_graph_replays(dev, orc):
+    """step_dev (device plans) captured in a graph: every replay equals the
+    eager step, with the plans rewritten between replays."""
+    from laprune_amd.retrieval import PLAN_FIELDS, RetrievalConfig, SparseDecoder
+    B, T = 2, 40064
+    dt = torch.bfloat16
+    cb, codes, kk, vv, q = _inputs(440, B, T, dt)
+    cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=2048, select="group")
+    dec = SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg)
+    cd, kd, vd, qd = codes.to(dev), kk.to(dev), vv.to(dev), q.to(dev)
+
+    def plans_for(tc, tt):
+        rows = [dec.row_plans([a], [b])[0] for a, b in zip(tc, tt)]
+        return torch.tensor([[r[f] for f in PLAN_FIELDS] for r in rows], dtype=torch.int32)
+
+    pdev = plans_for([40000, 36000], [40030, 36020]).to(dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dec.step_dev(qd, cd, kd, vd, pdev)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        dec.step_dev(qd, cd, kd, vd, pdev)
+    for tc, tt in [([40000, 36000], [40030, 36020]), ([38000, 40000], [38040, 40060]),
+                   ([40000, 36000], [40030, 36020])]:
+        pdev.copy_(plans_for(tc, tt))
+        gph.replay()
+        torch.cuda.synchronize()
+        got_out, got_sel = dec.out.clone(), dec.idx.clone()
+        dec.step_dev(qd, cd, kd, vd, pdev)
+        torch.cuda.synchronize()
+        assert torch.equal(got_sel, dec.idx)
+        assert torch.equal(got_out, dec.out)
