@@ -56,32 +56,48 @@ __device__ __forceinline__ RowCols row_cols(const ScoreOut& so, int b, int T) {
   return RowCols{min(max(p[0], 0), T), p[2], p[3]};
 }
 
+// Level-1 histograms in LDS: HC copies per selection row, at a pitch of 257
+// words so that the copies of one bin sit in different banks; lane l adds to
+// copy l % HC.  Keys of nearby scores share a few high bytes, and the LDS
+// serialises atomics that a wave aims at one address.
+constexpr int kHPitch = 257;
+template <int HC>
+using HistRows = uint32_t (*)[HC * kHPitch];
+
 // Copy the workgroup's level-1 histograms (one per selection row of KV row
-// r) to [row][nchunk][256]; with s_hist null, zeros (a chunk past the row's
-// columns).
-__device__ __forceinline__ void write_hists(const ScoreOut& so, uint32_t (*s_hist)[256],
-                                            int r, int R, int chunk, int tid, int threads) {
+// r, the sum of its copies) to [row][nchunk][256]; with s_hist null, zeros
+// (a chunk past the row's columns).
+template <int HC>
+__device__ __forceinline__ void write_hists(const ScoreOut& so, HistRows<HC> s_hist, int r,
+                                            int R, int chunk, int tid, int threads) {
   if (!so.hist) return;
   const int nchunk = gridDim.x / R, rows = key_rows(so);
   for (int i = tid; i < rows * 256; i += threads) {
     const int g = i >> 8, bin = i & 255;
-    so.hist[(((int64_t)r * rows + g) * nchunk + chunk) * 256 + bin] = s_hist ? s_hist[g][bin] : 0u;
+    uint32_t v = 0;
+    if (s_hist) {
+#pragma unroll
+      for (int c = 0; c < HC; ++c) v += s_hist[g][c * kHPitch + bin];
+    }
+    so.hist[(((int64_t)r * rows + g) * nchunk + chunk) * 256 + bin] = v;
   }
 }
 __device__ __forceinline__ void write_empty_hist(const ScoreOut& so, int r, int R, int chunk,
                                                  int tid, int threads) {
-  write_hists(so, nullptr, r, R, chunk, tid, threads);
+  write_hists<1>(so, nullptr, r, R, chunk, tid, threads);
 }
 
 // Selection keys of token t of KV row r and their level-1 histogram counts
 // (inside the candidate window): the group max of the four fp16 head scores
 // (fp16 rounding is monotone, so fp16(max) == max of the fp16 scores), or
 // with per_head each head's own key.
+template <int HC>
 __device__ __forceinline__ void emit_keys(const ScoreOut& so, const RowCols& rc, int r, int T,
                                           int t, float e0, float e1, float e2, float e3,
-                                          uint32_t (*s_hist)[256]) {
+                                          HistRows<HC> s_hist) {
   if (!so.keys && !so.hist) return;
   const bool counted = so.hist && t >= rc.cs && t < rc.ce;
+  const int copy = (int)(__lane_id() % HC) * kHPitch;
   auto key_of = [&](float e) {
     const uint16_t h = f2h(e);
     return so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(h) : f16_key(h);
@@ -92,12 +108,12 @@ __device__ __forceinline__ void emit_keys(const ScoreOut& so, const RowCols& rc,
     for (int g = 0; g < kG; ++g) {
       const uint32_t key = key_of(e[g]);
       if (so.keys) so.keys[((int64_t)r * kG + g) * T + t] = (uint16_t)key;
-      if (counted) atomicAdd(&s_hist[g][key >> 8], 1u);
+      if (counted) atomicAdd(&s_hist[g][copy + (key >> 8)], 1u);
     }
   } else {
     const uint32_t key = key_of(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
     if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
-    if (counted) atomicAdd(&s_hist[0][key >> 8], 1u);
+    if (counted) atomicAdd(&s_hist[0][copy + (key >> 8)], 1u);
   }
 }
 
@@ -221,7 +237,8 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
                 "bad THREADS");
   static_assert(kFill + 2 * kAhead <= 23 && 2 * kAhead <= 16, "vmcnt range");
   __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
-  __shared__ uint32_t s_hist[kG][256];
+  constexpr int HC = PH ? 2 : 4;  // histogram copies per selection row
+  __shared__ uint32_t s_hist[PH ? kG : 1][HC * kHPitch];
 
   const int r = blockIdx.x % R;
   const int chunk = blockIdx.x / R;
@@ -280,7 +297,8 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
                        &s_lut[(j * THREADS + tid) * 4]);
     }
   }
-  for (int i = tid; i < key_rows(so) * 256; i += THREADS) s_hist[i >> 8][i & 255] = 0;
+  for (int i = tid; i < key_rows(so) * HC * kHPitch; i += THREADS)
+    s_hist[i / (HC * kHPitch)][i % (HC * kHPitch)] = 0;
   lds_barrier();
 
   const char* lds = reinterpret_cast<const char*>(s_lut);
@@ -301,12 +319,12 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
       hp[2 * (int64_t)T] = f2h(e2);
       hp[3 * (int64_t)T] = f2h(e3);
     }
-    emit_keys(so, rc, r, T, t, e0, e1, e2, e3, s_hist);
+    emit_keys<HC>(so, rc, r, T, t, e0, e1, e2, e3, s_hist);
   }
 
   if (so.hist) {
     __syncthreads();
-    write_hists(so, s_hist, r, R, chunk, tid, THREADS);
+    write_hists<HC>(so, s_hist, r, R, chunk, tid, THREADS);
   }
 }
 
