@@ -366,10 +366,12 @@ Ws carve(void* base, int R, int64_t key_cols, int C1, int C2) {
 }
 
 // Level 2 and the compaction over chunks of candidates; n_max is the widest
-// row's window.  Each workgroup re-sums its row's chunk histograms, so when
-// 2048-key chunks would make more than 1024 workgroups (many long rows: one
-// top-k per query head at 128k), 8192-key chunks on 1024-thread workgroups
-// cut that repeated reading fourfold.
+// row's window.  Each workgroup re-sums its row's chunk histograms, so more
+// rows take longer chunks: 2048-key chunks on 256-thread workgroups while
+// they make fewer than 512 workgroups, then 4096-key chunks on 512 threads
+// (C2: 8 group rows or 32 per-head rows at 128k) up to 1024 workgroups, then
+// 8192-key chunks on 1024 threads.  LAPRUNE_LEVEL_TH=256|512|1024 forces a
+// shape.
 template <int TH>
 int run_levels_th(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int C1,
                   void* out, int out_dtype, int64_t out_stride, hipStream_t st) {
@@ -390,9 +392,18 @@ int run_levels_th(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, i
 
 int run_levels(const Ws& w, KeySrc ks, int R, const SelSpec& sp, int n_max, int C1,
                void* out, int out_dtype, int64_t out_stride, hipStream_t st) {
+  static const int forced = [] {
+    const char* e = getenv("LAPRUNE_LEVEL_TH");
+    return e ? atoi(e) : 0;
+  }();
   const int64_t small_wgs = (int64_t)R * ((n_max + kChunk - 1) / kChunk);
-  if (small_wgs > 1024)
+  const int64_t mid_wgs = (int64_t)R * ((n_max + 2 * kChunk - 1) / (2 * kChunk));
+  int th = small_wgs < 512 ? kThreads : mid_wgs <= 1024 ? 512 : 1024;
+  if (forced == 256 || forced == 512 || forced == 1024) th = forced;
+  if (th == 1024)
     return run_levels_th<1024>(w, ks, R, sp, n_max, C1, out, out_dtype, out_stride, st);
+  if (th == 512)
+    return run_levels_th<512>(w, ks, R, sp, n_max, C1, out, out_dtype, out_stride, st);
   return run_levels_th<kThreads>(w, ks, R, sp, n_max, C1, out, out_dtype, out_stride, st);
 }
 

@@ -55,17 +55,19 @@ def _check_attn(orc, out, q, kk, vv, sel_b, b, t_total, per_head):
     assert _rel(got, want) < 1e-2, b
 
 
-@pytest.mark.parametrize("select,dt,topk,zero", [
-    ("group", torch.bfloat16, 2048, False),
-    ("group", torch.float16, None, False),
-    ("head", torch.bfloat16, None, False),
-    ("group", torch.bfloat16, 2048, True),   # ties: the first 2048 candidates
+@pytest.mark.parametrize("select,dt,topk,zero,tc", [
+    ("group", torch.bfloat16, 2048, False, 40000),   # 256-thread levels
+    ("group", torch.float16, None, False, 40000),
+    ("head", torch.bfloat16, None, False, 40000),    # 512-thread levels
+    ("group", torch.bfloat16, 2048, True, 40000),    # ties: the first 2048 candidates
+    ("group", torch.bfloat16, 2048, False, 131072),  # C2's 512-thread levels
 ])
-def test_long_rows_uniform(dev, orc, select, dt, topk, zero):
+def test_long_rows_uniform(dev, orc, select, dt, topk, zero, tc):
     from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
-    B, tc, tt = 1, 40000, 40030
+    B, tt = 1, tc + 30
     T = tt + 16
-    cb, codes, kk, vv, q = _inputs(400 + len(select) + (topk or 0) % 7 + zero, B, T, dt, zero)
+    cb, codes, kk, vv, q = _inputs(400 + len(select) + (topk or 0) % 7 + zero + tc % 5, B, T, dt,
+                                   zero)
     cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=topk, select=select,
                           score_dtype=dt)
     dec = SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg, dtype=dt)
@@ -80,17 +82,20 @@ def test_long_rows_uniform(dev, orc, select, dt, topk, zero):
     _check_attn(orc, out, q, kk, vv, sel[0], 0, tt, per_head)
 
 
-@pytest.mark.parametrize("select", ["group", "head"])
-def test_long_rows_ragged(dev, orc, select):
-    """Ragged batch on the level path; head mode (3 sequences x 32 rows x 20
-    chunks) takes the 1024-thread level shape.  The second sequence has no
-    codes yet (no selection, sink and local rows only)."""
+@pytest.mark.parametrize("select,t_total,t_codes", [
+    ("group", [40100, 60, 36000], [40064, 0, 35968]),
+    ("head", [40100, 60, 36000], [40064, 0, 35968]),   # 96 rows: 512-thread levels
+    ("head", [40100, 60, 36000, 33000, 38000], [40064, 0, 35968, 32960, 37952]),  # 1024
+])
+def test_long_rows_ragged(dev, orc, select, t_total, t_codes):
+    """Ragged batches on the level path, with the level shape picked by the
+    row count (per-head rows: 96 x 10 four-kilokey chunks take 512 threads,
+    160 x 10 take 1024).  The second sequence has no codes yet (no
+    selection, sink and local rows only)."""
     from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
-    t_total = [40100, 60, 36000]
-    t_codes = [40064, 0, 35968]
     B, T = len(t_total), max(t_total) + 8
     dt = torch.bfloat16
-    cb, codes, kk, vv, q = _inputs(420 + len(select), B, T, dt)
+    cb, codes, kk, vv, q = _inputs(420 + len(select) + len(t_total), B, T, dt)
     cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=None, select=select)
     dec = SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg)
     out = dec.step(q.to(dev), codes.to(dev), kk.to(dev), vv.to(dev), t_codes=t_codes,
