@@ -400,8 +400,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 int choose_nsplit(int rows, int L) {
   DevInfo di;
   if (device_info(&di) != LAP_OK) return -1;
+  // Workgroups per CU the splits aim at: one (A/B at C2 and C5 against two
+  // and four: faster for the dense, group, per-head and ragged steps);
+  // LAPRUNE_ATTN_WPC overrides.
+  static const int wpc = [] {
+    const char* e = getenv("LAPRUNE_ATTN_WPC");
+    const int v = e ? atoi(e) : 0;
+    return v >= 1 && v <= 16 ? v : 1;
+  }();
   const int max_split = (L + kTile - 1) / kTile;
-  int ns = (di.cu_count * 2 + rows - 1) / rows;
+  int ns = (di.cu_count * wpc + rows - 1) / rows;
   if (ns > max_split) ns = max_split;
   if (ns > 1024) ns = 1024;
   return ns < 1 ? 1 : ns;
