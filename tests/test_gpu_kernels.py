@@ -429,6 +429,30 @@ def test_encode_bit_exact(dev, K, orc, N, D):
     assert np.array_equal(rn.cpu().numpy()[rows].view(np.uint32), want_r.view(np.uint32))
 
 
+def test_encode_c3_config(dev, K, orc):
+    """BASELINE config C3 exactly: 8 KV heads x 64 post-RoPE keys (pre-RoPE
+    bf16 N(0,1) x per-channel U(0.5, 4), rotate-half RoPE with theta 500000
+    at positions 131008..131071), 32 x 256 fp32 codebooks N(0, 0.02):
+    codes and residual norms bit-exact against the oracle."""
+    g = _gen(303)
+    Hkv, n_tok, D = 8, 64, 128
+    k = (torch.randn(Hkv, n_tok, D, generator=g) *
+         (torch.rand(D, generator=g) * 3.5 + 0.5)).bfloat16().float()
+    pos = torch.arange(131008, 131008 + n_tok, dtype=torch.float64)
+    inv = 500000.0 ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+    ang = pos[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).float()
+    sin = torch.cat([ang.sin(), ang.sin()], -1).float()
+    x = (k * cos + torch.cat([-k[..., D // 2:], k[..., :D // 2]], -1) * sin).reshape(-1, D)
+    cb = torch.randn(32, 256, D, generator=g) * 0.02
+    codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
+    torch.cuda.synchronize()
+    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
+    assert codes.shape == (Hkv * n_tok, 32)
+    assert np.array_equal(codes.cpu().numpy(), want_c)
+    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+
+
 @pytest.mark.parametrize("Kc,D", [(60, 64), (48, 128), (16, 64), (240, 128)])
 def test_encode_bit_exact_entry_counts(dev, K, orc, Kc, D):
     """K % 16 != 0 takes the all-VALU search, the rest the MFMA search with
