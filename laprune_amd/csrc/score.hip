@@ -225,7 +225,8 @@ __device__ __forceinline__ void interleave_heads(const u32x4& h0, const u32x4& h
 
 // PH: per-head selection keys (a template parameter, so the two key modes
 // are separate kernels in traces and the key code folds).
-template <int THREADS, int TOK, int PREF, bool IL, bool PH>
+// HC: level-1 histogram copies per selection row (see kHPitch).
+template <int THREADS, int TOK, int PREF, bool IL, bool PH, int HC>
 __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
     const uint16_t* __restrict__ lut, const uint8_t* __restrict__ codes, int64_t cs_b,
     int64_t cs_h, int64_t cs_t, int Hkv, int R, int T, ScoreOut so_arg, _Float16 one) {
@@ -237,7 +238,6 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
                 "bad THREADS");
   static_assert(kFill + 2 * kAhead <= 23 && 2 * kAhead <= 16, "vmcnt range");
   __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
-  constexpr int HC = PH ? 2 : 4;  // histogram copies per selection row
   __shared__ uint32_t s_hist[PH ? kG : 1][HC * kHPitch];
 
   const int r = blockIdx.x % R;
@@ -520,19 +520,23 @@ static int g4_plan(int R, int T, G4Plan* p) {
   return LAP_OK;
 }
 
+// Histogram copies: 4 per group row; per-head rows take 4 (82 KiB of LDS)
+// when the launch has at most one workgroup per CU, else 2 (72 KiB, two
+// workgroups per CU).
 template <int TH, int TK, int PF>
 static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, bool lut_il,
                        const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t, int Hkv,
-                       int R, int T, const ScoreOut& so) {
-#define LAP_G4P_LAUNCH(IL, PH)                                                             \
-  hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, IL, PH>), grid, dim3(TH), 0, st, lut, codes, \
-                     cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one())
+                       int R, int T, const ScoreOut& so, bool one_per_cu) {
+#define LAP_G4P_LAUNCH(IL, PH, HC)                                                          \
+  hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, IL, PH, HC>), grid, dim3(TH), 0, st, lut,  \
+                     codes, cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one())
   if (lut_il) {
-    if (so.per_head) LAP_G4P_LAUNCH(true, true);
-    else LAP_G4P_LAUNCH(true, false);
+    if (!so.per_head) LAP_G4P_LAUNCH(true, false, 4);
+    else if (one_per_cu) LAP_G4P_LAUNCH(true, true, 4);
+    else LAP_G4P_LAUNCH(true, true, 2);
   } else {
-    if (so.per_head) LAP_G4P_LAUNCH(false, true);
-    else LAP_G4P_LAUNCH(false, false);
+    if (so.per_head) LAP_G4P_LAUNCH(false, true, 2);
+    else LAP_G4P_LAUNCH(false, false, 4);
   }
 #undef LAP_G4P_LAUNCH
 }
@@ -549,12 +553,17 @@ int launch_score_g4(const uint16_t* lut, bool lut_il, const uint8_t* codes, int6
   if (s != LAP_OK) return s;
   ScoreOut so{heads, keys, hist, key_mode, cand_start, cand_end, plans, per_head ? 1 : 0};
   dim3 grid((unsigned)(R * pl.nchunk));
+  DevInfo di;
+  s = device_info(&di);
+  if (s != LAP_OK) return s;
+  const bool one_per_cu = (int64_t)grid.x <= di.cu_count;
   {
     const int key = (pl.threads * 16 + pl.tok) * 16 + pl.pref;
     switch (key) {
 #define LAP_G4P(TH, TK, PF)                                                               \
   case (TH * 16 + TK) * 16 + PF:                                                          \
-    launch_g4p<TH, TK, PF>(grid, st, lut, lut_il, codes, cs_b, cs_h, cs_t, Hkv, R, T, so); \
+    launch_g4p<TH, TK, PF>(grid, st, lut, lut_il, codes, cs_b, cs_h, cs_t, Hkv, R, T, so, \
+                           one_per_cu);                                                      \
     break;
       LAP_G4P(1024, 4, 1) LAP_G4P(512, 4, 1) LAP_G4P(512, 2, 1) LAP_G4P(256, 2, 1)
       LAP_G4P(256, 1, 1)
