@@ -96,6 +96,7 @@ class LAPruneLlama:
             dense = DenseDecoder(batch, self.Hq, self.Hkv, self.D, capacity, self.dev, self.dtype)
             self.states.append(_LayerState(cache, sparse, dense))
             attn = layer.self_attn
+            self._fuse_qkv(attn)
             attn.forward = self._make_forward(i, attn)
         self._row = None  # sequence being prefilled alone (ragged prefill)
         self._dev_mode = False
@@ -103,6 +104,38 @@ class LAPruneLlama:
         self._g = None
 
     # ------------------------------------------------------------ attention
+    @staticmethod
+    @torch.no_grad()
+    def _fuse_qkv(attn) -> None:
+        """One [q; k; v] weight per layer, so that a step projects with one
+        GEMV instead of three; the modules' own weights become views of it
+        (no second copy).  Layers whose biases are mixed keep three GEMVs."""
+        mods = (attn.q_proj, attn.k_proj, attn.v_proj)
+        has_b = [m.bias is not None for m in mods]
+        if any(has_b) and not all(has_b):
+            attn._lap_qkv = None
+            return
+        w = torch.cat([m.weight for m in mods], 0)
+        b = torch.cat([m.bias for m in mods], 0) if all(has_b) else None
+        sizes = [m.weight.shape[0] for m in mods]
+        o = 0
+        for m, n in zip(mods, sizes):
+            m.weight = torch.nn.Parameter(w[o:o + n], requires_grad=False)
+            if b is not None:
+                m.bias = torch.nn.Parameter(b[o:o + n], requires_grad=False)
+            o += n
+        attn._lap_qkv = (w, b, sizes)
+
+    @staticmethod
+    def _project(attn, h):
+        """q, k, v projections of h [B, T, hidden] as [B, T, n] (views of one
+        fused GEMV output when the layer's weights are fused)."""
+        f = getattr(attn, "_lap_qkv", None)
+        if f is None:
+            return attn.q_proj(h), attn.k_proj(h), attn.v_proj(h)
+        w, b, sizes = f
+        return F.linear(h, w, b).split(sizes, dim=-1)
+
     def _make_forward(self, idx: int, attn):
         def forward(hidden_states, position_embeddings=None, attention_mask=None,
                     past_key_values=None, **kwargs):
@@ -117,8 +150,8 @@ class LAPruneLlama:
         if T == 1 and self._dev_mode:
             # fixed launches, every per-step value in device memory; RoPE and
             # the cache write are one kernel
-            q = st.cache.rope_append(attn.q_proj(h), attn.k_proj(h), attn.v_proj(h), cos, sin,
-                                     self._g_pos, self._q_rope)
+            qp, kp, vp = self._project(attn, h)
+            q = st.cache.rope_append(qp, kp, vp, cos, sin, self._g_pos, self._q_rope)
             if st.sparse is not None:
                 if self._g_flush:
                     st.cache.encode_ranges(self._g_ranges)
@@ -128,9 +161,10 @@ class LAPruneLlama:
                 o = st.dense.step_dev(q, st.cache.k, st.cache.v, self._g_plan_dense)
             o = o.transpose(1, 2).reshape(B, T, Hq * D)
             return attn.o_proj(o), None
-        q = attn.q_proj(h).view(B, T, Hq, D).transpose(1, 2)
-        k = attn.k_proj(h).view(B, T, Hkv, D).transpose(1, 2)
-        v = attn.v_proj(h).view(B, T, Hkv, D).transpose(1, 2)
+        qp, kp, vp = self._project(attn, h)
+        q = qp.reshape(B, T, Hq, D).transpose(1, 2)
+        k = kp.reshape(B, T, Hkv, D).transpose(1, 2)
+        v = vp.reshape(B, T, Hkv, D).transpose(1, 2)
         q, k = self._rope(q, k, cos, sin)
         if T > 1:  # prefill: causal attention over the prompt, encode all its keys
             if self._row is None:
