@@ -127,10 +127,33 @@ class LAPruneLlama:
         attn._lap_qkv = (w, b, sizes)
 
     @staticmethod
-    def _project(attn, h):
+    def _fused_current(attn) -> bool:
+        """Whether the modules' weights (and biases) are still the views of
+        the fused tensors.  ``model.to(...)`` or ``load_state_dict(assign=True)``
+        replace the parameters; the fused copy is then stale."""
+        w, b, sizes = attn._lap_qkv
+        mods = (attn.q_proj, attn.k_proj, attn.v_proj)
+        off = 0
+        for m, n in zip(mods, sizes):
+            mw = m.weight
+            if (mw.dtype != w.dtype or mw.device != w.device or
+                    mw.data_ptr() != w.data_ptr() + off * w.stride(0) * w.element_size()):
+                return False
+            if b is not None and (m.bias is None or m.bias.dtype != b.dtype or
+                                  m.bias.data_ptr() != b.data_ptr() + off * b.element_size()):
+                return False
+            off += n
+        return True
+
+    @classmethod
+    def _project(cls, attn, h):
         """q, k, v projections of h [B, T, hidden] as [B, T, n] (views of one
-        fused GEMV output when the layer's weights are fused)."""
+        fused GEMV output when the layer's weights are fused).  A layer whose
+        parameters were replaced after wrapping is fused again first."""
         f = getattr(attn, "_lap_qkv", None)
+        if f is not None and not cls._fused_current(attn):
+            cls._fuse_qkv(attn)
+            f = attn._lap_qkv
         if f is None:
             return attn.q_proj(h), attn.k_proj(h), attn.v_proj(h)
         w, b, sizes = f
@@ -202,6 +225,18 @@ class LAPruneLlama:
     def lengths(self) -> list[int]:
         return list(self.states[0].cache.lengths)
 
+    def _check_room(self, new: int, rows=None) -> None:
+        """Raise before any layer runs when ``new`` more tokens for the given
+        sequences (all by default) would exceed ``capacity``, which sized
+        every layer's decoder and workspaces; nothing is appended then, so
+        the layers' caches stay consistent."""
+        lens = self.lengths
+        rows = range(self.B) if rows is None else rows
+        need = max(lens[b] for b in rows) + new
+        if need > self.capacity:
+            raise RuntimeError(f"{need} tokens exceed the capacity of {self.capacity} the "
+                               "model was wrapped with (wrap it with a larger capacity)")
+
     def _forward(self, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         out = self.model(input_ids=ids, position_ids=pos, use_cache=False, logits_to_keep=1)
         return out.logits[:, -1]
@@ -212,6 +247,9 @@ class LAPruneLlama:
         if input_ids.shape[0] != self.B:
             raise RuntimeError(f"expected {self.B} sequences, got {input_ids.shape[0]}")
         T = input_ids.shape[1]
+        if any(n != 0 for n in self.lengths):
+            raise RuntimeError("batched prefill needs empty caches (use reset())")
+        self._check_room(T)
         pos = torch.arange(T, device=self.dev)[None].expand(self.B, T)
         return self._forward(input_ids.to(self.dev), pos)
 
@@ -219,6 +257,9 @@ class LAPruneLlama:
     def prefill_row(self, b: int, input_ids: torch.Tensor) -> torch.Tensor:
         """Prefill sequence b alone ([1, T_b] prompt); returns its logits [1, V]."""
         T = input_ids.shape[-1]
+        if not 0 <= b < self.B:
+            raise RuntimeError(f"sequence {b} out of range for batch {self.B}")
+        self._check_room(T, rows=[b])
         self._row = b
         try:
             pos = torch.arange(T, device=self.dev)[None]
@@ -229,6 +270,7 @@ class LAPruneLlama:
     @torch.no_grad()
     def decode(self, tokens: torch.Tensor) -> torch.Tensor:
         """One decode step for all sequences: tokens [B, 1]; returns logits [B, V]."""
+        self._check_room(1)
         pos = torch.tensor(self.lengths, device=self.dev)[:, None]
         return self._forward(tokens.reshape(self.B, 1).to(self.dev), pos)
 
@@ -312,6 +354,7 @@ class LAPruneLlama:
         """One decode step for all sequences as one graph replay.  tokens
         [B, 1] (device or host); None feeds the previous step's greedy
         tokens.  Returns the logits [B, V] (a buffer the next step reuses)."""
+        self._check_room(1)
         if self._g is None:
             self._graph_buffers()
         if tokens is not None:

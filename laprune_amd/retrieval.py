@@ -88,6 +88,17 @@ def keep_segments(t_total: int, sink: int, local: int) -> tuple[int, int, int]:
     return sb_eff, start, tail_count
 
 
+def keep_plan(k: int, t_total: int, sink: int, local: int) -> tuple[int, int, int]:
+    """(sink_count, tail_start, tail_count) of a step that selects k
+    candidates.  As keep_segments, except that a step with no selected
+    candidate, no sink and no local window keeps the newest token instead of
+    nothing (aq_evaluation.py:233-234)."""
+    sb, start, tail = keep_segments(t_total, sink, local)
+    if k <= 0 and sb == 0 and tail == 0 and t_total > 0:
+        return 0, t_total - 1, 1
+    return sb, start, tail
+
+
 PLAN_FIELDS = ("t_codes", "t_total", "cand_start", "cand_end", "k", "sink", "tail_start",
                "tail_count")
 
@@ -174,7 +185,10 @@ class SparseDecoder:
         self.out = torch.empty((batch, num_q_heads, head_dim), dtype=dtype, device=self.dev)
         ws_r = N.size_query("lap_retrieve_workspace_size", batch * rows, max_tokens)
         self.ws_sel = torch.empty(max(ws_r, 1), dtype=torch.uint8, device=self.dev)
-        max_keep = k_cap + self.cfg.sink_size + max(self.cfg.local_window, 0)
+        # the tail holds the local window, or the newest token alone when
+        # there is none (keep_plan)
+        self.max_tail = max(self.cfg.local_window, 1)
+        max_keep = k_cap + self.cfg.sink_size + self.max_tail
         ws_a = N.size_query("lap_attn_decode_workspace_size", batch, num_q_heads, head_dim,
                             max(max_keep, 1))
         self.ws_attn = torch.empty(max(ws_a, 1), dtype=torch.uint8, device=self.dev)
@@ -199,7 +213,8 @@ class SparseDecoder:
         cs, ce = candidate_window(t_codes, t_total, c.sink_size, c.local_window)
         n = ce - cs
         k = min(c.topk, n) if c.topk is not None else budget_k(n, c.mask_out, c.min_remain)
-        sink, tail_start, tail_count = keep_segments(t_total, c.sink_size, c.local_window)
+        k = k if t_codes > 0 else 0
+        sink, tail_start, tail_count = keep_plan(k, t_total, c.sink_size, c.local_window)
         return dict(cand_start=cs, cand_end=ce, k=k, sink=sink, tail_start=tail_start,
                     tail_count=tail_count)
 
@@ -207,9 +222,7 @@ class SparseDecoder:
         """One plan per sequence (the uniform plan of each sequence's lengths)."""
         out = []
         for tc, tt in zip(t_codes, t_total):
-            p = self.plan(tc, tt)
-            p["k"] = p["k"] if tc > 0 else 0
-            out.append(dict(t_codes=tc, t_total=tt, **p))
+            out.append(dict(t_codes=tc, t_total=tt, **self.plan(tc, tt)))
         return out
 
     @torch.no_grad()
@@ -334,7 +347,7 @@ class SparseDecoder:
                N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, keys.shape[2], D, keys.stride(0),
                keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
                N.ptr(self.idx), N.I32, H_idx, k_cols, N.ptr(plans), self.cfg.sink_size,
-               max(self.cfg.local_window, 0), 1.0 / math.sqrt(D), N.ptr(self.out),
+               self.max_tail, 1.0 / math.sqrt(D), N.ptr(self.out),
                N.ptr(self.ws_attn), self.ws_attn.numel(), st)
         return self.out.unsqueeze(2)
 

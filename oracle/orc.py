@@ -280,7 +280,10 @@ def keep_list(topk_idx: np.ndarray, t_total: int, sink: int, local: int) -> np.n
         parts.append(np.arange(sb_eff, dtype=np.int64))
     if local > 0 and start < t_total:
         parts.append(np.arange(start, t_total, dtype=np.int64))
-    return np.concatenate(parts)
+    keep = np.concatenate(parts)
+    if keep.size == 0 and t_total > 0:  # nothing kept: the newest token (:233-234)
+        keep = np.array([t_total - 1], dtype=np.int64)
+    return keep
 
 
 def gather_rows(kv: np.ndarray, idx: np.ndarray, G: int) -> np.ndarray:

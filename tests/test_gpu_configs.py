@@ -1,0 +1,367 @@
+"""BASELINE configs C4 and C5 at their own sizes, checked for correctness.
+
+C5, one layer: batch 16, seeded per-sequence lengths uniform in
+[16384, 32768] (ragged), top-1024 per KV group on the bf16-cast scores, the
+newest ``len % 64`` keys of each sequence still unencoded (they are covered
+by the local window, as after a decode flush).  Eager and captured
+(``step_dev`` replayed from one graph) steps: every sequence's indices are
+bit-exact against the oracle's top-k of its own scores and window, and its
+attention output is within 1e-2 of float64 over its keep set.
+
+C5, model: Llama-3.1-8B attention geometry (hidden 4096, 32 / 8 heads,
+head_dim 128, the full MLP and vocabulary) with 4 layers (0-1 dense, 2-3
+LAPrune), batch 16, ragged prompts of 16k-32k tokens prefilled one sequence
+at a time, then 66 decode steps so that every sequence flushes its 64-token
+encode buffer once.  Keep-everything LAPrune equals the dense model; the
+captured top-1024 decode equals the eager one; the codes in the LAPrune
+caches (prefill rows and each sequence's flushed group) equal the oracle's
+greedy encode of the cached keys.
+
+C4, model: the full 32-layer random-init Llama-3.1-8B at a 131072-token
+context, batch 1 (layers 0-1 dense, 2-31 LAPrune, 4 sink, 64 local, 64-token
+buffer).  (i) keep-everything LAPrune equals the dense model; (ii) top-2048
+captured decode runs across a 64-token flush with finite logits and greedy
+tokens equal to the logits' argmax; (iii) at a sampled step one LAPrune
+layer's selection is bit-exact against the oracle over that layer's own
+cached codes and the step's post-RoPE query; (iv) the flushed codes and
+sampled prefill codes equal the oracle's encode.
+
+Logit tolerance: relative to the largest logit.  The sparse and dense
+attention kernels sum in different orders, so every LAPrune layer adds its
+own bf16 rounding noise to the residual stream; independent layers add in
+quadrature, so the tolerance is 1e-2 * sqrt(LAPrune layers) with a floor of
+3e-2 (the 2-layer tiny-model test measures 0.009).  A top-k control on the
+same step must move the logits by far more, so the comparison does see the
+attention.  Weights are random N(0, 0.02) from a local config (no
+download); prompts are uniform random token ids.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _synth import gaussian_codebooks
+
+pytestmark = pytest.mark.gpu
+
+SINK, LOCAL, GROUP = 4, 64, 64
+
+
+def _logit_tol(n_lap_layers):
+    return max(3e-2, 1e-2 * math.sqrt(n_lap_layers))
+
+
+def _rel(a, b):
+    a, b = a.float(), b.float()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-6))
+
+
+def _rel_np(a, b):
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-6))
+
+
+def _say(*a):
+    print("[c4c5]", *a, flush=True)
+
+
+def _oracle_selection(orc, q_rows, cb_np, codes_np, plan, topk, bf16_keys=True):
+    """Oracle top-k of one sequence: q_rows [Hq, D] float32, codes [Hkv, T, M]."""
+    lut = orc.lut_build(q_rows, cb_np)
+    s = orc.score_grouped(lut, codes_np[:, :plan["t_codes"]], 4)
+    return orc.topk(s, plan["k"], 4, plan["cand_start"], plan["cand_end"], key_bf16=bf16_keys)
+
+
+# ------------------------------------------------------------------ C5, one layer
+
+def _c5_lengths(seed, B=16):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(16384, 32769, (B,), generator=g).tolist()
+
+
+@pytest.mark.timeout(600)
+def test_c5_layer_ragged_topk_and_attention(dev, orc):
+    from laprune_amd.retrieval import PLAN_FIELDS, RetrievalConfig, SparseDecoder
+    B, Hq, Hkv, D = 16, 32, 8, 128
+    t_total = _c5_lengths(501)
+    t_codes = [t - t % GROUP for t in t_total]
+    T_max = max(t_total)
+    cap = 32768 + 64
+    _say("C5 layer lengths", t_total)
+    g = torch.Generator().manual_seed(502)
+    cb = gaussian_codebooks(503)
+    codes = torch.randint(0, 256, (B, Hkv, cap, 32), generator=g, dtype=torch.uint8)
+    q = torch.randn(B, Hq, 1, D, generator=g).bfloat16()
+    gd = torch.Generator(device=dev).manual_seed(504)
+    kk = torch.randn((B, Hkv, cap, D), generator=gd, device=dev).bfloat16()
+    vv = torch.randn((B, Hkv, cap, D), generator=gd, device=dev).bfloat16()
+    cfg = RetrievalConfig(topk=1024, sink_size=SINK, local_window=LOCAL, select="group",
+                          score_dtype=torch.bfloat16)
+    dec = SparseDecoder(cb.to(dev), B, Hq, Hkv, D, cap, cfg)
+    cd, qd = codes.to(dev), q.to(dev)
+    out = dec.step(qd, cd[:, :, :T_max], kk[:, :, :T_max], vv[:, :, :T_max], t_codes=t_codes,
+                   t_total=t_total).clone()
+    sel = dec.selected().cpu().numpy()
+    plans = dec.row_plans(t_codes, t_total)
+    assert all(p["k"] == 1024 for p in plans)
+    cb_np, codes_np = cb.numpy(), codes.numpy()
+    qf = q[:, :, 0].float().numpy()
+    want_idx = []
+    for b, p in enumerate(plans):
+        want = _oracle_selection(orc, qf[b], cb_np, codes_np[b], p, 1024)
+        assert np.array_equal(sel[b].astype(np.int64), want), b
+        want_idx.append(want)
+    _say("C5 layer: eager indices bit-exact for all 16 sequences")
+
+    def check_attn(o, which):
+        for b in (0, 5, 10, 15):
+            def keep(bb, h, b=b):
+                return orc.keep_list(want_idx[b][h // 4], t_total[b], SINK, LOCAL)
+            tt = t_total[b]
+            ref = orc.attn_decode_f64(q[b:b + 1, :, 0].double().numpy(),
+                                      kk[b:b + 1, :, :tt].double().cpu().numpy(),
+                                      vv[b:b + 1, :, :tt].double().cpu().numpy(), keep)
+            got = o[b:b + 1, :, 0].double().cpu().numpy()
+            assert _rel_np(got, ref) < 1e-2, (which, b)
+
+    check_attn(out, "eager")
+
+    # captured: fixed launches over the whole capacity, plans in device memory
+    plan_dev = torch.tensor([[p[f] for f in PLAN_FIELDS] for p in plans], dtype=torch.int32,
+                            device=dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        dec.step_dev(qd, cd, kk, vv, plan_dev)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = dec.step_dev(qd, cd, kk, vv, plan_dev)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        idx = dec.idx.cpu().numpy()
+        for b in range(B):
+            assert np.array_equal(idx[b, :, :1024].astype(np.int64), want_idx[b]), (rep, b)
+            assert np.all(idx[b, :, 1024:dec.k_cols] == -1), (rep, b)
+        check_attn(out_g.clone(), f"graph replay {rep}")
+        # eager work between replays (the graph must not depend on it)
+        dec.step(qd, cd[:, :, :T_max], kk[:, :, :T_max], vv[:, :, :T_max], t_codes=t_codes,
+                 t_total=t_total)
+        torch.cuda.synchronize()
+    _say("C5 layer: 3 graph replays bit-exact")
+
+    # the same graph after the host rewrites the plans (new lengths)
+    t_total2 = [max(t - 777 * (b % 3), 16500) for b, t in enumerate(t_total)]
+    t_codes2 = [t - t % GROUP for t in t_total2]
+    plans2 = dec.row_plans(t_codes2, t_total2)
+    plan_dev.copy_(torch.tensor([[p[f] for f in PLAN_FIELDS] for p in plans2],
+                                dtype=torch.int32))
+    graph.replay()
+    torch.cuda.synchronize()
+    idx = dec.idx.cpu().numpy()
+    for b in (1, 2, 7, 14):
+        want = _oracle_selection(orc, qf[b], cb_np, codes_np[b], plans2[b], 1024)
+        assert np.array_equal(idx[b, :, :1024].astype(np.int64), want), b
+
+
+# ------------------------------------------------------------------ models
+
+def _c5_model_config(layers=4):
+    from laprune_amd.llama import llama31_8b_config
+    return llama31_8b_config(num_layers=layers)
+
+
+def _teacher_tokens(seed, B, n, vocab=128256):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (B, n), generator=g)
+
+
+def _check_codes(orc, cache, cb_np, rows_per_seq, seed):
+    """Codes of sampled (sequence, head, token) rows of a cache against the
+    oracle's encode of the cached keys."""
+    g = torch.Generator().manual_seed(seed)
+    xs, got = [], []
+    for b, n_enc in enumerate(cache.encoded_lens):
+        hs = torch.randint(0, cache.Hkv, (rows_per_seq,), generator=g)
+        ts = torch.randint(0, n_enc, (rows_per_seq,), generator=g)
+        xs.append(cache.k[b, hs, ts].float().cpu())
+        got.append(cache.codes[b, hs, ts].cpu())
+    x = torch.cat(xs).numpy()
+    want, _ = orc.encode(x, cb_np)
+    assert np.array_equal(torch.cat(got).numpy(), want)
+
+
+def _check_flushed(orc, cache, cb_np, b, t0, t1):
+    x = cache.k[b, :, t0:t1].float().reshape(-1, cache.D).cpu().numpy()
+    want, _ = orc.encode(x, cb_np)
+    got = cache.codes[b, :, t0:t1].reshape(-1, cache.M).cpu().numpy()
+    assert np.array_equal(got, want), (b, t0, t1)
+
+
+@pytest.mark.timeout(900)
+def test_c5_model_ragged_decode(dev, orc):
+    from laprune_amd.llama import LAPruneLlama, LAPruneSettings, random_model
+    from laprune_amd.retrieval import RetrievalConfig
+    B, layers, steps = 16, 4, 66
+    lengths = _c5_lengths(511)
+    cfg = _c5_model_config(layers)
+    apply = [2, 3]
+    cbs = {i: gaussian_codebooks(520 + i) for i in apply}
+    prompts = _teacher_tokens(512, B, max(lengths))
+    teach = _teacher_tokens(513, B, steps)
+    cap = max(lengths) + steps + 64
+    P = random_model(cfg, dev, seed=514)
+    Q = random_model(cfg, dev, seed=514)
+
+    def settings(**kw):
+        return LAPruneSettings(apply_layers=apply, group_size=GROUP, retrieval=RetrievalConfig(
+            sink_size=SINK, local_window=LOCAL, select="group", score_dtype=torch.bfloat16, **kw))
+
+    def prefill(lm):
+        for b, n in enumerate(lengths):
+            lm.prefill_row(b, prompts[b:b + 1, :n - 1])
+        assert lm.lengths == [n - 1 for n in lengths]
+
+    def first_tok():
+        return torch.stack([prompts[b, n - 1] for b, n in enumerate(lengths)])[:, None]
+
+    # keep everything (mask_out = 0) against the dense model, 8 steps
+    keep = LAPruneLlama(P, cbs, settings(mask_out=0.0), batch=B, capacity=cap)
+    dense = LAPruneLlama(Q, {}, LAPruneSettings(apply_layers=[], group_size=GROUP),
+                         batch=B, capacity=cap)
+    prefill(keep)
+    prefill(dense)
+    _say("C5 model: prefilled keep-all and dense")
+    tok = first_tok()
+    for i in range(8):
+        a = keep.decode(tok)
+        d = dense.decode(tok)
+        assert torch.isfinite(d).all()
+        assert _rel(a, d) < 3e-2, i
+        tok = teach[:, i:i + 1]
+    del keep, dense
+    torch.cuda.empty_cache()
+    _say("C5 model: keep-all == dense for 8 steps")
+
+    # top-1024: captured steps against eager steps, across every flush
+    graph = LAPruneLlama(P, cbs, settings(topk=1024), batch=B, capacity=cap)
+    eager = LAPruneLlama(Q, cbs, settings(topk=1024), batch=B, capacity=cap)
+    prefill(graph)
+    prefill(eager)
+    _say("C5 model: prefilled top-1024 graph and eager")
+    tok = first_tok()
+    for i in range(steps):
+        want = eager.decode(tok)
+        got = graph.decode_graph(tok)
+        assert torch.isfinite(got).all(), i
+        assert _rel(got, want) < 3e-2, i
+        assert torch.equal(graph.next_tokens(), got.argmax(dim=-1, keepdim=True))
+        tok = teach[:, i:i + 1]
+    torch.cuda.synchronize()
+    for a, b in zip(eager.states, graph.states):
+        assert a.cache.lengths == b.cache.lengths
+        assert a.cache.encoded_lens == b.cache.encoded_lens
+    for L in apply:
+        cache = graph.states[L].cache
+        assert cache.lengths == [n - 1 + steps for n in lengths]
+        assert cache.encoded_lens == [n - 1 + GROUP for n in lengths], "one flush each"
+        cb_np = cbs[L].numpy()
+        _check_codes(orc, cache, cb_np, rows_per_seq=8, seed=530 + L)
+        for b in range(0, B, 5):
+            _check_flushed(orc, cache, cb_np, b, lengths[b] - 1, lengths[b] - 1 + GROUP)
+    _say("C5 model: graph == eager over 66 steps; codes exact")
+
+
+@pytest.mark.timeout(900)
+def test_c4_model_128k(dev, orc):
+    from laprune_amd.llama import LAPruneLlama, LAPruneSettings, llama31_8b_config, random_model
+    from laprune_amd.retrieval import RetrievalConfig
+    T = 131072
+    layers = 32
+    apply = list(range(2, layers))
+    probe_layer = 17
+    graph_steps = 66
+    cfg = llama31_8b_config(num_layers=layers)
+    cbs = {i: gaussian_codebooks(600 + i) for i in apply}
+    prompt = _teacher_tokens(601, 1, T)
+    teach = _teacher_tokens(602, 1, 4 + graph_steps)
+    cap = T + graph_steps + 64
+    P = random_model(cfg, dev, seed=603)
+    Q = random_model(cfg, dev, seed=603)
+    rcfg = RetrievalConfig(mask_out=0.0, sink_size=SINK, local_window=LOCAL, select="group",
+                           score_dtype=torch.bfloat16)
+    lm = LAPruneLlama(P, cbs, LAPruneSettings(apply_layers=apply, retrieval=rcfg,
+                                              group_size=GROUP), batch=1, capacity=cap)
+    dense = LAPruneLlama(Q, {}, LAPruneSettings(apply_layers=[], group_size=GROUP), batch=1,
+                         capacity=cap)
+    lm.prefill(prompt[:, :-1])
+    dense.prefill(prompt[:, :-1])
+    torch.cuda.synchronize()
+    _say("C4: prefilled LAPrune and dense at 131071 tokens")
+    # (i) keep everything: the LAPrune layers select all 131007 candidates
+    tok = prompt[:, -1:]
+    errs = []
+    for i in range(3):
+        a = lm.decode(tok)
+        d = dense.decode(tok)
+        assert torch.isfinite(d).all()
+        errs.append(_rel(a, d))
+        tok = teach[:, i:i + 1]
+    _say("C4: keep-all vs dense", [round(e, 4) for e in errs], "tol",
+         round(_logit_tol(len(apply)), 4))
+    assert max(errs) < _logit_tol(len(apply))
+
+    # (iii) top-2048 from here on; one eager step records the probe layer's query
+    rcfg.topk = 2048
+    st = lm.states[probe_layer]
+    seen = {}
+    orig = st.sparse.step_cached
+
+    def probe(q, cache):
+        seen["q"] = q.detach().clone()
+        seen["t_codes"] = cache.encoded_lens[0]
+        seen["t_total"] = cache.lengths[0]
+        o = orig(q, cache)
+        seen["sel"] = st.sparse.selected().clone()
+        return o
+
+    st.sparse.step_cached = probe
+    try:
+        a = lm.decode(tok)
+    finally:
+        st.sparse.step_cached = orig
+    control = _rel(a, dense.decode(tok))
+    _say("C4: top-2048 vs dense (control)", round(control, 4))
+    assert control > 2 * max(errs), "pruning must be visible in the logits"
+    del dense, Q
+    torch.cuda.empty_cache()
+    tok = teach[:, 3:4]
+    p = st.sparse.plan(seen["t_codes"], seen["t_total"])
+    p["t_codes"] = seen["t_codes"]
+    assert p["k"] == 2048
+    want = _oracle_selection(orc, seen["q"][0, :, 0].float().cpu().numpy(),
+                             cbs[probe_layer].numpy(), st.cache.codes[0].cpu().numpy(), p, 2048)
+    got = seen["sel"][0].cpu().numpy().astype(np.int64)
+    assert np.array_equal(got, want)
+    _say("C4: probe layer selection bit-exact at t_total", seen["t_total"])
+
+    # (ii) captured top-2048 decode across a 64-token flush
+    enc0 = st.cache.encoded_lens[0]
+    for i in range(graph_steps):
+        logits = lm.decode_graph(tok if i == 0 else teach[:, 4 + i - 1:4 + i])
+        assert torch.isfinite(logits).all(), i
+        assert torch.equal(lm.next_tokens(), logits.argmax(dim=-1, keepdim=True)), i
+    torch.cuda.synchronize()
+    n = st.cache.lengths[0]
+    assert n == T - 1 + 4 + graph_steps
+    assert st.cache.encoded_lens[0] == enc0 + GROUP, "one flush inside the captured steps"
+    _say("C4: captured decode crossed the flush at", enc0 + GROUP)
+
+    # (iv) flushed and sampled prefill codes
+    for L in (2, probe_layer, layers - 1):
+        cache = lm.states[L].cache
+        cb_np = cbs[L].numpy()
+        _check_flushed(orc, cache, cb_np, 0, enc0, enc0 + GROUP)
+        _check_codes(orc, cache, cb_np, rows_per_seq=256, seed=610 + L)
+    _say("C4: flushed and prefill codes exact")

@@ -154,3 +154,27 @@ def test_generate_with_captured_steps(dev):
     out = lm.generate(ids, max_new_tokens=70, graph=True)
     assert out.shape == (2, 170) and torch.equal(out[:, :100].cpu(), ids)
     assert lm.lengths == [169, 169] and lm.states[1].cache.encoded_lens == [163, 163]
+
+
+def test_over_capacity_raises_without_appending(dev):
+    """A step that would exceed the capacity the decoders were sized for
+    raises before any layer runs, so every layer keeps the same length."""
+    from laprune_amd.llama import LAPruneLlama, LAPruneSettings, random_model
+    from laprune_amd.retrieval import RetrievalConfig
+    s = LAPruneSettings(apply_layers=[1, 2], retrieval=RetrievalConfig(topk=16))
+    lm = LAPruneLlama(random_model(_tiny(), dev, seed=6), _codebooks([1, 2]), s, batch=2,
+                      capacity=128)
+    ids = torch.randint(0, VOCAB, (2, 129), generator=torch.Generator().manual_seed(8))
+    with pytest.raises(RuntimeError, match="capacity"):
+        lm.prefill(ids)
+    assert all(st.cache.lengths == [0, 0] for st in lm.states)
+    lm.prefill(ids[:, :127])
+    lm.decode(ids[:, 127:128])
+    assert lm.lengths == [128, 128]
+    for call in (lambda: lm.decode(ids[:, 128:129]), lambda: lm.decode_graph(ids[:, 128:129]),
+                 lambda: lm.prefill_row(0, ids[:1, :4])):
+        with pytest.raises(RuntimeError, match="capacity"):
+            call()
+        assert all(st.cache.lengths == [128, 128] for st in lm.states)
+        assert all(st.cache.encoded_lens == lm.states[1].cache.encoded_lens
+                   for st in lm.states[1:])

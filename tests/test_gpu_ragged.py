@@ -340,3 +340,33 @@ def test_encode_keys_ranges_per_sequence(dev, orc):
                 assert np.array_equal(got[b, h, t0:t1], want), (b, h)
             outside = np.concatenate([got[b, h, :t0], got[b, h, t1:]])
             assert np.all(outside == 0xAB), (b, h)
+
+
+def test_empty_keep_set_attends_newest_token(dev):
+    """No candidates (nothing encoded yet), no sink and no local window: the
+    reference keeps token T_total - 1 (aq_evaluation.py:233-234), so every
+    head's output is that token's V row.  Uniform, ragged and device-plan
+    steps."""
+    from laprune_amd.retrieval import PLAN_FIELDS, RetrievalConfig, SparseDecoder
+    g = _gen(380)
+    B, Hq, Hkv, D, T = 2, 32, 8, 128, 96
+    cb = (torch.randn(32, 256, D, generator=g) * 0.02).to(dev)
+    codes = torch.zeros(B, Hkv, T, 32, dtype=torch.uint8, device=dev)
+    kk = torch.randn(B, Hkv, T, D, generator=g).bfloat16().to(dev)
+    vv = torch.randn(B, Hkv, T, D, generator=g).bfloat16().to(dev)
+    q = torch.randn(B, Hq, 1, D, generator=g).bfloat16().to(dev)
+    dec = SparseDecoder(cb, B, Hq, Hkv, D, T, RetrievalConfig(sink_size=0, local_window=0))
+
+    def newest(lengths):
+        rows = torch.stack([vv[b, :, n - 1] for b, n in enumerate(lengths)])  # [B, Hkv, D]
+        return rows.repeat_interleave(Hq // Hkv, dim=1)
+
+    out = dec.step(q, codes[:, :, :0], kk[:, :, :80], vv[:, :, :80], t_codes=0, t_total=80)
+    assert torch.equal(out[:, :, 0], newest([80, 80]))
+    lens = [50, 70]
+    out = dec.step(q, codes, kk, vv, t_codes=[0, 0], t_total=lens)
+    assert torch.equal(out[:, :, 0], newest(lens))
+    plans = torch.tensor([[p[f] for f in PLAN_FIELDS] for p in dec.row_plans([0, 0], lens)],
+                         dtype=torch.int32, device=dev)
+    out = dec.step_dev(q, codes, kk, vv, plans)
+    assert torch.equal(out[:, :, 0], newest(lens))

@@ -17,9 +17,73 @@ def test_window_budget_keep(t, sink, local):
     cs, ce = R.candidate_window(t, t, sink, local)
     n = ce - cs
     assert R.budget_k(n, 0.98, 20) == orc.budget_k(n)
-    sb, start, tail = R.keep_segments(t, sink, local)
+    sb, start, tail = R.keep_plan(0, t, sink, local)
     keep = orc.keep_list(np.zeros(0, np.int64), t, sink, local)
     assert keep.tolist() == list(range(sb)) + list(range(start, start + tail))
+
+
+def test_empty_keep_set_keeps_newest_token():
+    """No candidate selected, no sink and no local window: the reference
+    keeps token T_total - 1 (aq_evaluation.py:233-234); selecting something
+    or having either window disables the fallback."""
+    for t in (1, 2, 100, 131072):
+        assert R.keep_plan(0, t, 0, 0) == (0, t - 1, 1)
+        assert orc.keep_list(np.zeros(0, np.int64), t, 0, 0).tolist() == [t - 1]
+        assert R.keep_plan(5, t, 0, 0) == (0, t, 0)
+        assert orc.keep_list(np.array([0]), t, 0, 0).tolist() == [0]
+    assert R.keep_plan(0, 0, 0, 0) == (0, 0, 0)
+    assert R.keep_plan(0, 100, 4, 0) == (4, 100, 0)
+    assert R.keep_plan(0, 100, 0, 8) == (0, 92, 8)
+
+
+def _tiny_attention(bias: bool):
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaAttention
+    cfg = LlamaConfig(hidden_size=64, num_attention_heads=4, num_key_value_heads=2, head_dim=16,
+                      attention_bias=bias)
+    torch.manual_seed(3)
+    attn = LlamaAttention(cfg, layer_idx=0)
+    with torch.no_grad():
+        for p in attn.parameters():
+            p.normal_()
+    return attn
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_fused_qkv_projection(bias):
+    """The fused [q; k; v] GEMV equals the three module projections, with and
+    without biases, and is fused again when the parameters are replaced
+    (model.to(dtype) after wrapping)."""
+    from laprune_amd.llama import LAPruneLlama
+    attn = _tiny_attention(bias)
+    h = torch.randn(2, 3, 64)
+    want = [attn.q_proj(h), attn.k_proj(h), attn.v_proj(h)]
+    LAPruneLlama._fuse_qkv(attn)
+    w, b, sizes = attn._lap_qkv
+    assert sizes == [64, 32, 32] and (b is not None) == bias
+    got = LAPruneLlama._project(attn, h)
+    for g_, w_ in zip(got, want):
+        torch.testing.assert_close(g_, w_, rtol=0, atol=1e-5)
+    assert LAPruneLlama._fused_current(attn)
+    attn.to(torch.float64)  # replaces every parameter
+    assert not LAPruneLlama._fused_current(attn)
+    h64 = h.double()
+    got = LAPruneLlama._project(attn, h64)
+    assert attn._lap_qkv[0].dtype == torch.float64 and LAPruneLlama._fused_current(attn)
+    for g_, w_ in zip(got, want):
+        torch.testing.assert_close(g_.float(), w_, rtol=0, atol=1e-4)
+
+
+def test_fused_qkv_mixed_bias_falls_back():
+    from laprune_amd.llama import LAPruneLlama
+    attn = _tiny_attention(True)
+    attn.k_proj.bias = None
+    h = torch.randn(1, 2, 64)
+    want = [attn.q_proj(h), attn.k_proj(h), attn.v_proj(h)]
+    LAPruneLlama._fuse_qkv(attn)
+    assert attn._lap_qkv is None
+    for g_, w_ in zip(LAPruneLlama._project(attn, h), want):
+        assert torch.equal(g_, w_)
 
 
 def test_keep_parts_are_disjoint_from_candidates():
