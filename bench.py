@@ -434,7 +434,8 @@ def main():
         return dense.step(q_sets[i % N_CODE_SETS], kk[:, :, :T], vv[:, :, :T])
 
     plan = dec.plan(T, T)
-    ws = dec.ws_sel
+    ws = torch.empty(N.size_query("lap_retrieve_workspace_size", HKV, T), dtype=torch.uint8,
+                     device=dev)
 
     def score_only(i):
         c = codes_sets[i % N_CODE_SETS][:, :, :T]

@@ -323,6 +323,56 @@ int lap_sparse_attn_decode_ragged(const void* q, int64_t q_sb, int64_t q_sh,
                                   lap_stream_t stream);
 
 /* ======================================================================= *
+ * A2 + A3 + A4 + A5  One decode step after the LUT                         *
+ * Replaces the chain of _decode_attention for one layer and one token,     *
+ *   laprune/llm/modifiers/aq_evaluation.py:146-253: grouped LUT scoring    *
+ *   (aq_kv.py:684 -> aq_kernels/aq_lut_gqa.cu:460-534), the candidate      *
+ *   window and torch.topk (aq_evaluation.py:185-205), the keep set         *
+ *   (:210-237), the K/V gather (aq_lut_gqa.cu:606-664) and SDPA (:251).    *
+ * ======================================================================= *
+ * Same results as lap_retrieve_topk (lap_retrieve_topk_ragged when plans is
+ * non-NULL) followed by lap_sparse_attn_decode (_ragged) with H_idx = Hkv
+ * (or Hq with LAP_SELECT_PER_HEAD): the selected indices in out_idx
+ * [B][rows][k] (ragged: [B][rows][k_cols], padded with -1) and the attention
+ * output in out [B][Hq][D].  Uniform calls pass the window, budget, sink and
+ * tail as scalars (k is clamped to the window; k_cols, max_sink and max_tail
+ * are ignored); ragged calls read them per sequence from plans.
+ *   codes  u8 [B][Hkv][>=T][32] strides (b, h, t, 1), 16-byte aligned (may
+ *          be NULL when the call selects nothing: k = 0, or k_cols = 0)
+ *   T      code columns scored (the grid; plans clamp to it), T_kv K/V rows
+ *   q, K, V as lap_sparse_attn_decode; G = Hq / Hkv must be 4
+ * Group selection with D = 128 runs as one launch (per KV row, the
+ * workgroups of one XCD score, select and attend, and the last merges);
+ * other shapes run the kernel chain.  Workspace: lap_decode_step_workspace_size
+ * with keep_max = k + sink + tail (ragged: k_cols + max_sink + max_tail).  It
+ * must be zero-filled once before its first use; every call leaves its
+ * barrier words at zero again.  Calls that share a workspace must be ordered
+ * (same stream). */
+int lap_decode_step_workspace_size(int B, int Hq, int Hkv, int T, int D, int keep_max,
+                                   int key_mode, size_t* bytes);
+int lap_decode_step(const void* lut_gmkg, const uint8_t* codes,
+                    int64_t codes_stride_b, int64_t codes_stride_h, int64_t codes_stride_t,
+                    int T, int cand_start, int cand_end, int k,
+                    int sink_count, int tail_start, int tail_count,
+                    const lap_row_plan* plans, int k_cols, int max_sink, int max_tail,
+                    int key_mode,
+                    const void* q, int64_t q_sb, int64_t q_sh,
+                    const void* keys, const void* vals, int dtype,
+                    int B, int Hq, int Hkv, int T_kv, int D,
+                    int64_t k_sb, int64_t k_sh, int64_t k_st,
+                    int64_t v_sb, int64_t v_sh, int64_t v_st, float scale,
+                    void* out_idx, int idx_dtype, void* out,
+                    void* workspace, size_t workspace_bytes, lap_stream_t stream);
+/* Health counters of the one-launch step in a lap_decode_step workspace
+ * (copied to the host, synchronising): rows whose workgroups did not all run
+ * on one XCD (their exchange through that XCD's L2 then has no guarantee),
+ * and barrier spins that gave up.  Both stay zero on a healthy device; a
+ * non-zero count means the calls since the workspace was zeroed are not to
+ * be trusted. */
+int lap_decode_step_status(const void* workspace, size_t workspace_bytes,
+                           uint32_t* split_rows, uint32_t* timeouts);
+
+/* ======================================================================= *
  * A6  Greedy AQ encode                                                     *
  * Replaces: fused_linear_encode_forward, aq_kernels/fused_linear_encode.cu:
  *   168-234 (kernel :34-102), called from laprune/llm/aq_kv.py:44-75; the

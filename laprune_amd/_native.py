@@ -43,6 +43,7 @@ _TORCH_DTYPE = {
 vp, i32, i64, f32, sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
 psz = C.POINTER(C.c_size_t)
 pint = C.POINTER(C.c_int)
+pu32 = C.POINTER(C.c_uint32)
 
 # name -> argtypes; every function returns int status
 SIGNATURES = {
@@ -77,6 +78,11 @@ SIGNATURES = {
                                       f32, vp, vp, sz, vp],
     "lap_dense_attn_decode": [vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32, i64, i64,
                               i64, i64, i64, i64, f32, vp, vp, sz, vp],
+    "lap_decode_step_workspace_size": [i32, i32, i32, i32, i32, i32, i32, psz],
+    "lap_decode_step": [vp, vp, i64, i64, i64, i32, i32, i32, i32, i32, i32, i32, vp, i32, i32,
+                        i32, i32, vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32, i64, i64,
+                        i64, i64, i64, i64, f32, vp, i32, vp, vp, sz, vp],
+    "lap_decode_step_status": [vp, sz, pu32, pu32],
     "lap_encode_prep_size": [i32, i32, i32, psz],
     "lap_encode_prepare": [vp, i32, i32, i32, vp, sz, vp],
     "lap_encode_greedy": [vp, i64, i32, i32, vp, i32, i32, vp, sz, vp, i64, vp, vp],
@@ -156,6 +162,10 @@ def dtype_code(dt: torch.dtype) -> int:
 
 def ptr(t: torch.Tensor | None):
     return None if t is None else C.c_void_p(t.data_ptr())
+
+
+u32 = C.c_uint32
+byref = C.byref
 
 
 def stream_of(t: torch.Tensor):

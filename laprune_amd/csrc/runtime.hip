@@ -55,7 +55,7 @@ extern "C" {
 
 const char* lap_last_error(void) { return lap::t_error.c_str(); }
 
-int lap_abi_version(void) { return 6; }
+int lap_abi_version(void) { return 7; }
 
 int lap_device_info(int* cu_count, int* lds_bytes_per_block, int* wave_size) {
   lap::DevInfo d;

@@ -1,0 +1,819 @@
+// step.hip — the fused decode step: A2 scoring, A3 selection and A5
+// attention, with the split merge, in one launch.
+//
+// Replaces, for one layer and one decode token, the chain of the reference's
+// _decode_attention (laprune/llm/modifiers/aq_evaluation.py:146-253):
+// grouped LUT scoring (aq_kv.py:684 -> aq_lut_gqa.cu:460-534), the candidate
+// window and torch.topk (aq_evaluation.py:185-205), the keep set (:210-237)
+// and SDPA over the kept rows (:251).  The LUT itself is built by the
+// launch before (lut.hip), which is the only other kernel of the step.
+//
+// Work shape.  Selection is per KV group (the group max of its four query
+// heads' scores).  Each KV row r (batch row b, KV head h) is served by WR
+// workgroups of 1024 threads, all on the same XCD: the hardware deals a
+// launch's workgroups to the XCDs round-robin by block id (block i runs on
+// XCD (i + s) % nxcc, where the start s can differ from launch to launch),
+// and the blocks of row r are the ones with i % nxcc == r % nxcc.  The last
+// workgroup of each row checks, from the XCC_ID registers its row's
+// workgroups recorded, that they did share one XCD, and counts any row that
+// did not in the status word.  The workgroups of a row share one L2, and the data they pass
+// each other (histograms, candidates, attention partials) never leaves it:
+// a producer's plain stores are complete in L2 once its vmcnt drains, and a
+// consumer reads them with device-scope loads, which miss the L1 (where a
+// stale copy could sit) and hit the shared L2.  No cache write-back or
+// invalidate is needed, which is what makes the two in-kernel barriers cost
+// well under a kernel boundary.
+//
+// Phases of the workgroup owning chunk c of row r (TOK * 1024 tokens):
+//   S  score its tokens (the scorer's pipeline, score_core.h): selection keys
+//      stay in registers, the level-1 histogram of the key high bytes over
+//      the candidate window goes to the row's histogram array;
+//   B1 row barrier;
+//   H  sum the row's chunk histograms: the threshold bin b1, the number of
+//      keys above it, and this chunk's offset among the row's candidates
+//      (keys in bins >= b1);
+//   C  write the chunk's candidates (key, column) in column order;
+//   B2 row barrier;
+//   F  every workgroup of the row reads the row's candidate list and runs
+//      the rest of the radix select on it (level 2 on the low bytes of bin
+//      b1, then the ordered selection: keys above tau, then the `need`
+//      lowest-column ties), so each knows the whole selection without a
+//      third barrier; it keeps the slice of the keep list (selection ++ sink
+//      ++ local tail) it attends to and writes that slice's indices;
+//   A  attention of the group's four query heads over the slice (the MFMA
+//      wave step of attn_core.h), one (m, l, o) partial per head;
+//   E  the last workgroup of the row to arrive merges the partials and
+//      writes the output.
+// Selection results equal the two-level top-k of topk.hip bit for bit: the
+// same keys, threshold and tie rule.
+//
+// Barriers spin a bounded number of polls; a spin that gives up counts a
+// time-out in the status word and lets the kernel finish (results of that
+// call are then undefined, and the caller must re-zero the workspace).
+#include "common.h"
+#include "attn_core.h"
+#include "score_core.h"
+#include "topk_core.h"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace lap {
+
+bool score_g4_supported(const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t);
+
+namespace {
+
+constexpr int kTH = 1024;
+constexpr int kWaves = kTH / 64;
+constexpr int kMaxTok = 8;          // tokens per thread (chunk = TOK * 1024)
+constexpr int kHC = 4;              // level-1 histogram copies
+constexpr int kDh = 128;            // head dim of the fused path
+constexpr int kKeepMax = 8192;      // keep-list slice per workgroup (32 KiB of LDS)
+constexpr int kSpin = 1 << 21;      // polls before a barrier gives up
+constexpr int kBarWords = 16;       // one 64-byte line per barrier
+constexpr int kStatusBytes = 256;
+
+struct StepArgs {
+  const uint16_t* lut;   // [R][M][K][4] fp16 (GMKG)
+  const uint8_t* codes;
+  int64_t cs_b, cs_h, cs_t;
+  int B, Hkv, T;         // T: code columns the grid covers
+  const int32_t* plans;  // lap_row_plan[B] or null (then the scalars below)
+  int cand_start, cand_end, k, sink, tail_start, tail_count;
+  int k_cols;            // index row stride; rows pad [k, k_cols) with -1
+  int max_sink, max_tail;
+  int key_bf16;
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
+  int T_kv;              // K/V rows available
+  float scale_log2;
+  void* idx;
+  int idx_i64;
+  uint16_t* out;         // [B][Hkv * 4][128]
+  uint32_t* status;      // [0] rows spread over XCDs, [1] barrier time-outs
+  uint32_t* bar;         // [R][3][kBarWords]
+  uint32_t* hist;        // [R][WR][256]
+  uint2* cand;           // [R][cand_cap] (key, column)
+  float* part;           // [R][WR][4][kDh + 2] (m, l, o)
+  int nxcc, RX, WR, cand_cap, keep_cap;
+  _Float16 one;
+};
+
+// One row's windows: the call's scalars, or its sequence's plan clamped to
+// the grid (as the scorer, top-k and attention kernels clamp them).
+struct StepRow {
+  int t_end, cs, ce, k, sink, tail_start, tail_count, t_total;
+};
+__device__ __forceinline__ StepRow step_row(const StepArgs& a, int b) {
+  if (!a.plans)
+    return StepRow{a.T, a.cand_start, a.cand_end, a.k, a.sink, a.tail_start, a.tail_count,
+                   a.T_kv};
+  const int32_t* p = a.plans + (int64_t)b * kPlanInts;
+  const int te = min(max(p[0], 0), a.T);
+  const int c0 = min(max(p[2], 0), te), c1 = min(max(p[3], c0), te);
+  return StepRow{te,
+                 c0,
+                 c1,
+                 max(0, min(min(p[4], c1 - c0), a.k_cols)),
+                 min(max(p[5], 0), a.max_sink),
+                 p[6],
+                 min(max(p[7], 0), a.max_tail),
+                 min(p[1], a.T_kv)};
+}
+
+__device__ __forceinline__ unsigned xcc_id() {
+  return __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11));  // HW_REG_XCC_ID[15:0]
+}
+
+// Device-scope loads of what other workgroups of the row wrote (they miss
+// the L1 and are served by the XCD's L2).
+template <typename T>
+__device__ __forceinline__ T ld_dev(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint2 ld_dev2(const uint2* p) {
+  const uint64_t v = ld_dev(reinterpret_cast<const uint64_t*>(p));
+  return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+
+// Sense-reversing barrier of the n workgroups of one row, run by one thread
+// of each after its workgroup's stores have drained.  blk[0] counts
+// arrivals and returns to zero; blk[1] is the generation the last arrival
+// advances.
+__device__ void row_barrier(uint32_t* blk, int n, uint32_t* status) {
+  uint32_t* cnt = blk;
+  uint32_t* gen = blk + 1;
+  const uint32_t g0 = ld_dev(gen);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the generation is read before arriving
+  const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old == (uint32_t)n - 1) {
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  for (int s = 0; s < kSpin; ++s) {
+    if (ld_dev(gen) != g0) return;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  __hip_atomic_fetch_add(status + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// All of the workgroup's global stores complete, then one barrier arrival.
+__device__ __forceinline__ void wg_row_barrier(const StepArgs& a, int r, int which) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) row_barrier(a.bar + ((int64_t)r * 3 + which) * kBarWords, a.WR, a.status);
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t key_of_score(float e, int key_bf16) {
+  const uint16_t h = f2h(e);
+  return key_bf16 ? bf16_key_of_f16(h) : f16_key(h);
+}
+
+template <typename IT>
+__device__ __forceinline__ void put_idx(void* idx, int64_t i, int v) {
+  static_cast<IT*>(idx)[i] = (IT)v;
+}
+
+// LDS carve of the 64 KiB region that holds the table during S.
+struct Lds {
+  uint4* lut;                // S: [kLutBytes / 16]
+  uint32_t (*tot)[256];      // H: [4][256]
+  uint32_t (*pre)[256];      // H: [4][256]
+  int* keep;                 // F, A: [kKeepMax]
+  float* o;                  // A: [kWaves][4][kDh]
+};
+
+template <int DT, int TOK>
+__global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
+  static_assert(TOK >= 1 && TOK <= kMaxTok, "TOK");
+  static_assert(kKeepMax * 4 + kWaves * 4 * kDh * 4 <= kLutBytes, "LDS carve");
+  __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
+  __shared__ uint32_t s_hist[kHC * kHPitch];
+  __shared__ uint32_t s_h2[256], s_wsum[kWaves], s_res[4], s_cnt[kMaxTok][kWaves];
+  __shared__ uint32_t s_red[kWaves], s_flag;
+  __shared__ float s_m[kWaves][4], s_l[kWaves][4];
+
+  Lds lds;
+  lds.lut = s_big;
+  lds.tot = reinterpret_cast<uint32_t(*)[256]>(s_big);
+  lds.pre = reinterpret_cast<uint32_t(*)[256]>(reinterpret_cast<uint32_t*>(s_big) + 4 * 256);
+  lds.keep = reinterpret_cast<int*>(s_big);
+  lds.o = reinterpret_cast<float*>(s_big) + kKeepMax;
+
+  const int nx = a.nxcc;
+  const int x = blockIdx.x % nx, slot = blockIdx.x / nx;
+  const int rs = slot / a.WR, c = slot - rs * a.WR;
+  const int r = rs * nx + x;
+  if (rs >= a.RX || r >= a.B * a.Hkv) return;  // no row here
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = r / a.Hkv, hkv = r - b * a.Hkv;
+  const StepRow pr = step_row(a, b);
+  constexpr int CH = TOK * kTH;
+  const int t0 = c * CH, t1 = min(pr.t_end, t0 + CH);
+  const bool select = pr.k > 0;
+
+  // ---------------------------------------------------------------- S
+  uint32_t kv[TOK];
+#pragma unroll
+  for (int j = 0; j < TOK; ++j) kv[j] = 0xffffffffu;  // no key
+  for (int i = tid; i < kHC * kHPitch; i += kTH) s_hist[i] = 0;
+  if (select && t0 < t1) {
+    constexpr int kFill = kLutBytes / 16 / kTH;
+    const uint4* src = reinterpret_cast<const uint4*>(a.lut + (int64_t)r * (kG * kM * kK));
+    u32x4 f[kFill];
+#pragma unroll
+    for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * kTH + tid);
+    const uint8_t* crow = a.codes + (int64_t)b * a.cs_b + (int64_t)hkv * a.cs_h;
+    u32x4 cc[TOK][2];
+    auto request = [&](int j) {
+      const int t = min(t0 + j * kTH + tid, t1 - 1);
+      const uint8_t* p = crow + (int64_t)t * a.cs_t;
+      cc[j][0] = gload16_ordered(p);
+      cc[j][1] = gload16_ordered(p + 16);
+    };
+    request(0);
+#pragma unroll
+    for (int i = 0; i < kFill; ++i) {
+      vm_wait(kFill - 1 - i + 2, f[i]);
+      lds.lut[i * kTH + tid] = as_uint4(f[i]);
+    }
+    lds_barrier();
+    const char* tab = reinterpret_cast<const char*>(lds.lut);
+    const int copy = (int)(__lane_id() % kHC) * kHPitch;
+#pragma unroll
+    for (int j = 0; j < TOK; ++j) {
+      vm_wait(0, cc[j][0], cc[j][1]);
+      if (j + 1 < TOK) request(j + 1);
+      float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
+      score_token(tab, as_uint4(cc[j][0]), as_uint4(cc[j][1]), a.one, e0, e1, e2, e3);
+      const int t = t0 + j * kTH + tid;
+      if (t < t1 && t >= pr.cs && t < pr.ce) {
+        const uint32_t key = key_of_score(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)), a.key_bf16);
+        kv[j] = key;
+        atomicAdd(&s_hist[copy + (key >> 8)], 1u);
+      }
+    }
+  }
+  __syncthreads();
+  if (select && tid < 256) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int cp = 0; cp < kHC; ++cp) v += s_hist[cp * kHPitch + tid];
+    a.hist[((int64_t)r * a.WR + c) * 256 + tid] = v;
+  }
+
+  // ---------------------------------------------------------------- B1, H
+  uint32_t b1 = 0, gt1 = 0, n_cand = 0, my_off = 0;
+  if (select) {
+    wg_row_barrier(a, r, 0);
+    const int bin = tid & 255, part = tid >> 8;
+    uint32_t tot = 0, pre = 0;
+    const uint32_t* hr = a.hist + (int64_t)r * a.WR * 256 + bin;
+    for (int cc2 = part; cc2 < a.WR; cc2 += 4) {
+      const uint32_t v = ld_dev(hr + (int64_t)cc2 * 256);
+      tot += v;
+      pre += cc2 < c ? v : 0u;
+    }
+    lds.tot[part][bin] = tot;
+    lds.pre[part][bin] = pre;
+    __syncthreads();
+    if (tid < 256) {
+      lds.tot[0][tid] += lds.tot[1][tid] + lds.tot[2][tid] + lds.tot[3][tid];
+      lds.pre[0][tid] += lds.pre[1][tid] + lds.pre[2][tid] + lds.pre[3][tid];
+    }
+    __syncthreads();
+    select_bin(lds.tot[0], (uint32_t)pr.k, s_wsum, s_res);
+    b1 = s_res[0];
+    gt1 = s_res[1];
+    // candidates of earlier chunks and of the row: bins >= b1
+    uint32_t po = 0, pn = 0;
+    if (tid < 256 && (uint32_t)tid >= b1) {
+      po = lds.pre[0][tid];
+      pn = lds.tot[0][tid];
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      po += __shfl_xor(po, d, 64);
+      pn += __shfl_xor(pn, d, 64);
+    }
+    if (lane == 0 && wave < 4) {
+      s_cnt[0][wave] = po;
+      s_cnt[1][wave] = pn;
+    }
+    __syncthreads();
+    my_off = s_cnt[0][0] + s_cnt[0][1] + s_cnt[0][2] + s_cnt[0][3];
+    n_cand = s_cnt[1][0] + s_cnt[1][1] + s_cnt[1][2] + s_cnt[1][3];
+    __syncthreads();
+
+    // ------------------------------------------------------------ C
+    const uint32_t lo_key = b1 << 8;
+    uint64_t m[TOK];
+#pragma unroll
+    for (int j = 0; j < TOK; ++j) {
+      m[j] = __ballot(kv[j] != 0xffffffffu && kv[j] >= lo_key);
+      if (lane == 0) s_cnt[j][wave] = (uint32_t)__popcll(m[j]);
+    }
+    __syncthreads();
+    uint2* crow_out = a.cand + (int64_t)r * a.cand_cap + my_off;
+    uint32_t stage_base = 0;
+#pragma unroll
+    for (int j = 0; j < TOK; ++j) {
+      uint32_t before = 0, all = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const uint32_t v = s_cnt[j][w];
+        before += w < wave ? v : 0u;
+        all += v;
+      }
+      const uint32_t at = my_off + stage_base + before + lanes_below(m[j]);
+      // at < n_cand <= cand_cap by construction; the test keeps a workgroup
+      // that read inconsistent histograms inside the buffer
+      if (kv[j] != 0xffffffffu && kv[j] >= lo_key && at < (uint32_t)a.cand_cap)
+        crow_out[at - my_off] = make_uint2(kv[j], (uint32_t)(t0 + j * kTH + tid));
+      stage_base += all;
+    }
+    wg_row_barrier(a, r, 1);
+  }
+
+  // ---------------------------------------------------------------- F
+  const int L = pr.k + pr.sink + pr.tail_count;
+  const int S = (L + a.WR - 1) / a.WR;
+  const int lo = min(c * S, L), hi = min(L, lo + S);
+  if (select) {
+    const uint2* cl = a.cand + (int64_t)r * a.cand_cap;
+    n_cand = min(n_cand, (uint32_t)a.cand_cap);
+    const uint32_t P = (n_cand + kTH - 1) / kTH;  // candidates per thread, contiguous
+    const uint32_t i0 = tid * P, i1 = min(n_cand, i0 + P);
+    if (tid < 256) s_h2[tid] = 0;
+    __syncthreads();
+    for (uint32_t i = i0; i < i1; ++i) {
+      const uint32_t key = ld_dev2(cl + i).x;
+      if ((key >> 8) == b1) atomicAdd(&s_h2[key & 255u], 1u);
+    }
+    __syncthreads();
+    const uint32_t k2 = (uint32_t)pr.k - gt1;
+    select_bin(s_h2, k2, s_wsum, s_res);
+    const uint32_t tau = (b1 << 8) | s_res[0];
+    const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
+    uint32_t ngt = 0, ntie = 0;
+    for (uint32_t i = i0; i < i1; ++i) {
+      const uint32_t key = ld_dev2(cl + i).x;
+      ngt += key > tau;
+      ntie += key == tau;
+    }
+    uint32_t all_ties, all_sel;
+    const uint32_t tie_rank0 = block_exclusive_scan<kTH>(ntie, s_wsum, &all_ties);
+    const uint32_t take = tie_rank0 >= need ? 0u : min(ntie, need - tie_rank0);
+    uint32_t pos = block_exclusive_scan<kTH>(ngt + take, s_wsum, &all_sel);
+    uint32_t taken = 0;
+    int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols;
+    for (uint32_t i = i0; i < i1; ++i) {
+      const uint2 v = ld_dev2(cl + i);
+      bool sel = v.x > tau;
+      if (v.x == tau && taken < take) {
+        sel = true;
+        ++taken;
+      }
+      if (!sel) continue;
+      const int p = (int)pos++;
+      if (p >= lo && p < hi && p < pr.k) {
+        lds.keep[p - lo] = (int)v.y;
+        if (a.idx_i64) put_idx<int64_t>(a.idx, irow + p, (int)v.y);
+        else put_idx<int32_t>(a.idx, irow + p, (int)v.y);
+      }
+    }
+  }
+  if (a.plans) {  // ragged rows: pad [k, k_cols) with -1, split over the row's workgroups
+    const int pad = a.k_cols - pr.k;
+    const int ps = (pad + a.WR - 1) / a.WR;
+    const int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols + pr.k;
+    for (int i = c * ps + tid; i < min(pad, (c + 1) * ps); i += kTH) {
+      if (a.idx_i64) put_idx<int64_t>(a.idx, irow + i, -1);
+      else put_idx<int32_t>(a.idx, irow + i, -1);
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- A
+  const int h0 = hkv * kG;
+  const uint16_t* kb = a.kc + (int64_t)b * a.k_sb + (int64_t)hkv * a.k_sh;
+  const uint16_t* vb = a.vc + (int64_t)b * a.v_sb + (int64_t)hkv * a.v_sh;
+  WaveState<DT, kG, kDh> ws;
+  {
+    const int rq = lane >> 4, cq = lane & 15;
+    const uint16_t* qp =
+        a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (cq < kG ? cq : 0)) * a.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < kDh / 16; ++ks) {
+      const uint16_t* q4 = qp + rq * (kDh / 4) + 4 * ks;
+      i16x4 fq;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) fq[e] = cq < kG ? (short)q4[e] : (short)0;
+      ws.qf[ks] = fq;
+      ws.acc[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    ws.m = -INFINITY;
+    ws.l = 0.f;
+  }
+  // keep-list position j in [lo, hi) -> cache row (-1 past the row's rows)
+  auto keep_tok = [&](int j) -> int {
+    int64_t t;
+    if (j < pr.k) t = lds.keep[j - lo];
+    else {
+      const int jt = j - pr.k;
+      t = jt < pr.sink ? jt : (int64_t)pr.tail_start + (jt - pr.sink);
+    }
+    return (t < 0 || t >= pr.t_total) ? -1 : (int)t;
+  };
+  const int nsteps = (hi - lo + kKeys - 1) / kKeys;
+  for (int i = wave; i < nsteps; i += kWaves) {
+    const int jpos = lo + i * kKeys + (lane & 15);
+    const int tok = jpos < hi ? keep_tok(jpos) : -1;
+    KvStep<kDh> st;
+    kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane);
+    attn_step<DT, kG, kDh>(ws, st, a.scale_log2, lane);
+  }
+  __syncthreads();  // the keep slice is no longer read; lds.o may follow it
+  {
+    const int rq = lane >> 4, cq = lane & 15;
+    if (lane < kG) {
+      s_m[wave][lane] = ws.m;
+      s_l[wave][lane] = ws.l;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int g = 4 * rq + e;
+      if (g < kG)
+#pragma unroll
+        for (int ch = 0; ch < kDh / 16; ++ch)
+          lds.o[(wave * kG + g) * kDh + cq * (kDh / 16) + ch] = ws.acc[ch][e];
+    }
+  }
+  __syncthreads();
+  float* mypart = a.part + ((int64_t)r * a.WR + c) * kG * (kDh + 2);
+  if (tid < kG * kDh) {
+    const int g = tid / kDh, d = tid - g * kDh;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][g]);
+    float l = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = (M == -INFINITY || s_m[w][g] == -INFINITY) ? 0.f : exp2f(s_m[w][g] - M);
+      l += s_l[w][g] * wt;
+      o += lds.o[(w * kG + g) * kDh + d] * wt;
+    }
+    if (a.WR == 1) {
+      a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
+    } else {
+      float* pp = mypart + g * (kDh + 2);
+      if (d == 0) {
+        pp[0] = M;
+        pp[1] = l;
+      }
+      pp[2 + d] = o;
+    }
+  }
+  if (a.WR == 1) return;
+
+  // ---------------------------------------------------------------- E
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    // blk[0] counts arrivals, blk[1] collects the XCDs the row ran on; the
+    // last arrival checks and clears both
+    uint32_t* blk = a.bar + ((int64_t)r * 3 + 2) * kBarWords;
+    __hip_atomic_fetch_or(blk + 1, 1u << (xcc_id() & 31u), __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // recorded before arriving
+    const uint32_t old =
+        __hip_atomic_fetch_add(blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == (uint32_t)a.WR - 1;
+    if (last) {
+      const uint32_t seen = ld_dev(blk + 1);
+      if (__popc(seen) > 1)
+        __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(blk + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_flag = last ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_flag) return;
+  const float* rp = a.part + (int64_t)r * a.WR * kG * (kDh + 2);
+  float* sw = lds.o;  // [WR][4] split weights, then [4] totals
+  if (tid < kG) {
+    float M = -INFINITY;
+    for (int s = 0; s < a.WR; ++s) M = fmaxf(M, ld_dev(rp + ((int64_t)s * kG + tid) * (kDh + 2)));
+    float l = 0.f;
+    for (int s = 0; s < a.WR; ++s) {
+      const float* pp = rp + ((int64_t)s * kG + tid) * (kDh + 2);
+      const float ms = ld_dev(pp);
+      const float w = (ms == -INFINITY || M == -INFINITY) ? 0.f : exp2f(ms - M);
+      sw[s * kG + tid] = w;
+      l += ld_dev(pp + 1) * w;
+    }
+    sw[a.WR * kG + tid] = l;
+  }
+  __syncthreads();
+  if (tid < kG * kDh) {
+    const int g = tid / kDh, d = tid - g * kDh;
+    float o = 0.f;
+    for (int s = 0; s < a.WR; ++s)
+      o = __builtin_fmaf(ld_dev(rp + ((int64_t)s * kG + g) * (kDh + 2) + 2 + d), sw[s * kG + g], o);
+    const float l = sw[a.WR * kG + g];
+    a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
+  }
+}
+
+inline _Float16 f16_one() { return (_Float16)1.0f; }
+
+// Device facts the fused launch needs: XCDs and CUs per device.
+struct XcdInfo {
+  int nxcc = 0, cu = 0;
+};
+int xcd_info(XcdInfo* out) {
+  static XcdInfo cache[64];
+  int dev = 0;
+  LAP_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) {
+    set_error("device index %d out of range", dev);
+    return LAP_ERR_HIP;
+  }
+  if (cache[dev].nxcc == 0) {
+    int n = 0, cu = 0;
+    LAP_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev), "XCC count");
+    LAP_HIP(hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+    cache[dev].cu = cu;
+    cache[dev].nxcc = n < 1 ? 1 : n;
+  }
+  *out = cache[dev];
+  return LAP_OK;
+}
+
+// Launch shape of the fused step, or false when it does not apply.
+struct FusedPlan {
+  int nxcc, RX, WR, tok, grid;
+};
+bool fused_plan(int R, int T, int keep_max, FusedPlan* p) {
+  static const int mode = [] {
+    const char* e = getenv("LAPRUNE_FUSED");
+    return e ? atoi(e) : 1;
+  }();
+  if (mode == 0) return false;
+  XcdInfo xi;
+  if (xcd_info(&xi) != LAP_OK || xi.cu % xi.nxcc != 0) return false;
+  const int per_xcd = xi.cu / xi.nxcc;
+  const int RX = (R + xi.nxcc - 1) / xi.nxcc;
+  int WR = per_xcd / RX;
+  WR = std::min(WR, std::max(1, (T + kTH - 1) / kTH));
+  if (WR < 1) return false;
+  const int ch = (T + WR - 1) / WR;
+  const int tok = (ch + kTH - 1) / kTH;
+  if (tok < 1 || tok > kMaxTok) return false;
+  if ((keep_max + WR - 1) / WR > kKeepMax) return false;
+  *p = FusedPlan{xi.nxcc, RX, WR, tok, xi.nxcc * RX * WR};
+  return true;
+}
+
+struct StepWs {
+  uint32_t* status;
+  uint32_t* bar;
+  uint32_t* hist;
+  uint2* cand;
+  float* part;
+  size_t bytes;
+};
+// Workspace of the fused step for R rows, WR workgroups each, T columns:
+// status, barrier lines (these two must start zeroed and are left zeroed),
+// histograms, candidates, partials.
+StepWs carve_step(void* base, int R, int WR, int T) {
+  StepWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) {
+    char* q = p ? p + off : nullptr;
+    off = align_up(off + bytes, 256);
+    return q;
+  };
+  w.status = reinterpret_cast<uint32_t*>(take(kStatusBytes));
+  w.bar = reinterpret_cast<uint32_t*>(take((size_t)R * 3 * kBarWords * 4));
+  w.hist = reinterpret_cast<uint32_t*>(take((size_t)R * WR * 256 * 4));
+  w.cand = reinterpret_cast<uint2*>(take((size_t)R * T * 8));
+  w.part = reinterpret_cast<float*>(take((size_t)R * WR * kG * (kDh + 2) * 4));
+  w.bytes = off;
+  return w;
+}
+
+template <int DT>
+void launch_fused_dt(const StepArgs& a, int tok, int grid, hipStream_t st) {
+  switch (tok) {
+#define LAP_STEP(TK)                                                                     \
+  case TK:                                                                               \
+    hipLaunchKernelGGL((step_fused_kernel<DT, TK>), dim3(grid), dim3(kTH), 0, st, a);    \
+    break;
+    LAP_STEP(1) LAP_STEP(2) LAP_STEP(3) LAP_STEP(4) LAP_STEP(5) LAP_STEP(6) LAP_STEP(7)
+    LAP_STEP(8)
+#undef LAP_STEP
+  }
+}
+
+}  // namespace
+
+// Bytes at the start of a lap_decode_step workspace that only the fused
+// kernel uses: the status words and barrier lines (kept zero between calls,
+// whatever path a call takes) and, when the fused kernel applies to this
+// shape, its histograms, candidates and partials.
+size_t decode_step_fused_bytes(int R, int T, int keep_max) {
+  FusedPlan fp;
+  if (!fused_plan(R, T, keep_max, &fp)) return carve_step(nullptr, R, 0, 0).bytes;
+  return carve_step(nullptr, R, fp.WR, T).bytes;
+}
+
+// Run the fused step; LAP_ERR_UNSUPPORTED when this shape must take the
+// kernel chain instead.
+int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, int64_t cs_h,
+                      int64_t cs_t, const void* q, int64_t q_sb, int64_t q_sh, const void* keys,
+                      const void* vals, int dtype, int B, int Hkv, int T_kv, int64_t k_sb,
+                      int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                      int T, int cand_start, int cand_end, int k, int sink, int tail_start,
+                      int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
+                      int max_tail, int key_bf16, float scale, void* out_idx, int idx_dtype,
+                      void* out, void* workspace, size_t ws_bytes, hipStream_t st) {
+  const int R = B * Hkv;
+  const int keep_max = plans ? k_cols + max_sink + max_tail : k + sink + tail_count;
+  FusedPlan fp;
+  if (!fused_plan(R, T, keep_max, &fp)) return LAP_ERR_UNSUPPORTED;
+  if (!score_g4_supported(codes, cs_b, cs_h, cs_t)) return LAP_ERR_UNSUPPORTED;
+  StepWs w = carve_step(workspace, R, fp.WR, T);
+  LAP_CHECK_CODE(workspace && ws_bytes >= w.bytes, LAP_ERR_WORKSPACE,
+                 "lap_decode_step: workspace of %zu bytes needed", w.bytes);
+  StepArgs a{};
+  a.lut = static_cast<const uint16_t*>(lut_gmkg);
+  a.codes = codes;
+  a.cs_b = cs_b; a.cs_h = cs_h; a.cs_t = cs_t;
+  a.B = B; a.Hkv = Hkv; a.T = T;
+  a.plans = reinterpret_cast<const int32_t*>(plans);
+  a.cand_start = cand_start; a.cand_end = cand_end; a.k = k;
+  a.sink = sink; a.tail_start = tail_start; a.tail_count = tail_count;
+  a.k_cols = k_cols; a.max_sink = max_sink; a.max_tail = max_tail;
+  a.key_bf16 = key_bf16;
+  a.q = static_cast<const uint16_t*>(q); a.q_sb = q_sb; a.q_sh = q_sh;
+  a.kc = static_cast<const uint16_t*>(keys); a.vc = static_cast<const uint16_t*>(vals);
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.T_kv = T_kv;
+  a.scale_log2 = scale * kLog2e;
+  a.idx = out_idx;
+  a.idx_i64 = idx_dtype == LAP_DTYPE_I64;
+  a.out = static_cast<uint16_t*>(out);
+  a.status = w.status; a.bar = w.bar; a.hist = w.hist; a.cand = w.cand; a.part = w.part;
+  a.nxcc = fp.nxcc; a.RX = fp.RX; a.WR = fp.WR; a.cand_cap = T; a.keep_cap = kKeepMax;
+  a.one = f16_one();
+  if (dtype == LAP_DTYPE_F16) launch_fused_dt<LAP_DTYPE_F16>(a, fp.tok, fp.grid, st);
+  else launch_fused_dt<LAP_DTYPE_BF16>(a, fp.tok, fp.grid, st);
+  LAP_LAUNCH_CHECK("step_fused_kernel");
+  return LAP_OK;
+}
+
+}  // namespace lap
+
+using namespace lap;
+
+namespace {
+
+// Rows a selection serves per KV row: 4 with LAP_SELECT_PER_HEAD, else 1.
+int step_rows_per_kv(int key_mode) { return (key_mode & LAP_SELECT_PER_HEAD) ? 4 : 1; }
+
+// The chain's part of the workspace (after the fused part): the retrieve
+// workspace, then the attention partials.
+struct ChainWs {
+  size_t ret, attn;
+};
+int chain_ws(int B, int Hq, int Hkv, int T, int D, int keep_max, int key_mode, ChainWs* w) {
+  size_t r = 0, a = 0;
+  int s = lap_retrieve_workspace_size(B * Hkv * step_rows_per_kv(key_mode), T, &r);
+  if (s != LAP_OK) return s;
+  s = lap_attn_decode_workspace_size(B, Hq, D, keep_max, &a);
+  if (s != LAP_OK) return s;
+  w->ret = align_up(r, 256);
+  w->attn = align_up(a, 256);
+  return LAP_OK;
+}
+
+}  // namespace
+
+extern "C" int lap_decode_step_workspace_size(int B, int Hq, int Hkv, int T, int D, int keep_max,
+                                              int key_mode, size_t* bytes) {
+  clear_error();
+  LAP_CHECK(bytes, "lap_decode_step_workspace_size: null output");
+  LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T >= 0 && D > 0 && keep_max >= 0,
+            "lap_decode_step_workspace_size: bad sizes");
+  ChainWs cw;
+  int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
+  if (s != LAP_OK) return s;
+  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max), 256);
+  *bytes = fused + cw.ret + cw.attn;
+  return LAP_OK;
+}
+
+extern "C" int lap_decode_step_status(const void* workspace, size_t workspace_bytes,
+                                      uint32_t* split_rows, uint32_t* timeouts) {
+  clear_error();
+  LAP_CHECK(workspace && split_rows && timeouts, "lap_decode_step_status: null pointer");
+  LAP_CHECK(workspace_bytes >= 8, "lap_decode_step_status: workspace too small");
+  uint32_t h[2] = {0, 0};
+  LAP_HIP(hipMemcpy(h, workspace, sizeof(h), hipMemcpyDeviceToHost), "status copy");
+  *split_rows = h[0];
+  *timeouts = h[1];
+  return LAP_OK;
+}
+
+extern "C" int lap_decode_step(
+    const void* lut_gmkg, const uint8_t* codes, int64_t codes_stride_b, int64_t codes_stride_h,
+    int64_t codes_stride_t, int T, int cand_start, int cand_end, int k, int sink_count,
+    int tail_start, int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
+    int max_tail, int key_mode, const void* q, int64_t q_sb, int64_t q_sh, const void* keys,
+    const void* vals, int dtype, int B, int Hq, int Hkv, int T_kv, int D, int64_t k_sb,
+    int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, float scale,
+    void* out_idx, int idx_dtype, void* out, void* workspace, size_t workspace_bytes,
+    lap_stream_t stream) {
+  clear_error();
+  const char* who = "lap_decode_step";
+  LAP_CHECK(lut_gmkg && q && keys && vals && out, "%s: null pointer", who);
+  LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T > 0 && T_kv > 0 && D > 0, "%s: bad sizes", who);
+  LAP_CHECK(Hq == 4 * Hkv, "%s: the fused scorer serves G = 4 query heads per KV head", who);
+  LAP_CHECK(dtype == LAP_DTYPE_BF16 || dtype == LAP_DTYPE_F16, "%s: q/K/V must be bf16 or fp16",
+            who);
+  LAP_CHECK(idx_dtype == LAP_DTYPE_I32 || idx_dtype == LAP_DTYPE_I64,
+            "%s: idx must be int32 or int64", who);
+  const int km = key_mode & ~LAP_SELECT_PER_HEAD;
+  LAP_CHECK(km == LAP_KEY_F16 || km == LAP_KEY_BF16, "%s: bad key mode", who);
+  LAP_CHECK(!plans || (k_cols >= 0 && max_sink >= 0 && max_tail >= 0), "%s: negative bound",
+            who);
+  int keep_max = 0;
+  int k_eff = 0;
+  if (!plans) {
+    LAP_CHECK(cand_start >= 0 && cand_end <= T && cand_start <= cand_end,
+              "%s: candidate window [%d,%d) outside [0,%d)", who, cand_start, cand_end, T);
+    LAP_CHECK(k >= 0 && sink_count >= 0 && tail_count >= 0, "%s: negative count", who);
+    if (tail_count > 0) LAP_CHECK(tail_start >= 0, "%s: tail_start < 0", who);
+    k_eff = std::min(k, cand_end - cand_start);
+    keep_max = k_eff + sink_count + tail_count;
+  } else {
+    keep_max = k_cols + max_sink + max_tail;
+  }
+  const bool selects = plans ? k_cols > 0 : k_eff > 0;
+  LAP_CHECK(out_idx || !selects, "%s: null index output", who);
+  LAP_CHECK(codes || !selects, "%s: null pointer (codes)", who);
+  ChainWs cw;
+  int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
+  if (s != LAP_OK) return s;
+  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max), 256);
+  LAP_CHECK_CODE(workspace && workspace_bytes >= fused + cw.ret + cw.attn, LAP_ERR_WORKSPACE,
+                 "%s: workspace of %zu bytes needed", who, fused + cw.ret + cw.attn);
+  hipStream_t st = as_stream(stream);
+  if (km == key_mode && D == 128) {
+    s = decode_step_fused(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, q, q_sb,
+                          q_sh, keys, vals, dtype, B, Hkv, T_kv, k_sb, k_sh, k_st, v_sb, v_sh,
+                          v_st, T, cand_start, cand_end, k_eff, sink_count, tail_start,
+                          tail_count, plans, plans ? k_cols : k_eff, max_sink, max_tail,
+                          km == LAP_KEY_BF16, scale, out_idx, idx_dtype, out, workspace, fused,
+                          st);
+    if (s != LAP_ERR_UNSUPPORTED) return s;
+    clear_error();
+  }
+  // the kernel chain: scorer + top-k, then the split-K attention and merge
+  char* base = static_cast<char*>(workspace) + fused;
+  void* ws_r = base;
+  void* ws_a = base + cw.ret;
+  const int H_idx = Hkv * step_rows_per_kv(key_mode);
+  if (!plans) {
+    if (k_eff > 0) {
+      s = lap_retrieve_topk(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
+                            Hkv, T, cand_start, cand_end, k_eff, key_mode, nullptr, out_idx,
+                            idx_dtype, ws_r, cw.ret, stream);
+      if (s != LAP_OK) return s;
+    }
+    return lap_sparse_attn_decode(q, q_sb, q_sh, keys, vals, dtype, B, Hq, Hkv, T_kv, D, k_sb,
+                                  k_sh, k_st, v_sb, v_sh, v_st, out_idx, idx_dtype, H_idx, k_eff,
+                                  sink_count, tail_start, tail_count, scale, out, ws_a, cw.attn,
+                                  stream);
+  }
+  if (k_cols > 0) {
+    s = lap_retrieve_topk_ragged(lut_gmkg, codes, codes_stride_b, codes_stride_h,
+                                 codes_stride_t, B, Hkv, T, plans, k_cols, key_mode, nullptr,
+                                 out_idx, idx_dtype, ws_r, cw.ret, stream);
+    if (s != LAP_OK) return s;
+  }
+  return lap_sparse_attn_decode_ragged(q, q_sb, q_sh, keys, vals, dtype, B, Hq, Hkv, T_kv, D,
+                                       k_sb, k_sh, k_st, v_sb, v_sh, v_st, out_idx, idx_dtype,
+                                       H_idx, k_cols, plans, max_sink, max_tail, scale, out, ws_a,
+                                       cw.attn, stream);
+}

@@ -183,18 +183,18 @@ class SparseDecoder:
         self.H_idx = rows
         self.idx = torch.empty((batch, rows, max(k_cap, 1)), dtype=torch.int32, device=self.dev)
         self.out = torch.empty((batch, num_q_heads, head_dim), dtype=dtype, device=self.dev)
-        ws_r = N.size_query("lap_retrieve_workspace_size", batch * rows, max_tokens)
-        self.ws_sel = torch.empty(max(ws_r, 1), dtype=torch.uint8, device=self.dev)
         # the tail holds the local window, or the newest token alone when
         # there is none (keep_plan)
         self.max_tail = max(self.cfg.local_window, 1)
-        max_keep = k_cap + self.cfg.sink_size + self.max_tail
-        ws_a = N.size_query("lap_attn_decode_workspace_size", batch, num_q_heads, head_dim,
-                            max(max_keep, 1))
-        self.ws_attn = torch.empty(max(ws_a, 1), dtype=torch.uint8, device=self.dev)
+        self.max_keep = k_cap + self.cfg.sink_size + self.max_tail
         self.key_mode = N.KEY_BF16 if self.cfg.score_dtype == torch.bfloat16 else N.KEY_F16
         if self.cfg.select == "head":  # the scorer emits one key row per query head
             self.key_mode |= N.SELECT_PER_HEAD
+        # one workspace for every step: zero-filled once (the one-launch
+        # step's barrier words start at zero and every call leaves them so)
+        ws = N.size_query("lap_decode_step_workspace_size", batch, num_q_heads, num_kv_heads,
+                          max(max_tokens, 1), head_dim, self.max_keep, self.key_mode)
+        self.ws = torch.zeros(max(ws, 1), dtype=torch.uint8, device=self.dev)
         self.last_k = 0
         self._plans = None
         self._plan_key = None
@@ -254,21 +254,35 @@ class SparseDecoder:
         N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
                N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
                N.ptr(self.lut), st)
-        k = p["k"] if t_codes > 0 else 0
-        self.last_k = k
-        H_idx = self.H_idx
-        if k > 0:  # else sink + local only
-            N.call("lap_retrieve_topk", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
-                   codes.stride(1), codes.stride(2), B, Hkv, t_codes, p["cand_start"],
-                   p["cand_end"], k, self.key_mode, None, N.ptr(self.idx), N.I32,
-                   N.ptr(self.ws_sel), self.ws_sel.numel(), st)
-        scale = 1.0 / math.sqrt(D)
-        N.call("lap_sparse_attn_decode", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
-               N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, t_total, D, keys.stride(0),
-               keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
-               N.ptr(self.idx), N.I32, H_idx, k, p["sink"], p["tail_start"], p["tail_count"],
-               scale, N.ptr(self.out), N.ptr(self.ws_attn), self.ws_attn.numel(), st)
+        self.last_k = p["k"]
+        self._decode_step(q, codes, keys, vals, max(t_codes, 1), t_total, p, None, 0, 0, 0, st)
         return self.out.unsqueeze(2)
+
+    def _decode_step(self, q, codes, keys, vals, T, T_kv, p, plans, k_cols, max_sink,
+                     max_tail, st) -> None:
+        """lap_decode_step: scoring, top-k and sparse attention after the LUT
+        (one launch for group selection, the kernel chain otherwise)."""
+        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
+        if p is None:
+            p = dict(cand_start=0, cand_end=0, k=0, sink=0, tail_start=0, tail_count=0)
+        N.call("lap_decode_step", N.ptr(self.lut), N.ptr(codes), codes.stride(0), codes.stride(1),
+               codes.stride(2), T, p["cand_start"], p["cand_end"], p["k"], p["sink"],
+               p["tail_start"], p["tail_count"], N.ptr(plans), k_cols, max_sink, max_tail,
+               self.key_mode, N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys), N.ptr(vals),
+               N.dtype_code(q.dtype), B, Hq, Hkv, T_kv, D, keys.stride(0), keys.stride(1),
+               keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
+               1.0 / math.sqrt(D), N.ptr(self.idx), N.I32, N.ptr(self.out), N.ptr(self.ws),
+               self.ws.numel(), st)
+
+    def fused_status(self) -> tuple[int, int]:
+        """(rows whose workgroups spread over XCDs, barrier time-outs) of
+        the one-launch steps run on this decoder's workspace so far
+        (synchronises); both stay zero on a healthy device."""
+        torch.cuda.synchronize(self.dev)
+        a, b = N.u32(), N.u32()
+        N.call("lap_decode_step_status", N.ptr(self.ws), self.ws.numel(), N.byref(a),
+               N.byref(b))
+        return int(a.value), int(b.value)
 
     def _step_ragged(self, q, codes, keys, vals, t_codes: list[int],
                      t_total: list[int]) -> torch.Tensor:
@@ -294,21 +308,11 @@ class SparseDecoder:
                N.ptr(self.lut), st)
         k_cols = max(p["k"] for p in plans)
         T = max(max(t_codes), 1)
-        H_idx = self.H_idx
-        if k_cols > 0:
-            N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
-                   codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(pdev), k_cols,
-                   self.key_mode, None, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
-                   self.ws_sel.numel(), st)
         self.last_k = k_cols
         max_sink = max(p["sink"] for p in plans)
         max_tail = max(p["tail_count"] for p in plans)
-        N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
-               N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, keys.shape[2], D, keys.stride(0),
-               keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
-               N.ptr(self.idx), N.I32, H_idx, k_cols, N.ptr(pdev), max_sink, max_tail,
-               1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws_attn), self.ws_attn.numel(),
-               st)
+        self._decode_step(q, codes, keys, vals, T, keys.shape[2], None, pdev, k_cols, max_sink,
+                          max_tail, st)
         return self.out.unsqueeze(2)
 
     @property
@@ -337,18 +341,9 @@ class SparseDecoder:
                N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
                N.ptr(self.lut), st)
         k_cols = self.k_cols
-        N.call("lap_retrieve_topk_ragged", N.ptr(self.lut), N.ptr(codes), codes.stride(0),
-               codes.stride(1), codes.stride(2), B, Hkv, T, N.ptr(plans), k_cols,
-               self.key_mode, None, N.ptr(self.idx), N.I32, N.ptr(self.ws_sel),
-               self.ws_sel.numel(), st)
-        H_idx = self.H_idx
         self.last_k = k_cols
-        N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
-               N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, keys.shape[2], D, keys.stride(0),
-               keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
-               N.ptr(self.idx), N.I32, H_idx, k_cols, N.ptr(plans), self.cfg.sink_size,
-               self.max_tail, 1.0 / math.sqrt(D), N.ptr(self.out),
-               N.ptr(self.ws_attn), self.ws_attn.numel(), st)
+        self._decode_step(q, codes, keys, vals, T, keys.shape[2], None, plans, k_cols,
+                          self.cfg.sink_size, self.max_tail, st)
         return self.out.unsqueeze(2)
 
     @torch.no_grad()

@@ -38,7 +38,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.lap_abi_version() == 6
+    assert lib.lap_abi_version() == 7
 
 
 def _err(lib):
@@ -131,3 +131,31 @@ def test_cpu_tensors_are_rejected_loudly():
                                     torch.zeros(1, 10, 32, dtype=torch.uint8), 4)
     with pytest.raises(RuntimeError):
         _impl.aq_lut_build(torch.zeros(4, 128), torch.zeros(32, 256, 128))
+
+
+def test_decode_step_argument_checks(lib):
+    """lap_decode_step validates before touching the device: null inputs,
+    a group size other than 4, and a missing workspace."""
+    from laprune_amd import _native as N
+    one = C.c_void_p(4096)  # never dereferenced
+    args = dict(lut=one, codes=one, T=1024, cs=4, ce=960, k=64, sink=4, ts=960, tc=64, key=N.KEY_BF16,
+                q=one, Hq=32, Hkv=8, ws=None, ws_n=0)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.lap_decode_step(a["lut"], a["codes"], 8 * 1024 * 32, 1024 * 32, 32, a["T"],
+                                   a["cs"], a["ce"], a["k"], a["sink"], a["ts"], a["tc"], None, 0,
+                                   0, 0, a["key"], a["q"], 32 * 128, 128, one, one, N.BF16, 1,
+                                   a["Hq"], a["Hkv"], 1024, 128, 8 * 1024 * 128, 1024 * 128, 128,
+                                   8 * 1024 * 128, 1024 * 128, 128, C.c_float(0.088), one, N.I32,
+                                   one, a["ws"], a["ws_n"], None)
+
+    assert call(lut=None) == N.LAP_ERR_INVALID and "null pointer" in _err(lib)
+    assert call(Hq=16) == N.LAP_ERR_INVALID and "G = 4" in _err(lib)
+    assert call(ce=2000) == N.LAP_ERR_INVALID and "candidate window" in _err(lib)
+    assert call(key=7) == N.LAP_ERR_INVALID and "key mode" in _err(lib)
+    assert call() == N.LAP_ERR_WORKSPACE and "workspace of" in _err(lib)
+    need = C.c_size_t(0)
+    assert lib.lap_decode_step_workspace_size(1, 32, 8, 1024, 128, 132, N.KEY_BF16,
+                                              C.byref(need)) == N.LAP_OK
+    assert need.value > 0
