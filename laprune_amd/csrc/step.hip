@@ -17,7 +17,7 @@
 // workgroup of each row checks, from the XCC_ID registers its row's
 // workgroups recorded, that they did share one XCD, and counts any row that
 // did not in the status word.  The workgroups of a row share one L2, and the data they pass
-// each other (histograms, candidates, attention partials) never leaves it:
+// each other (histograms, level-2 tables, attention partials) never leaves it:
 // a producer's plain stores are complete in L2 once its vmcnt drains, and a
 // consumer reads them with device-scope loads, which miss the L1 (where a
 // stale copy could sit) and hit the shared L2.  No cache write-back or
@@ -26,26 +26,26 @@
 //
 // Phases of the workgroup owning chunk c of row r (TOK * 1024 tokens):
 //   S  score its tokens (the scorer's pipeline, score_core.h): selection keys
-//      stay in registers, the level-1 histogram of the key high bytes over
-//      the candidate window goes to the row's histogram array;
+//      stay in registers, and the level-1 histogram of the keys' top ten
+//      bits over the candidate window is added to the row's histogram (L2
+//      atomics);
 //   B1 row barrier;
-//   H  sum the row's chunk histograms: the threshold bin b1, the number of
-//      keys above it, and this chunk's offset among the row's candidates
-//      (keys in bins >= b1);
-//   C  write the chunk's candidates (key, column) in column order;
+//   H  the row's threshold bin b1 and the count above it; the chunk
+//      publishes its own count above b1 and the level-2 histogram (low six
+//      bits) of its keys in b1;
 //   B2 row barrier;
-//   F  every workgroup of the row reads the row's candidate list and runs
-//      the rest of the radix select on it (level 2 on the low bytes of bin
-//      b1, then the ordered selection: keys above tau, then the `need`
-//      lowest-column ties), so each knows the whole selection without a
-//      third barrier; it keeps the slice of the keep list (selection ++ sink
-//      ++ local tail) it attends to and writes that slice's indices;
-//   A  attention of the group's four query heads over the slice (the MFMA
-//      wave step of attn_core.h), one (m, l, o) partial per head;
+//   H2 the row's level-2 tables give the threshold tau, the ties at tau to
+//      take (lowest columns first) and where this chunk's selection starts;
+//      the chunk compacts its own selection in column order, writes those
+//      indices and keeps them in LDS;
+//   A  attention of the group's four query heads over its selection and its
+//      share of the sink and local tail (the MFMA wave step of attn_core.h),
+//      one (m, l, o) partial per head;
 //   E  the last workgroup of the row to arrive merges the partials and
 //      writes the output.
 // Selection results equal the two-level top-k of topk.hip bit for bit: the
-// same keys, threshold and tie rule.
+// same keys, threshold and tie rule (the radix split is 10 + 6 bits here,
+// 8 + 8 there).
 //
 // Barriers spin a bounded number of polls; a spin that gives up counts a
 // time-out in the status word and lets the kernel finish (results of that
@@ -69,10 +69,11 @@ constexpr int kWaves = kTH / 64;
 constexpr int kMaxTok = 8;          // tokens per thread (chunk = TOK * 1024)
 constexpr int kHC = 4;              // level-1 histogram copies
 constexpr int kDh = 128;            // head dim of the fused path
-constexpr int kKeepMax = 8192;      // keep-list slice per workgroup (32 KiB of LDS)
+constexpr int kKeepMax = 8192;      // a workgroup's own selection (32 KiB of LDS)
 constexpr int kSpin = 1 << 21;      // polls before a barrier gives up
 constexpr int kBarWords = 16;       // one 64-byte line per barrier
 constexpr int kStatusBytes = 256;
+constexpr int kMaxWR = 32;          // workgroups per row (one per CU of an XCD)
 
 struct StepArgs {
   const uint16_t* lut;   // [R][M][K][4] fp16 (GMKG)
@@ -96,10 +97,10 @@ struct StepArgs {
   uint16_t* out;         // [B][Hkv * 4][128]
   uint32_t* status;      // [0] rows spread over XCDs, [1] barrier time-outs
   uint32_t* bar;         // [R][3][kBarWords]
-  uint32_t* hist;        // [R][WR][256]
-  uint2* cand;           // [R][cand_cap] (key, column)
+  uint32_t* hist;        // [R][1024] level-1 counts of the row (zero between calls)
+  uint32_t* t2;          // [R][WR][kT2] per chunk: level-2 counts, keys above b1
   float* part;           // [R][WR][4][kDh + 2] (m, l, o)
-  int nxcc, RX, WR, cand_cap, keep_cap;
+  int nxcc, RX, WR;
   _Float16 one;
 };
 
@@ -140,24 +141,33 @@ __device__ __forceinline__ uint2 ld_dev2(const uint2* p) {
   return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
 }
 
-// Sense-reversing barrier of the n workgroups of one row, run by one thread
-// of each after its workgroup's stores have drained.  blk[0] counts
-// arrivals and returns to zero; blk[1] is the generation the last arrival
-// advances.
+// Arrival on a row counter: blk holds a 64-bit count that only grows and
+// that every call advances by exactly kMaxWR (the call's n <= kMaxWR
+// arrivals, then kMaxWR - n added by the last), so calls with different n
+// can share it and nothing is reset.  Returns the count that ends this call
+// and whether this arrival was the call's last.
+__device__ __forceinline__ uint64_t row_arrive(uint32_t* blk, int n, bool* last) {
+  uint64_t* cnt = reinterpret_cast<uint64_t*>(blk);
+  const uint64_t old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t pos = old % (uint64_t)kMaxWR;
+  *last = pos == (uint64_t)n - 1;
+  if (*last && n < kMaxWR)
+    __hip_atomic_fetch_add(cnt, (uint64_t)(kMaxWR - n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return old - pos + (uint64_t)kMaxWR;
+}
+
+// Barrier of the n workgroups of one row, run by one thread of each after
+// its workgroup's stores have drained: arrive, then poll the count (one
+// device-scope atomic and polls of the same line; no second word for the
+// last arrival to publish).
 __device__ void row_barrier(uint32_t* blk, int n, uint32_t* status) {
-  uint32_t* cnt = blk;
-  uint32_t* gen = blk + 1;
-  const uint32_t g0 = ld_dev(gen);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the generation is read before arriving
-  const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (old == (uint32_t)n - 1) {
-    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
+  bool last;
+  const uint64_t target = row_arrive(blk, n, &last);
+  if (last) return;
+  const uint64_t* cnt = reinterpret_cast<const uint64_t*>(blk);
   for (int s = 0; s < kSpin; ++s) {
-    if (ld_dev(gen) != g0) return;
-    __builtin_amdgcn_s_sleep(2);
+    if (ld_dev(cnt) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
   }
   __hip_atomic_fetch_add(status + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -170,6 +180,13 @@ __device__ __forceinline__ void wg_row_barrier(const StepArgs& a, int r, int whi
   __syncthreads();
 }
 
+// Record the XCD this workgroup runs on in its row's mask (word 2 of the
+// merge counter's line), which the row's last merge arrival checks.
+__device__ __forceinline__ void record_xcd(const StepArgs& a, int r) {
+  __hip_atomic_fetch_or(a.bar + ((int64_t)r * 3 + 2) * kBarWords + 2, 1u << (xcc_id() & 31u),
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ uint32_t key_of_score(float e, int key_bf16) {
   const uint16_t h = f2h(e);
   return key_bf16 ? bf16_key_of_f16(h) : f16_key(h);
@@ -180,12 +197,50 @@ __device__ __forceinline__ void put_idx(void* idx, int64_t i, int v) {
   static_cast<IT*>(idx)[i] = (IT)v;
 }
 
+// Radix split of the 16-bit selection keys: level 1 on bits 15..6 (1024
+// bins, one per thread of the workgroup), level 2 on bits 5..0, so the
+// level-2 table every chunk publishes is 64 counts and reading all of a
+// row's tables after B2 is a few loads per thread.
+constexpr int kL1 = 1024, kLoBits = 6, kL2 = 1 << kLoBits;
+constexpr int kH1Pitch = kL1 + 1;  // copies of one bin in different banks
+constexpr int kT2 = kL2 + 4;       // per-chunk table: level-2 counts, keys above b1
+constexpr uint32_t kNoKey = 0xffffffffu;  // a thread's token outside the window
+
+// The unique bin b of h[0..1023] with S(b) >= target > S(b+1), S(i) =
+// sum_{j >= i} h[j]: s_res = {b, S(b+1)}.  1024 threads, one bin each;
+// 1 <= target <= S(0).
+__device__ __forceinline__ void select_bin1024(const uint32_t* h, uint32_t target,
+                                               uint32_t* s_wsum, uint32_t* s_res) {
+  const int tid = threadIdx.x;
+  const uint32_t x = h[kL1 - 1 - tid];
+  uint32_t total;
+  const uint32_t above = block_exclusive_scan<kTH>(x, s_wsum, &total);
+  if (above + x >= target && above < target) {
+    s_res[0] = kL1 - 1 - tid;
+    s_res[1] = above;
+  }
+  __syncthreads();
+}
+// The same over 64 bins, by wave 0 (every thread synchronises).
+__device__ __forceinline__ void select_bin64(const uint32_t* h, uint32_t target,
+                                             uint32_t* s_res) {
+  if (threadIdx.x < kL2) {
+    const int l = threadIdx.x;
+    const uint32_t x = h[kL2 - 1 - l];
+    const uint32_t inc = wave_inclusive_scan(x);
+    if (inc >= target && inc - x < target) {
+      s_res[0] = kL2 - 1 - l;
+      s_res[1] = inc - x;
+    }
+  }
+  __syncthreads();
+}
+
 // LDS carve of the 64 KiB region that holds the table during S.
 struct Lds {
   uint4* lut;                // S: [kLutBytes / 16]
-  uint32_t (*tot)[256];      // H: [4][256]
-  uint32_t (*pre)[256];      // H: [4][256]
-  int* keep;                 // F, A: [kKeepMax]
+  uint32_t* tot;             // H: [kL1]
+  int* keep;                 // H2, A: [kKeepMax]
   float* o;                  // A: [kWaves][4][kDh]
 };
 
@@ -193,16 +248,17 @@ template <int DT, int TOK>
 __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   static_assert(TOK >= 1 && TOK <= kMaxTok, "TOK");
   static_assert(kKeepMax * 4 + kWaves * 4 * kDh * 4 <= kLutBytes, "LDS carve");
+  static_assert(kMaxWR * 4 * 3 + 4 + kTH <= kWaves * 4 * kDh && kG * kDh * 2 == kTH, "E carve");
   __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
-  __shared__ uint32_t s_hist[kHC * kHPitch];
-  __shared__ uint32_t s_h2[256], s_wsum[kWaves], s_res[4], s_cnt[kMaxTok][kWaves];
-  __shared__ uint32_t s_red[kWaves], s_flag;
+  __shared__ uint32_t s_hist[kHC * kH1Pitch];
+  __shared__ uint32_t s_h2[kL2], s_wsum[kWaves], s_res[4], s_cnt[kMaxTok][kWaves];
+  __shared__ uint32_t s_cnt2[kMaxTok][kWaves];
+  __shared__ uint32_t s_flag;
   __shared__ float s_m[kWaves][4], s_l[kWaves][4];
 
   Lds lds;
   lds.lut = s_big;
-  lds.tot = reinterpret_cast<uint32_t(*)[256]>(s_big);
-  lds.pre = reinterpret_cast<uint32_t(*)[256]>(reinterpret_cast<uint32_t*>(s_big) + 4 * 256);
+  lds.tot = reinterpret_cast<uint32_t*>(s_big);
   lds.keep = reinterpret_cast<int*>(s_big);
   lds.o = reinterpret_cast<float*>(s_big) + kKeepMax;
 
@@ -217,12 +273,26 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   constexpr int CH = TOK * kTH;
   const int t0 = c * CH, t1 = min(pr.t_end, t0 + CH);
   const bool select = pr.k > 0;
+  const int h0 = hkv * kG;
+  // The query fragments of the attention phase (A-operand layout of
+  // attn_core.h), requested now so that their latency hides behind S.
+  i16x4 qpre[kDh / 16];
+  {
+    const int rq = lane >> 4, cq = lane & 15;
+    const uint16_t* qp =
+        a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (cq < kG ? cq : 0)) * a.q_sh + rq * (kDh / 4);
+#pragma unroll
+    for (int ks = 0; ks < kDh / 16; ++ks) {
+      const uint2 w = *reinterpret_cast<const uint2*>(qp + 4 * ks);  // 8-byte aligned (host check)
+      qpre[ks] = cq < kG ? __builtin_bit_cast(i16x4, w) : i16x4{0, 0, 0, 0};
+    }
+  }
 
   // ---------------------------------------------------------------- S
   uint32_t kv[TOK];
 #pragma unroll
-  for (int j = 0; j < TOK; ++j) kv[j] = 0xffffffffu;  // no key
-  for (int i = tid; i < kHC * kHPitch; i += kTH) s_hist[i] = 0;
+  for (int j = 0; j < TOK; ++j) kv[j] = kNoKey;
+  for (int i = tid; i < kHC * kH1Pitch; i += kTH) s_hist[i] = 0;
   if (select && t0 < t1) {
     constexpr int kFill = kLutBytes / 16 / kTH;
     const uint4* src = reinterpret_cast<const uint4*>(a.lut + (int64_t)r * (kG * kM * kK));
@@ -245,7 +315,7 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     }
     lds_barrier();
     const char* tab = reinterpret_cast<const char*>(lds.lut);
-    const int copy = (int)(__lane_id() % kHC) * kHPitch;
+    const int copy = (int)(__lane_id() % kHC) * kH1Pitch;
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
       vm_wait(0, cc[j][0], cc[j][1]);
@@ -256,138 +326,192 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       if (t < t1 && t >= pr.cs && t < pr.ce) {
         const uint32_t key = key_of_score(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)), a.key_bf16);
         kv[j] = key;
-        atomicAdd(&s_hist[copy + (key >> 8)], 1u);
+        atomicAdd(&s_hist[copy + (key >> kLoBits)], 1u);
       }
     }
   }
   __syncthreads();
-  if (select && tid < 256) {
-    uint32_t v = 0;
+  // This chunk's level-1 count of bin tid (the sum of the copies), added to
+  // the row's histogram.
+  uint32_t h1 = 0;
+  if (select) {
 #pragma unroll
-    for (int cp = 0; cp < kHC; ++cp) v += s_hist[cp * kHPitch + tid];
-    a.hist[((int64_t)r * a.WR + c) * 256 + tid] = v;
+    for (int cp = 0; cp < kHC; ++cp) h1 += s_hist[cp * kH1Pitch + tid];
+    if (h1)
+      __hip_atomic_fetch_add(a.hist + (int64_t)r * kL1 + tid, h1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---------------------------------------------------------------- B1, H
-  uint32_t b1 = 0, gt1 = 0, n_cand = 0, my_off = 0;
+  // After B1 the row's level-1 histogram is whole: the threshold bin b1 and
+  // the keys above it.  Each chunk then publishes, for its own keys, the
+  // count above b1 and the level-2 histogram of its keys in b1.
+  uint32_t tau = 0, take = 0, base = 0, n_sel = 0;
   if (select) {
+    if (tid == 0) record_xcd(a, r);  // complete before B2's arrival
     wg_row_barrier(a, r, 0);
-    const int bin = tid & 255, part = tid >> 8;
-    uint32_t tot = 0, pre = 0;
-    const uint32_t* hr = a.hist + (int64_t)r * a.WR * 256 + bin;
-    for (int cc2 = part; cc2 < a.WR; cc2 += 4) {
-      const uint32_t v = ld_dev(hr + (int64_t)cc2 * 256);
-      tot += v;
-      pre += cc2 < c ? v : 0u;
-    }
-    lds.tot[part][bin] = tot;
-    lds.pre[part][bin] = pre;
+    lds.tot[tid] = ld_dev(a.hist + (int64_t)r * kL1 + tid);
+    if (tid < kL2) s_h2[tid] = 0;
     __syncthreads();
-    if (tid < 256) {
-      lds.tot[0][tid] += lds.tot[1][tid] + lds.tot[2][tid] + lds.tot[3][tid];
-      lds.pre[0][tid] += lds.pre[1][tid] + lds.pre[2][tid] + lds.pre[3][tid];
-    }
-    __syncthreads();
-    select_bin(lds.tot[0], (uint32_t)pr.k, s_wsum, s_res);
-    b1 = s_res[0];
-    gt1 = s_res[1];
-    // candidates of earlier chunks and of the row: bins >= b1
-    uint32_t po = 0, pn = 0;
-    if (tid < 256 && (uint32_t)tid >= b1) {
-      po = lds.pre[0][tid];
-      pn = lds.tot[0][tid];
-    }
+    select_bin1024(lds.tot, (uint32_t)pr.k, s_wsum, s_res);
+    const uint32_t b1 = s_res[0], gt1 = s_res[1];
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-      po += __shfl_xor(po, d, 64);
-      pn += __shfl_xor(pn, d, 64);
-    }
-    if (lane == 0 && wave < 4) {
-      s_cnt[0][wave] = po;
-      s_cnt[1][wave] = pn;
-    }
+    for (int j = 0; j < TOK; ++j)
+      if (kv[j] != kNoKey && (kv[j] >> kLoBits) == b1) atomicAdd(&s_h2[kv[j] & (kL2 - 1)], 1u);
+    uint32_t gt = (uint32_t)tid > b1 ? h1 : 0u;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) gt += __shfl_xor(gt, d, 64);
+    if (lane == 0) s_cnt[0][wave] = gt;
     __syncthreads();
-    my_off = s_cnt[0][0] + s_cnt[0][1] + s_cnt[0][2] + s_cnt[0][3];
-    n_cand = s_cnt[1][0] + s_cnt[1][1] + s_cnt[1][2] + s_cnt[1][3];
-    __syncthreads();
+    uint32_t* t2 = a.t2 + ((int64_t)r * a.WR + c) * kT2;
+    if (tid < kL2) t2[tid] = s_h2[tid];
+    if (tid == kL2) {
+      uint32_t my_gt1 = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) my_gt1 += s_cnt[0][w];
+      t2[kL2] = my_gt1;
+    }
+    wg_row_barrier(a, r, 1);
+    // Every chunk has read the row histogram: clear it for the next call.
+    if (c == 0) a.hist[(int64_t)r * kL1 + tid] = 0u;
 
-    // ------------------------------------------------------------ C
-    const uint32_t lo_key = b1 << 8;
-    uint64_t m[TOK];
+    // ------------------------------------------------------------ H2
+    // The row's level-2 tables: the threshold tau = (b1, b2), the ties at
+    // tau to take, and where this chunk's selection starts in the row's.
+    // Thread (chunk cc = tid / 32, q = tid % 32) holds bins 2q, 2q + 1 of
+    // chunk cc's table (and, for q = 0, its count above b1).
+    uint32_t* st2 = reinterpret_cast<uint32_t*>(lds.o);  // [kMaxWR][kL2] level-2 counts
+    uint32_t* s_cgt = st2 + kMaxWR * kL2;                // [kMaxWR] keys above tau per chunk
+    uint32_t* s_cti = s_cgt + kMaxWR;                    // [kMaxWR] ties at tau per chunk
+    const int cc = tid >> 5, qq = tid & 31;
+    const bool cin = cc < a.WR;
+    uint32_t v0, v1, v2;
+    {
+      const uint32_t* src2 = a.t2 + ((int64_t)r * a.WR + min(cc, a.WR - 1)) * kT2;
+      v0 = ld_dev(src2 + 2 * qq);
+      v1 = ld_dev(src2 + 2 * qq + 1);
+      v2 = qq == 0 ? ld_dev(src2 + kL2) : 0u;
+      if (!cin) v0 = v1 = v2 = 0u;
+      st2[cc * kL2 + 2 * qq] = v0;
+      st2[cc * kL2 + 2 * qq + 1] = v1;
+    }
+    __syncthreads();
+    if (tid < kL2) {
+      uint32_t t = 0;
+      for (int c2 = 0; c2 < a.WR; ++c2) t += st2[c2 * kL2 + tid];
+      s_h2[tid] = t;
+    }
+    __syncthreads();
+    const uint32_t k2 = (uint32_t)pr.k - gt1;
+    select_bin64(s_h2, k2, s_res);
+    const uint32_t b2 = s_res[0];
+    tau = (b1 << kLoBits) | b2;
+    const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
+    {
+      // per chunk: keys above tau (above b1, or in b1 with low bits above
+      // b2) and ties at tau, summed over the chunk's 32 threads
+      uint32_t g = v2 + ((uint32_t)(2 * qq) > b2 ? v0 : 0u) + ((uint32_t)(2 * qq + 1) > b2 ? v1 : 0u);
+      uint32_t ti = (uint32_t)(2 * qq) == b2 ? v0 : ((uint32_t)(2 * qq + 1) == b2 ? v1 : 0u);
+#pragma unroll
+      for (int d = 16; d >= 1; d >>= 1) {
+        g += __shfl_xor(g, d, 64);
+        ti += __shfl_xor(ti, d, 64);
+      }
+      if (qq == 0) {
+        s_cgt[cc] = g;
+        s_cti[cc] = ti;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const uint32_t g = lane < c ? s_cgt[lane] : 0u, ti = lane < c ? s_cti[lane] : 0u;
+      uint32_t gs = g, ts = ti;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        gs += __shfl_xor(gs, d, 64);
+        ts += __shfl_xor(ts, d, 64);
+      }
+      if (lane == 0) {
+        const uint32_t my_ties = s_cti[c];
+        const uint32_t tk = ts >= need ? 0u : min(my_ties, need - ts);
+        // ties taken by the earlier chunks, min(need, ts), from an explicit
+        // instruction: hipcc 7.2 at -O3 folds this min (written as min() or
+        // as a select) to ts here, which is wrong once the row's ties run out
+        uint32_t taken_before;
+        asm volatile("v_min_u32 %0, %1, %2" : "=v"(taken_before) : "v"(need), "v"(ts));
+        s_res[2] = tk;
+        s_res[3] = gs + taken_before;
+        s_res[1] = my_ties;
+        s_flag = s_cgt[c] + tk;
+      }
+    }
+    __syncthreads();
+    take = s_res[2];
+    base = s_res[3];
+    n_sel = s_flag;
+    const uint32_t my_ties = s_res[1];
+
+    // Ordered compaction of this chunk's selection (column order: stage j,
+    // then thread): keys above tau, and its first `take` ties at tau.  Only
+    // the chunk where the row's ties run out takes some of its ties and
+    // needs their ranks.
+    bool sel[TOK];
+    if (take == 0 || take >= my_ties) {
+      const bool all_ties = take > 0;
+#pragma unroll
+      for (int j = 0; j < TOK; ++j)
+        sel[j] = kv[j] != kNoKey && (kv[j] > tau || (all_ties && kv[j] == tau));
+    } else {
+      uint64_t mt[TOK];
+#pragma unroll
+      for (int j = 0; j < TOK; ++j) {
+        mt[j] = __ballot(kv[j] != kNoKey && kv[j] == tau);
+        if (lane == 0) s_cnt[j][wave] = (uint32_t)__popcll(mt[j]);
+      }
+      __syncthreads();
+      uint32_t tie_base = 0;
+#pragma unroll
+      for (int j = 0; j < TOK; ++j) {
+        uint32_t before = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const uint32_t v = s_cnt[j][w];
+          before += w < wave ? v : 0u;
+          all += v;
+        }
+        const uint32_t rank = tie_base + before + lanes_below(mt[j]);
+        sel[j] = kv[j] != kNoKey && (kv[j] > tau || (kv[j] == tau && rank < take));
+        tie_base += all;
+      }
+    }
+    uint64_t ms[TOK];
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
-      m[j] = __ballot(kv[j] != 0xffffffffu && kv[j] >= lo_key);
-      if (lane == 0) s_cnt[j][wave] = (uint32_t)__popcll(m[j]);
+      ms[j] = __ballot(sel[j]);
+      if (lane == 0) s_cnt2[j][wave] = (uint32_t)__popcll(ms[j]);
     }
     __syncthreads();
-    uint2* crow_out = a.cand + (int64_t)r * a.cand_cap + my_off;
-    uint32_t stage_base = 0;
+    const int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols;
+    uint32_t sel_base = 0;
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
       uint32_t before = 0, all = 0;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
-        const uint32_t v = s_cnt[j][w];
+        const uint32_t v = s_cnt2[j][w];
         before += w < wave ? v : 0u;
         all += v;
       }
-      const uint32_t at = my_off + stage_base + before + lanes_below(m[j]);
-      // at < n_cand <= cand_cap by construction; the test keeps a workgroup
-      // that read inconsistent histograms inside the buffer
-      if (kv[j] != 0xffffffffu && kv[j] >= lo_key && at < (uint32_t)a.cand_cap)
-        crow_out[at - my_off] = make_uint2(kv[j], (uint32_t)(t0 + j * kTH + tid));
-      stage_base += all;
-    }
-    wg_row_barrier(a, r, 1);
-  }
-
-  // ---------------------------------------------------------------- F
-  const int L = pr.k + pr.sink + pr.tail_count;
-  const int S = (L + a.WR - 1) / a.WR;
-  const int lo = min(c * S, L), hi = min(L, lo + S);
-  if (select) {
-    const uint2* cl = a.cand + (int64_t)r * a.cand_cap;
-    n_cand = min(n_cand, (uint32_t)a.cand_cap);
-    const uint32_t P = (n_cand + kTH - 1) / kTH;  // candidates per thread, contiguous
-    const uint32_t i0 = tid * P, i1 = min(n_cand, i0 + P);
-    if (tid < 256) s_h2[tid] = 0;
-    __syncthreads();
-    for (uint32_t i = i0; i < i1; ++i) {
-      const uint32_t key = ld_dev2(cl + i).x;
-      if ((key >> 8) == b1) atomicAdd(&s_h2[key & 255u], 1u);
-    }
-    __syncthreads();
-    const uint32_t k2 = (uint32_t)pr.k - gt1;
-    select_bin(s_h2, k2, s_wsum, s_res);
-    const uint32_t tau = (b1 << 8) | s_res[0];
-    const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
-    uint32_t ngt = 0, ntie = 0;
-    for (uint32_t i = i0; i < i1; ++i) {
-      const uint32_t key = ld_dev2(cl + i).x;
-      ngt += key > tau;
-      ntie += key == tau;
-    }
-    uint32_t all_ties, all_sel;
-    const uint32_t tie_rank0 = block_exclusive_scan<kTH>(ntie, s_wsum, &all_ties);
-    const uint32_t take = tie_rank0 >= need ? 0u : min(ntie, need - tie_rank0);
-    uint32_t pos = block_exclusive_scan<kTH>(ngt + take, s_wsum, &all_sel);
-    uint32_t taken = 0;
-    int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols;
-    for (uint32_t i = i0; i < i1; ++i) {
-      const uint2 v = ld_dev2(cl + i);
-      bool sel = v.x > tau;
-      if (v.x == tau && taken < take) {
-        sel = true;
-        ++taken;
+      const uint32_t q = sel_base + before + lanes_below(ms[j]);
+      if (sel[j] && q < (uint32_t)kKeepMax && base + q < (uint32_t)pr.k) {
+        const int col = t0 + j * kTH + tid;
+        lds.keep[q] = col;
+        if (a.idx_i64) put_idx<int64_t>(a.idx, irow + base + q, col);
+        else put_idx<int32_t>(a.idx, irow + base + q, col);
       }
-      if (!sel) continue;
-      const int p = (int)pos++;
-      if (p >= lo && p < hi && p < pr.k) {
-        lds.keep[p - lo] = (int)v.y;
-        if (a.idx_i64) put_idx<int64_t>(a.idx, irow + p, (int)v.y);
-        else put_idx<int32_t>(a.idx, irow + p, (int)v.y);
-      }
+      sel_base += all;
     }
+    n_sel = min(n_sel, (uint32_t)kKeepMax);
   }
   if (a.plans) {  // ragged rows: pad [k, k_cols) with -1, split over the row's workgroups
     const int pad = a.k_cols - pr.k;
@@ -398,48 +522,43 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       else put_idx<int32_t>(a.idx, irow + i, -1);
     }
   }
-  __syncthreads();
+  lds_barrier();  // the keep list; the index stores may still be in flight
 
   // ---------------------------------------------------------------- A
-  const int h0 = hkv * kG;
+  // This workgroup attends over its own selection and every WR-th entry
+  // (from c) of the row's sink ++ local tail.
   const uint16_t* kb = a.kc + (int64_t)b * a.k_sb + (int64_t)hkv * a.k_sh;
   const uint16_t* vb = a.vc + (int64_t)b * a.v_sb + (int64_t)hkv * a.v_sh;
   WaveState<DT, kG, kDh> ws;
-  {
-    const int rq = lane >> 4, cq = lane & 15;
-    const uint16_t* qp =
-        a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (cq < kG ? cq : 0)) * a.q_sh;
 #pragma unroll
-    for (int ks = 0; ks < kDh / 16; ++ks) {
-      const uint16_t* q4 = qp + rq * (kDh / 4) + 4 * ks;
-      i16x4 fq;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) fq[e] = cq < kG ? (short)q4[e] : (short)0;
-      ws.qf[ks] = fq;
-      ws.acc[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    ws.m = -INFINITY;
-    ws.l = 0.f;
+  for (int ks = 0; ks < kDh / 16; ++ks) {
+    ws.qf[ks] = qpre[ks];
+    ws.acc[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // keep-list position j in [lo, hi) -> cache row (-1 past the row's rows)
-  auto keep_tok = [&](int j) -> int {
+  ws.m = -INFINITY;
+  ws.l = 0.f;
+  const int n_fix = pr.sink + pr.tail_count;
+  const int n_st = n_fix > c ? (n_fix - c + a.WR - 1) / a.WR : 0;
+  const int n_loc = (int)n_sel + n_st;
+  // local keep position p -> cache row (-1 past the row's rows)
+  auto keep_tok = [&](int p) -> int {
     int64_t t;
-    if (j < pr.k) t = lds.keep[j - lo];
+    if (p < (int)n_sel) t = lds.keep[p];
     else {
-      const int jt = j - pr.k;
+      const int jt = c + (p - (int)n_sel) * a.WR;
       t = jt < pr.sink ? jt : (int64_t)pr.tail_start + (jt - pr.sink);
     }
     return (t < 0 || t >= pr.t_total) ? -1 : (int)t;
   };
-  const int nsteps = (hi - lo + kKeys - 1) / kKeys;
+  const int nsteps = (n_loc + kKeys - 1) / kKeys;
   for (int i = wave; i < nsteps; i += kWaves) {
-    const int jpos = lo + i * kKeys + (lane & 15);
-    const int tok = jpos < hi ? keep_tok(jpos) : -1;
+    const int p = i * kKeys + (lane & 15);
+    const int tok = p < n_loc ? keep_tok(p) : -1;
     KvStep<kDh> st;
     kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane);
     attn_step<DT, kG, kDh>(ws, st, a.scale_log2, lane);
   }
-  __syncthreads();  // the keep slice is no longer read; lds.o may follow it
+  lds_barrier();  // the keep list is no longer read; lds.o may follow it
   {
     const int rq = lane >> 4, cq = lane & 15;
     if (lane < kG) {
@@ -455,7 +574,7 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
           lds.o[(wave * kG + g) * kDh + cq * (kDh / 16) + ch] = ws.acc[ch][e];
     }
   }
-  __syncthreads();
+  lds_barrier();
   float* mypart = a.part + ((int64_t)r * a.WR + c) * kG * (kDh + 2);
   if (tid < kG * kDh) {
     const int g = tid / kDh, d = tid - g * kDh;
@@ -486,48 +605,72 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    // blk[0] counts arrivals, blk[1] collects the XCDs the row ran on; the
-    // last arrival checks and clears both
+    // blk[0..1]: the row counter of row_arrive; blk[2] collects the XCDs
+    // the row ran on, which the last arrival checks and clears
     uint32_t* blk = a.bar + ((int64_t)r * 3 + 2) * kBarWords;
-    __hip_atomic_fetch_or(blk + 1, 1u << (xcc_id() & 31u), __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // recorded before arriving
-    const uint32_t old =
-        __hip_atomic_fetch_add(blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old == (uint32_t)a.WR - 1;
+    if (!select) {  // rows that select recorded it before B1
+      record_xcd(a, r);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // recorded before arriving
+    }
+    bool last;
+    row_arrive(blk, a.WR, &last);
     if (last) {
-      const uint32_t seen = ld_dev(blk + 1);
+      const uint32_t seen = ld_dev(blk + 2);
       if (__popc(seen) > 1)
         __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(blk + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(blk + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     s_flag = last ? 1u : 0u;
   }
   __syncthreads();
   if (!s_flag) return;
+  // The row's partials: (m, l) of every (split, head) into LDS, the split
+  // weights 2^(m - M) per head, then o summed over the splits by two threads
+  // per output (each with its splits' loads all in flight).
   const float* rp = a.part + (int64_t)r * a.WR * kG * (kDh + 2);
-  float* sw = lds.o;  // [WR][4] split weights, then [4] totals
-  if (tid < kG) {
+  float* sm = lds.o;                  // [kMaxWR * 4] m
+  float* sl = sm + kMaxWR * kG;       // [kMaxWR * 4] l
+  float* sw = sl + kMaxWR * kG;       // [kMaxWR * 4] weights (0 past WR)
+  float* stl = sw + kMaxWR * kG;      // [4] sum of l * weight
+  float* so = stl + kG;               // [kTH] half sums of o
+  if (tid < kMaxWR * kG) {
+    const bool in = tid < a.WR * kG;
+    sm[tid] = in ? ld_dev(rp + (int64_t)tid * (kDh + 2)) : -INFINITY;
+    sl[tid] = in ? ld_dev(rp + (int64_t)tid * (kDh + 2) + 1) : 0.f;
+  }
+  __syncthreads();
+  if (tid < kMaxWR * kG) {
+    const int g = tid % kG;
     float M = -INFINITY;
-    for (int s = 0; s < a.WR; ++s) M = fmaxf(M, ld_dev(rp + ((int64_t)s * kG + tid) * (kDh + 2)));
+    for (int s2 = 0; s2 < a.WR; ++s2) M = fmaxf(M, sm[s2 * kG + g]);
+    sw[tid] = (sm[tid] == -INFINITY || M == -INFINITY) ? 0.f : exp2f(sm[tid] - M);
+  }
+  __syncthreads();
+  if (tid < kG) {
     float l = 0.f;
-    for (int s = 0; s < a.WR; ++s) {
-      const float* pp = rp + ((int64_t)s * kG + tid) * (kDh + 2);
-      const float ms = ld_dev(pp);
-      const float w = (ms == -INFINITY || M == -INFINITY) ? 0.f : exp2f(ms - M);
-      sw[s * kG + tid] = w;
-      l += ld_dev(pp + 1) * w;
+    for (int s2 = 0; s2 < a.WR; ++s2) l += sl[s2 * kG + tid] * sw[s2 * kG + tid];
+    stl[tid] = l;
+  }
+  {
+    constexpr int kHalf = kMaxWR / 2;
+    const int half = tid / (kG * kDh), e = tid % (kG * kDh);
+    const int g = e / kDh, d = e - g * kDh;
+    float v[kHalf];
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u) {
+      const int s2 = min(half * kHalf + u, a.WR - 1);
+      v[u] = ld_dev(rp + ((int64_t)s2 * kG + g) * (kDh + 2) + 2 + d);
     }
-    sw[a.WR * kG + tid] = l;
+    float o = 0.f;
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u) o = __builtin_fmaf(v[u], sw[(half * kHalf + u) * kG + g], o);
+    so[tid] = o;
   }
   __syncthreads();
   if (tid < kG * kDh) {
     const int g = tid / kDh, d = tid - g * kDh;
-    float o = 0.f;
-    for (int s = 0; s < a.WR; ++s)
-      o = __builtin_fmaf(ld_dev(rp + ((int64_t)s * kG + g) * (kDh + 2) + 2 + d), sw[s * kG + g], o);
-    const float l = sw[a.WR * kG + g];
+    const float o = so[tid] + so[tid + kG * kDh];
+    const float l = stl[g];
     a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
   }
 }
@@ -571,13 +714,13 @@ bool fused_plan(int R, int T, int keep_max, FusedPlan* p) {
   if (xcd_info(&xi) != LAP_OK || xi.cu % xi.nxcc != 0) return false;
   const int per_xcd = xi.cu / xi.nxcc;
   const int RX = (R + xi.nxcc - 1) / xi.nxcc;
-  int WR = per_xcd / RX;
+  int WR = std::min(per_xcd / RX, kMaxWR);
   WR = std::min(WR, std::max(1, (T + kTH - 1) / kTH));
   if (WR < 1) return false;
   const int ch = (T + WR - 1) / WR;
   const int tok = (ch + kTH - 1) / kTH;
   if (tok < 1 || tok > kMaxTok) return false;
-  if ((keep_max + WR - 1) / WR > kKeepMax) return false;
+  (void)keep_max;  // a workgroup keeps at most its chunk's tokens: tok * 1024 <= kKeepMax
   *p = FusedPlan{xi.nxcc, RX, WR, tok, xi.nxcc * RX * WR};
   return true;
 }
@@ -586,14 +729,15 @@ struct StepWs {
   uint32_t* status;
   uint32_t* bar;
   uint32_t* hist;
-  uint2* cand;
+  uint32_t* t2;
   float* part;
   size_t bytes;
 };
-// Workspace of the fused step for R rows, WR workgroups each, T columns:
-// status, barrier lines (these two must start zeroed and are left zeroed),
-// histograms, candidates, partials.
-StepWs carve_step(void* base, int R, int WR, int T) {
+// Workspace of the fused step for R rows and WR workgroups per row: status
+// words, barrier lines and row histograms (these three must start zeroed,
+// and every call leaves them zeroed), then the per-chunk level-2 tables and
+// the attention partials.  With WR = 0, the persistent head only.
+StepWs carve_step(void* base, int R, int WR) {
   StepWs w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -604,8 +748,8 @@ StepWs carve_step(void* base, int R, int WR, int T) {
   };
   w.status = reinterpret_cast<uint32_t*>(take(kStatusBytes));
   w.bar = reinterpret_cast<uint32_t*>(take((size_t)R * 3 * kBarWords * 4));
-  w.hist = reinterpret_cast<uint32_t*>(take((size_t)R * WR * 256 * 4));
-  w.cand = reinterpret_cast<uint2*>(take((size_t)R * T * 8));
+  w.hist = reinterpret_cast<uint32_t*>(take((size_t)R * kL1 * 4));
+  w.t2 = reinterpret_cast<uint32_t*>(take((size_t)R * WR * kT2 * 4));
   w.part = reinterpret_cast<float*>(take((size_t)R * WR * kG * (kDh + 2) * 4));
   w.bytes = off;
   return w;
@@ -627,13 +771,13 @@ void launch_fused_dt(const StepArgs& a, int tok, int grid, hipStream_t st) {
 }  // namespace
 
 // Bytes at the start of a lap_decode_step workspace that only the fused
-// kernel uses: the status words and barrier lines (kept zero between calls,
-// whatever path a call takes) and, when the fused kernel applies to this
-// shape, its histograms, candidates and partials.
+// kernel uses: the status words, barrier lines and row histograms (kept zero
+// between calls, whatever path a call takes) and, when the fused kernel applies to this
+// shape, its level-2 tables and partials.
 size_t decode_step_fused_bytes(int R, int T, int keep_max) {
   FusedPlan fp;
-  if (!fused_plan(R, T, keep_max, &fp)) return carve_step(nullptr, R, 0, 0).bytes;
-  return carve_step(nullptr, R, fp.WR, T).bytes;
+  if (!fused_plan(R, T, keep_max, &fp)) return carve_step(nullptr, R, 0).bytes;
+  return carve_step(nullptr, R, fp.WR).bytes;
 }
 
 // Run the fused step; LAP_ERR_UNSUPPORTED when this shape must take the
@@ -651,7 +795,9 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
   FusedPlan fp;
   if (!fused_plan(R, T, keep_max, &fp)) return LAP_ERR_UNSUPPORTED;
   if (!score_g4_supported(codes, cs_b, cs_h, cs_t)) return LAP_ERR_UNSUPPORTED;
-  StepWs w = carve_step(workspace, R, fp.WR, T);
+  // query fragments are read as 8-byte vectors
+  if ((reinterpret_cast<uintptr_t>(q) & 7) || (q_sb & 3) || (q_sh & 3)) return LAP_ERR_UNSUPPORTED;
+  StepWs w = carve_step(workspace, R, fp.WR);
   LAP_CHECK_CODE(workspace && ws_bytes >= w.bytes, LAP_ERR_WORKSPACE,
                  "lap_decode_step: workspace of %zu bytes needed", w.bytes);
   StepArgs a{};
@@ -673,8 +819,8 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
   a.idx = out_idx;
   a.idx_i64 = idx_dtype == LAP_DTYPE_I64;
   a.out = static_cast<uint16_t*>(out);
-  a.status = w.status; a.bar = w.bar; a.hist = w.hist; a.cand = w.cand; a.part = w.part;
-  a.nxcc = fp.nxcc; a.RX = fp.RX; a.WR = fp.WR; a.cand_cap = T; a.keep_cap = kKeepMax;
+  a.status = w.status; a.bar = w.bar; a.hist = w.hist; a.t2 = w.t2; a.part = w.part;
+  a.nxcc = fp.nxcc; a.RX = fp.RX; a.WR = fp.WR;
   a.one = f16_one();
   if (dtype == LAP_DTYPE_F16) launch_fused_dt<LAP_DTYPE_F16>(a, fp.tok, fp.grid, st);
   else launch_fused_dt<LAP_DTYPE_BF16>(a, fp.tok, fp.grid, st);
