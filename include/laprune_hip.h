@@ -371,6 +371,29 @@ int lap_decode_step(const void* lut_gmkg, const uint8_t* codes,
  * be trusted. */
 int lap_decode_step_status(const void* workspace, size_t workspace_bytes,
                            uint32_t* split_rows, uint32_t* timeouts);
+/* lap_decode_step without a workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * results and errors as lap_decode_step, minus the workspace; the step's
+ * scratch is a static device array of 64 MiB per GPU (held by every GPU the
+ * library runs on until the process ends), its row barriers and histograms
+ * laid out for B * Hkv <= 256 KV rows.  Shapes that need more scratch than
+ * that (or more rows) fail with LAP_ERR_WORKSPACE; nothing is allocated.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (different streams, or other threads) race and must not be issued. */
+int lap_decode_step_noalloc(const void* lut_gmkg, const uint8_t* codes,
+                            int64_t codes_stride_b, int64_t codes_stride_h,
+                            int64_t codes_stride_t,
+                            int T, int cand_start, int cand_end, int k,
+                            int sink_count, int tail_start, int tail_count,
+                            const lap_row_plan* plans, int k_cols, int max_sink, int max_tail,
+                            int key_mode,
+                            const void* q, int64_t q_sb, int64_t q_sh,
+                            const void* keys, const void* vals, int dtype,
+                            int B, int Hq, int Hkv, int T_kv, int D,
+                            int64_t k_sb, int64_t k_sh, int64_t k_st,
+                            int64_t v_sb, int64_t v_sh, int64_t v_st, float scale,
+                            void* out_idx, int idx_dtype, void* out, lap_stream_t stream);
 
 /* ======================================================================= *
  * A6  Greedy AQ encode                                                     *

@@ -57,6 +57,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 namespace lap {
 
@@ -736,8 +737,11 @@ struct StepWs {
 // Workspace of the fused step for R rows and WR workgroups per row: status
 // words, barrier lines and row histograms (these three must start zeroed,
 // and every call leaves them zeroed), then the per-chunk level-2 tables and
-// the attention partials.  With WR = 0, the persistent head only.
-StepWs carve_step(void* base, int R, int WR) {
+// the attention partials.  The barrier lines and histograms are laid out for
+// head_rows >= R rows, so that calls of different R on one buffer find
+// their persistent words at the same addresses.  With WR = 0, the persistent
+// head only.
+StepWs carve_step(void* base, int R, int WR, int head_rows) {
   StepWs w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -747,8 +751,8 @@ StepWs carve_step(void* base, int R, int WR) {
     return q;
   };
   w.status = reinterpret_cast<uint32_t*>(take(kStatusBytes));
-  w.bar = reinterpret_cast<uint32_t*>(take((size_t)R * 3 * kBarWords * 4));
-  w.hist = reinterpret_cast<uint32_t*>(take((size_t)R * kL1 * 4));
+  w.bar = reinterpret_cast<uint32_t*>(take((size_t)head_rows * 3 * kBarWords * 4));
+  w.hist = reinterpret_cast<uint32_t*>(take((size_t)head_rows * kL1 * 4));
   w.t2 = reinterpret_cast<uint32_t*>(take((size_t)R * WR * kT2 * 4));
   w.part = reinterpret_cast<float*>(take((size_t)R * WR * kG * (kDh + 2) * 4));
   w.bytes = off;
@@ -774,10 +778,10 @@ void launch_fused_dt(const StepArgs& a, int tok, int grid, hipStream_t st) {
 // kernel uses: the status words, barrier lines and row histograms (kept zero
 // between calls, whatever path a call takes) and, when the fused kernel applies to this
 // shape, its level-2 tables and partials.
-size_t decode_step_fused_bytes(int R, int T, int keep_max) {
+size_t decode_step_fused_bytes(int R, int T, int keep_max, int head_rows) {
   FusedPlan fp;
-  if (!fused_plan(R, T, keep_max, &fp)) return carve_step(nullptr, R, 0).bytes;
-  return carve_step(nullptr, R, fp.WR).bytes;
+  if (!fused_plan(R, T, keep_max, &fp)) return carve_step(nullptr, R, 0, head_rows).bytes;
+  return carve_step(nullptr, R, fp.WR, head_rows).bytes;
 }
 
 // Run the fused step; LAP_ERR_UNSUPPORTED when this shape must take the
@@ -789,7 +793,8 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
                       int T, int cand_start, int cand_end, int k, int sink, int tail_start,
                       int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
                       int max_tail, int key_bf16, float scale, void* out_idx, int idx_dtype,
-                      void* out, void* workspace, size_t ws_bytes, hipStream_t st) {
+                      void* out, void* workspace, size_t ws_bytes, int head_rows,
+                      const char* who, hipStream_t st) {
   const int R = B * Hkv;
   const int keep_max = plans ? k_cols + max_sink + max_tail : k + sink + tail_count;
   FusedPlan fp;
@@ -797,9 +802,9 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
   if (!score_g4_supported(codes, cs_b, cs_h, cs_t)) return LAP_ERR_UNSUPPORTED;
   // query fragments are read as 8-byte vectors
   if ((reinterpret_cast<uintptr_t>(q) & 7) || (q_sb & 3) || (q_sh & 3)) return LAP_ERR_UNSUPPORTED;
-  StepWs w = carve_step(workspace, R, fp.WR);
+  StepWs w = carve_step(workspace, R, fp.WR, head_rows);
   LAP_CHECK_CODE(workspace && ws_bytes >= w.bytes, LAP_ERR_WORKSPACE,
-                 "lap_decode_step: workspace of %zu bytes needed", w.bytes);
+                 "%s: %zu bytes of workspace needed", who, w.bytes);
   StepArgs a{};
   a.lut = static_cast<const uint16_t*>(lut_gmkg);
   a.codes = codes;
@@ -855,43 +860,23 @@ int chain_ws(int B, int Hq, int Hkv, int T, int D, int keep_max, int key_mode, C
 
 }  // namespace
 
-extern "C" int lap_decode_step_workspace_size(int B, int Hq, int Hkv, int T, int D, int keep_max,
-                                              int key_mode, size_t* bytes) {
-  clear_error();
-  LAP_CHECK(bytes, "lap_decode_step_workspace_size: null output");
-  LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T >= 0 && D > 0 && keep_max >= 0,
-            "lap_decode_step_workspace_size: bad sizes");
-  ChainWs cw;
-  int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
-  if (s != LAP_OK) return s;
-  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max), 256);
-  *bytes = fused + cw.ret + cw.attn;
-  return LAP_OK;
-}
+namespace {
 
-extern "C" int lap_decode_step_status(const void* workspace, size_t workspace_bytes,
-                                      uint32_t* split_rows, uint32_t* timeouts) {
-  clear_error();
-  LAP_CHECK(workspace && split_rows && timeouts, "lap_decode_step_status: null pointer");
-  LAP_CHECK(workspace_bytes >= 8, "lap_decode_step_status: workspace too small");
-  uint32_t h[2] = {0, 0};
-  LAP_HIP(hipMemcpy(h, workspace, sizeof(h), hipMemcpyDeviceToHost), "status copy");
-  *split_rows = h[0];
-  *timeouts = h[1];
-  return LAP_OK;
-}
-
-extern "C" int lap_decode_step(
-    const void* lut_gmkg, const uint8_t* codes, int64_t codes_stride_b, int64_t codes_stride_h,
-    int64_t codes_stride_t, int T, int cand_start, int cand_end, int k, int sink_count,
-    int tail_start, int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
-    int max_tail, int key_mode, const void* q, int64_t q_sb, int64_t q_sh, const void* keys,
-    const void* vals, int dtype, int B, int Hq, int Hkv, int T_kv, int D, int64_t k_sb,
-    int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, float scale,
-    void* out_idx, int idx_dtype, void* out, void* workspace, size_t workspace_bytes,
-    lap_stream_t stream) {
-  clear_error();
-  const char* who = "lap_decode_step";
+// One decode step after argument checks, on `workspace` of `ws_bytes`
+// bytes whose persistent head is laid out for head_rows rows.  With
+// need_all, the workspace must hold the fused part and the chain's part
+// whatever path runs (lap_decode_step's contract); otherwise each path
+// checks only what it uses.
+int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
+                    int64_t codes_stride_b, int64_t codes_stride_h, int64_t codes_stride_t, int T,
+                    int cand_start, int cand_end, int k, int sink_count, int tail_start,
+                    int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
+                    int max_tail, int key_mode, const void* q, int64_t q_sb, int64_t q_sh,
+                    const void* keys, const void* vals, int dtype, int B, int Hq, int Hkv,
+                    int T_kv, int D, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
+                    int64_t v_sh, int64_t v_st, float scale, void* out_idx, int idx_dtype,
+                    void* out, void* workspace, size_t workspace_bytes, int head_rows,
+                    bool need_all, lap_stream_t stream) {
   LAP_CHECK(lut_gmkg && q && keys && vals && out, "%s: null pointer", who);
   LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T > 0 && T_kv > 0 && D > 0, "%s: bad sizes", who);
   LAP_CHECK(Hq == 4 * Hkv, "%s: the fused scorer serves G = 4 query heads per KV head", who);
@@ -921,21 +906,24 @@ extern "C" int lap_decode_step(
   ChainWs cw;
   int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
   if (s != LAP_OK) return s;
-  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max), 256);
-  LAP_CHECK_CODE(workspace && workspace_bytes >= fused + cw.ret + cw.attn, LAP_ERR_WORKSPACE,
-                 "%s: workspace of %zu bytes needed", who, fused + cw.ret + cw.attn);
+  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max, head_rows), 256);
+  if (need_all)
+    LAP_CHECK_CODE(workspace && workspace_bytes >= fused + cw.ret + cw.attn, LAP_ERR_WORKSPACE,
+                   "%s: workspace of %zu bytes needed", who, fused + cw.ret + cw.attn);
   hipStream_t st = as_stream(stream);
   if (km == key_mode && D == 128) {
     s = decode_step_fused(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, q, q_sb,
                           q_sh, keys, vals, dtype, B, Hkv, T_kv, k_sb, k_sh, k_st, v_sb, v_sh,
                           v_st, T, cand_start, cand_end, k_eff, sink_count, tail_start,
                           tail_count, plans, plans ? k_cols : k_eff, max_sink, max_tail,
-                          km == LAP_KEY_BF16, scale, out_idx, idx_dtype, out, workspace, fused,
-                          st);
+                          km == LAP_KEY_BF16, scale, out_idx, idx_dtype, out, workspace,
+                          std::min(workspace_bytes, fused), head_rows, who, st);
     if (s != LAP_ERR_UNSUPPORTED) return s;
     clear_error();
   }
   // the kernel chain: scorer + top-k, then the split-K attention and merge
+  LAP_CHECK_CODE(workspace && workspace_bytes >= fused + cw.ret + cw.attn, LAP_ERR_WORKSPACE,
+                 "%s: workspace of %zu bytes needed", who, fused + cw.ret + cw.attn);
   char* base = static_cast<char*>(workspace) + fused;
   void* ws_r = base;
   void* ws_a = base + cw.ret;
@@ -962,4 +950,130 @@ extern "C" int lap_decode_step(
                                        k_sb, k_sh, k_st, v_sb, v_sh, v_st, out_idx, idx_dtype,
                                        H_idx, k_cols, plans, max_sink, max_tail, scale, out, ws_a,
                                        cw.attn, stream);
+}
+
+}  // namespace
+
+extern "C" int lap_decode_step_workspace_size(int B, int Hq, int Hkv, int T, int D, int keep_max,
+                                              int key_mode, size_t* bytes) {
+  clear_error();
+  LAP_CHECK(bytes, "lap_decode_step_workspace_size: null output");
+  LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T >= 0 && D > 0 && keep_max >= 0,
+            "lap_decode_step_workspace_size: bad sizes");
+  ChainWs cw;
+  int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
+  if (s != LAP_OK) return s;
+  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max, B * Hkv), 256);
+  *bytes = fused + cw.ret + cw.attn;
+  return LAP_OK;
+}
+
+extern "C" int lap_decode_step_status(const void* workspace, size_t workspace_bytes,
+                                      uint32_t* split_rows, uint32_t* timeouts) {
+  clear_error();
+  LAP_CHECK(workspace && split_rows && timeouts, "lap_decode_step_status: null pointer");
+  LAP_CHECK(workspace_bytes >= 8, "lap_decode_step_status: workspace too small");
+  uint32_t h[2] = {0, 0};
+  LAP_HIP(hipMemcpy(h, workspace, sizeof(h), hipMemcpyDeviceToHost), "status copy");
+  *split_rows = h[0];
+  *timeouts = h[1];
+  return LAP_OK;
+}
+
+extern "C" int lap_decode_step(
+    const void* lut_gmkg, const uint8_t* codes, int64_t codes_stride_b, int64_t codes_stride_h,
+    int64_t codes_stride_t, int T, int cand_start, int cand_end, int k, int sink_count,
+    int tail_start, int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
+    int max_tail, int key_mode, const void* q, int64_t q_sb, int64_t q_sh, const void* keys,
+    const void* vals, int dtype, int B, int Hq, int Hkv, int T_kv, int D, int64_t k_sb,
+    int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, float scale,
+    void* out_idx, int idx_dtype, void* out, void* workspace, size_t workspace_bytes,
+    lap_stream_t stream) {
+  clear_error();
+  return decode_step_run("lap_decode_step", lut_gmkg, codes, codes_stride_b, codes_stride_h,
+                         codes_stride_t, T, cand_start, cand_end, k, sink_count, tail_start,
+                         tail_count, plans, k_cols, max_sink, max_tail, key_mode, q, q_sb, q_sh,
+                         keys, vals, dtype, B, Hq, Hkv, T_kv, D, k_sb, k_sh, k_st, v_sb, v_sh,
+                         v_st, scale, out_idx, idx_dtype, out, workspace, workspace_bytes,
+                         B * Hkv, true, stream);
+}
+
+// ------------------------------------------------------------------------
+// lap_decode_step_noalloc: the same step on a static per-device scratch
+// array instead of a caller workspace, for callers that may not allocate.
+//
+// `scratch` is one file-scope device array; every GPU the library runs on
+// holds its own copy (at its own address) until the process ends.  In host
+// code its name is only a stand-in, so host code uses the address that
+// hipGetSymbolAddress returns for the current device, taken once per device
+// at the first call there.  Its persistent head (status words, row
+// barriers, row histograms) is laid out for kScratchRows rows, so calls of
+// any shape find those words in place; the fused kernel leaves them zeroed
+// (counters at multiples of their per-call advance), and the first call on
+// a device clears them with a fill kernel on the call's stream.
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr int kScratchRows = 256;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ void scratch_clear_kernel(uint4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[64];
+
+int scratch_for_device(hipStream_t st, void** out) {
+  int dev = 0;
+  LAP_HIP(hipGetDevice(&dev), "hipGetDevice");
+  LAP_CHECK_CODE(dev >= 0 && dev < 64, LAP_ERR_UNSUPPORTED, "device ordinal %d out of range",
+                 dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    LAP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    LAP_CHECK_CODE(p && (reinterpret_cast<uintptr_t>(p) & 255) == 0, LAP_ERR_HIP,
+                   "scratch symbol address %p is not 256-byte aligned", p);
+    const size_t head = carve_step(nullptr, kScratchRows, 0, kScratchRows).bytes;
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, st, static_cast<uint4*>(p),
+                       head / 16);
+    LAP_LAUNCH_CHECK("scratch_clear_kernel");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return LAP_OK;
+}
+
+}  // namespace
+
+extern "C" int lap_decode_step_noalloc(
+    const void* lut_gmkg, const uint8_t* codes, int64_t codes_stride_b, int64_t codes_stride_h,
+    int64_t codes_stride_t, int T, int cand_start, int cand_end, int k, int sink_count,
+    int tail_start, int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
+    int max_tail, int key_mode, const void* q, int64_t q_sb, int64_t q_sh, const void* keys,
+    const void* vals, int dtype, int B, int Hq, int Hkv, int T_kv, int D, int64_t k_sb,
+    int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, float scale,
+    void* out_idx, int idx_dtype, void* out, lap_stream_t stream) {
+  clear_error();
+  const char* who = "lap_decode_step_noalloc";
+  LAP_CHECK(B > 0 && Hkv > 0, "%s: bad sizes", who);
+  LAP_CHECK_CODE((int64_t)B * Hkv <= kScratchRows, LAP_ERR_WORKSPACE,
+                 "%s: %d x %d KV rows exceed the static scratch's %d rows", who, B, Hkv,
+                 kScratchRows);
+  void* p = nullptr;
+  int s = scratch_for_device(as_stream(stream), &p);
+  if (s != LAP_OK) return s;
+  s = decode_step_run(who, lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, T,
+                      cand_start, cand_end, k, sink_count, tail_start, tail_count, plans, k_cols,
+                      max_sink, max_tail, key_mode, q, q_sb, q_sh, keys, vals, dtype, B, Hq, Hkv,
+                      T_kv, D, k_sb, k_sh, k_st, v_sb, v_sh, v_st, scale, out_idx, idx_dtype, out,
+                      p, kScratchBytes, kScratchRows, false, stream);
+  if (s == LAP_ERR_WORKSPACE)
+    set_error("%s: this shape needs more than the static scratch of %zu bytes (%s)", who,
+              kScratchBytes, lap_last_error());
+  return s;
 }
