@@ -26,7 +26,9 @@ so that the 256 MB Infinity Cache cannot serve the step from cache.
                  query heads outside the timed region: the stock framework
                  decode, reported beside the comparator of record.
 ``cpu_baseline`` the reference's fp32 PyTorch scoring + bf16 cast + top-k
-                 path (restated in oracle/ref_path.py) on the host cores.
+                 path (restated in oracle/ref_path.py) on the host cores, at
+                 the metric's 131072 tokens and, under "c1", at configs[0]
+                 (C1: 8192 tokens, top-2048); 3 warm-ups, median of >= 10.
 ``encode``       configs[2] (C3): greedy AQ encode of one 64-token flush of
                  post-RoPE keys (8 KV heads x 64 tokens = 512 rows, 32x256
                  codebooks), MFMA coarse search + exact recheck, next to the
@@ -92,47 +94,74 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(seconds: float) -> dict:
-    """Time the reference's fp32 CPU path (restated) at T = 131072, top-2048."""
-    import torch
-    from oracle import ref_path
-    ncpu = os.cpu_count() or 1
-    torch.set_num_threads(ncpu)
-    g = torch.Generator().manual_seed(123)
-    q = torch.randn(HQ, D, generator=g).bfloat16().float()
-    cb = torch.randn(M, K, D, generator=g) * 0.02
-    codes = torch.randint(0, 256, (HKV, T, M), generator=g, dtype=torch.uint8)
-
-    def one():
-        s = ref_path.scores_fp32(q, cb, codes, HQ // HKV)
-        return ref_path.select_topk(s, torch.bfloat16, T, sink=SINK, local=LOCAL, k=TOPK)
-
-    for _ in range(3):
-        one()
-    ts = []
-    t_end = time.perf_counter() + seconds
-    while len(ts) < 10 or (time.perf_counter() < t_end and len(ts) < 30):
-        t0 = time.perf_counter()
-        one()
-        ts.append(time.perf_counter() - t0)
-    med = sorted(ts)[len(ts) // 2]
-    model = ""
+def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return "unknown"
+
+
+def _median_time(fn, seconds: float, warmup: int = 3, min_runs: int = 10,
+                 max_runs: int = 30) -> tuple[float, int]:
+    """3 untimed warm-ups, then at least min_runs timed calls (more while
+    `seconds` last, up to max_runs); returns (median seconds, runs)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    t_end = time.perf_counter() + seconds
+    while len(ts) < min_runs or (time.perf_counter() < t_end and len(ts) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2], len(ts)
+
+
+def _ref_select_leg(t_ctx: int, seconds: float, seed: int):
+    """The reference's fp32 CPU path (restated in oracle/ref_path.py) at
+    t_ctx tokens: einsum LUT + int64 gather + sum, bf16 cast, top-2048 per
+    query head.  Returns (median seconds, runs)."""
+    import torch
+    from oracle import ref_path
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(HQ, D, generator=g).bfloat16().float()
+    cb = torch.randn(M, K, D, generator=g) * 0.02
+    codes = torch.randint(0, 256, (HKV, t_ctx, M), generator=g, dtype=torch.uint8)
+
+    def one():
+        s = ref_path.scores_fp32(q, cb, codes, HQ // HKV)
+        return ref_path.select_topk(s, torch.bfloat16, t_ctx, sink=SINK, local=LOCAL, k=TOPK)
+
+    return _median_time(one, seconds)
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The reference's fp32 CPU path at the metric's workload (T = 131072)
+    and at configs[0] (C1: T = 8192), both top-2048, on every host core."""
+    import torch
+    torch.set_num_threads(os.cpu_count() or 1)
+    med, runs = _ref_select_leg(T, seconds, 123)
+    med1, runs1 = _ref_select_leg(8192, min(seconds, 4.0), 124)
+    model = _cpu_model()
     return {
         "value": round(CODE_BYTES / med / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"3 warm-up + {len(ts)} timed calls (median {med * 1e3:.1f} ms) of the "
+        "sample": (f"3 warm-up + {runs} timed calls (median {med * 1e3:.1f} ms) of the "
                    "reference fp32 PyTorch path restated in oracle/ref_path.py: einsum LUT, "
                    "int64 gather + sum over 32 codebooks for 32 q heads x 131072 tokens, "
-                   f"bf16 cast, top-{TOPK} per head; host CPU: {model or 'unknown'}"),
+                   f"bf16 cast, top-{TOPK} per head; host CPU: {model}"),
+        "c1": {
+            "ms": round(med1 * 1e3, 3),
+            "gbs": round(HKV * 8192 * M / med1 / 1e9, 4),
+            "cores": torch.get_num_threads(),
+            "sample": (f"configs[0] (C1): the same path at 8192 tokens (codes [8, 8192, 32]), "
+                       f"top-{TOPK} per head; 3 warm-up + {runs1} timed calls, median; "
+                       f"host CPU: {model}"),
+        },
     }
 
 
@@ -157,17 +186,11 @@ def encode_cpu_baseline(x, cb, seconds: float) -> dict:
     import torch
     from oracle import ref_path
     xc, cbc = x.cpu(), cb.cpu()
-    ref_path.encode_fp32(xc, cbc)
-    ts = []
-    t_end = time.perf_counter() + seconds
-    while len(ts) < 5 or (time.perf_counter() < t_end and len(ts) < 30):
-        t0 = time.perf_counter()
-        ref_path.encode_fp32(xc, cbc)
-        ts.append(time.perf_counter() - t0)
-    med = sorted(ts)[len(ts) // 2]
+    med, runs = _median_time(lambda: ref_path.encode_fp32(xc, cbc), seconds)
     return {"us": round(med * 1e6, 1), "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"1 warm-up + {len(ts)} timed calls of the reference fp32 greedy "
-                      "encode (laprune/quantizer.py:346-355, restated), median"}
+            "sample": f"3 warm-up + {runs} timed calls of the reference fp32 greedy "
+                      "encode (laprune/quantizer.py:346-355, restated), median; "
+                      f"host CPU: {_cpu_model()}"}
 
 
 def traffic_from_profile() -> dict | None:
