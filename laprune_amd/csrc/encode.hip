@@ -34,6 +34,7 @@ struct Prep {
   float* cn;       // [M][K]
   float* scn;      // [M][K] sqrtf(cn)
   uint16_t* frag;  // bf16 MFMA B fragments [M][K/16][D/16][64 lanes][4] (K % 16 == 0)
+  uint16_t* frag4; // 4x4x4 B operands [M][ceil(K/64)][D/8][64 lanes][8] (K % 16 == 0)
   size_t bytes;
 };
 
@@ -49,6 +50,8 @@ Prep carve_prep(void* base, int M, int K, int D) {
   off = align_up(off + (size_t)M * K * 4, 256);
   p.frag = reinterpret_cast<uint16_t*>(b ? b + off : nullptr);
   if (K % 16 == 0) off = align_up(off + (size_t)M * K * D * 2, 256);
+  p.frag4 = reinterpret_cast<uint16_t*>(b ? b + off : nullptr);
+  if (K % 16 == 0) off = align_up(off + (size_t)M * ((K + 63) / 64) * 64 * D * 2, 256);
   p.bytes = off;
   return p;
 }
@@ -279,6 +282,28 @@ __global__ __launch_bounds__(256) void encode_prep_frag(const float* __restrict_
   for (int e = 0; e < 4; ++e) dst[e] = f2bf(src[e]);
 }
 
+// One thread per (m, quarter q, step pair p, lane l): the eight bf16 of
+// C[m][64q + l][8p .. 8p+7] (zeros past K), the B operands of two 4x4x4 steps.
+__global__ __launch_bounds__(256) void encode_prep_frag4(const float* __restrict__ cb, int M,
+                                                         int K, int D,
+                                                         uint16_t* __restrict__ frag4) {
+  const int NQ = (K + 63) / 64, NP = D / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)M * NQ * NP * 64;
+  if (i >= total) return;
+  const int l = (int)(i % 64);
+  int64_t q = i / 64;
+  const int pp = (int)(q % NP);
+  q /= NP;
+  const int qq = (int)(q % NQ);
+  const int m = (int)(q / NQ);
+  const int k = qq * 64 + l;
+  uint16_t* dst = frag4 + i * 8;
+  const float* src = cb + ((int64_t)m * K + k) * D + 8 * pp;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dst[e] = k < K ? f2bf(src[e]) : (uint16_t)0;
+}
+
 // Cross-lane moves within a row of 16 lanes (DPP, no LDS round trip).
 // row_shl:n gives lane i the value of lane i + n of its row (0 past the end).
 template <int CTRL>
@@ -349,9 +374,10 @@ struct EncShared {
   float r[16][D];
   uint16_t rb[16][D];  // bf16(r): the MFMA A operand
   float rn[16];
-  float u[EncCfg<D>::WAVES][16];
-  uint32_t cnt[16];       // survivors of the coarse pass per row
-  uint8_t list[16][256];  // their entries, in no particular order
+  float u[16][EncCfg<D>::WAVES];  // per row, per wave: min of the upper bounds
+  uint16_t mask[16][16];          // per row, per 16-entry tile: coarse-pass survivors
+  uint8_t list[16][256];          // survivors of a row, ascending
+  uint8_t code[16][64];           // codes of stages < 64, stored after the last stage
 };
 
 // Pull this workgroup's quarter of codebook m (fp32) into L2 ahead of the
@@ -367,7 +393,9 @@ __device__ __forceinline__ uint32_t enc_prefetch_l2(const float* __restrict__ cb
   const int64_t words = (int64_t)K * D;     // fp32 words of codebook m
   const int64_t q = words / 4;              // this workgroup's quarter
   const int64_t lo = ((blockIdx.x >> 3) & 3) * q;
-  int64_t w = lo + ((int64_t)lane * C::WAVES + wave) * 32;  // one word per 128-byte line
+  // one word per 32 bytes of the quarter (a wave's four lanes on one line
+  // share a request)
+  int64_t w = lo + ((int64_t)wave * 64 + lane) * (q / C::THREADS > 8 ? q / C::THREADS : 8);
   w = w < words - 1 ? w : words - 1;
   return __builtin_bit_cast(uint32_t, cb[(int64_t)m * words + w]);
 }
@@ -428,24 +456,26 @@ __device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st
   for (int e = 0; e < 4; ++e) umin[e] = row_min16(umin[e]);
   if ((lane & 15) == 0)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s.u[wave][4 * (lane >> 4) + e] = umin[e];
+    for (int e = 0; e < 4; ++e) s.u[4 * (lane >> 4) + e][wave] = umin[e];
   lds_barrier();
+  // Survivors: entries whose lower bound does not exceed the row's least
+  // upper bound U.  One ballot per (tile, row slot) gives the four rows'
+  // 16-entry masks; lane 16g writes row 4g + e's (no atomics, no returns).
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int row = 4 * (lane >> 4) + e;
-    float U = s.u[0][row];
+    const float4* up = reinterpret_cast<const float4*>(s.u[row]);
+    float U = INFINITY;
 #pragma unroll
-    for (int w = 1; w < C::WAVES; ++w) U = fminf(U, s.u[w][row]);
-    uint32_t keep = 0;
+    for (int w = 0; w < C::WAVES / 4; ++w) {
+      const float4 v = up[w];
+      U = fminf(U, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
+    }
 #pragma unroll
-    for (int i = 0; i < C::TPW; ++i)
-      keep |= (uint32_t)(wave + i * C::WAVES < NT && !(g_lo[i][e] > U)) << i;
-    // Only lanes holding survivors (about 1.7 per row) reserve list slots.
-    if (keep) {
-      uint32_t slot = atomicAdd(&s.cnt[row], (uint32_t)__builtin_popcount(keep));
-#pragma unroll
-      for (int i = 0; i < C::TPW; ++i)
-        if (keep & (1u << i)) s.list[row][slot++] = (uint8_t)((wave + i * C::WAVES) * 16 + (lane & 15));
+    for (int i = 0; i < C::TPW; ++i) {
+      const int tile = wave + i * C::WAVES;
+      const uint64_t b = __ballot(tile < NT && !(g_lo[i][e] > U));
+      if ((lane & 15) == 0) s.mask[row][tile] = (uint16_t)(b >> (lane & 48));
     }
   }
   lds_barrier();
@@ -467,8 +497,27 @@ __device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st
       rc[t + 3] = v.w;
     }
     const float rn = s.rn[row];
-    const uint32_t n = s.cnt[row];
-    if (j == 0) s.cnt[row] = 0;  // ready for the next stage (read above by the whole group)
+    // The row's survivor list: lane j takes tile j's mask, an inclusive scan
+    // over the group's 16 lanes gives each tile its offset, and the lanes
+    // write their entries in ascending order.  The group reads the list
+    // back in the same wave, so LDS order is all that is needed.
+    uint32_t n;
+    {
+      const uint32_t mk = s.mask[row][j];
+      const uint32_t c = (uint32_t)__builtin_popcount(mk);
+      uint32_t inc = c;
+      inc += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)inc, 0x111, 0xf, 0xf, true);  // row_shr:1
+      inc += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)inc, 0x112, 0xf, 0xf, true);  // row_shr:2
+      inc += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)inc, 0x114, 0xf, 0xf, true);  // row_shr:4
+      inc += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)inc, 0x118, 0xf, 0xf, true);  // row_shr:8
+      n = (uint32_t)__builtin_amdgcn_ds_bpermute((lane | 15) << 2, (int)inc);
+      uint32_t o = inc - c, mm = mk;
+      while (mm) {
+        s.list[row][o++] = (uint8_t)(j * 16 + __builtin_ctz(mm));
+        mm &= mm - 1;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
     float bc[C::L];
 #pragma unroll
     for (int t = 0; t < C::L; ++t) bc[t] = 0.f;
@@ -537,7 +586,9 @@ __device__ __forceinline__ void enc_stage(EncShared<D>& s, const EncStage<D>& st
     a2 = row_fold16(a2);
     if (j == 0) {
       s.rn[row] = a2;
-      if (row0 + row < N && rm.live(row0 + row)) rm.crow(row0 + row)[m] = (uint8_t)code;
+      // held in LDS: a store here would hold up the next stage's operand wait
+      if (m < 64) s.code[row][m] = (uint8_t)code;
+      else if (row0 + row < N && rm.live(row0 + row)) rm.crow(row0 + row)[m] = (uint8_t)code;
     }
   }
   lds_barrier();
@@ -558,14 +609,20 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
     for (int r = 0; r < 16; ++r) any = any || (row0 + r < N && rm.live(row0 + r));
     if (!any) return;
   }
+  // Stage 0's fragments are requested first, so that they arrive with the
+  // rows.  Stage m + 1's are requested before stage m runs.  The request is
+  // unconditional (the last stage re-requests itself) so that no branch
+  // joins paths with different numbers of loads in flight, which would force
+  // the compiler to wait for all of them before the first MFMA.
+  EncStage<D> st0, st1;
+  enc_load_stage<D>(st0, frag, cn, scn, 0, NT, K, wave, lane);
   for (int i = tid; i < 16 * D; i += C::THREADS) {
     const int r = i / D, d = i - r * D;
     const float v = (row0 + r < N && rm.live(row0 + r)) ? rm.xval(row0 + r, d) : 0.f;
     s.r[r][d] = v;
     s.rb[r][d] = __builtin_bit_cast(uint16_t, (__bf16)v);
   }
-  if (tid < 16) s.cnt[tid] = 0;
-  __syncthreads();
+  lds_barrier();
   const int grp = wave * 4 + (lane >> 4), j = lane & 15;
   if (grp < 16) {
     const float* rr = s.r[grp] + j * C::L;
@@ -575,14 +632,8 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
     a2 = row_fold16(a2);
     if (j == 0) s.rn[grp] = a2;
   }
-  __syncthreads();
+  lds_barrier();
 
-  // Stage m + 1's fragments are requested before stage m runs.  The request
-  // is unconditional (the last stage re-requests itself) so that no branch
-  // joins paths with different numbers of loads in flight, which would force
-  // the compiler to wait for all of them before the first MFMA.
-  EncStage<D> st0, st1;
-  enc_load_stage<D>(st0, frag, cn, scn, 0, NT, K, wave, lane);
   uint32_t sink = 0, pfa = 0, pfb = 0;
   for (int m = 0; m < M; m += 2) {
     enc_load_stage<D>(st1, frag, cn, scn, min(m + 1, M - 1), NT, K, wave, lane);
@@ -597,7 +648,296 @@ __global__ __launch_bounds__(EncCfg<D>::THREADS) void encode_mfma_kernel(
   }
   sink ^= pfa ^ pfb;
   if (sink == 0x9e3779b9u && N < 0) rm.codes[0] = 0;  // never true: keeps the prefetch loads
+  const int mc = M < 64 ? M : 64;
+  for (int i = tid; i < 16 * mc; i += C::THREADS) {
+    const int r = i / mc, mm = i - r * mc;
+    if (row0 + r < N && rm.live(row0 + r)) rm.crow(row0 + r)[mm] = s.code[r][mm];
+  }
   if (tid < 16 && rnorm && row0 + tid < N && rm.live(row0 + tid))
+    rnorm[row0 + tid] = sqrtf(s.rn[tid]);
+}
+
+// ------------------------------------------ four rows per workgroup (flushes)
+// The stage of enc_stage for 4 rows, so that a decode flush (8 KV heads x 64
+// tokens = 512 rows) spreads over 128 CUs instead of 32.  The stage chain is
+// latency-bound: a 16-row workgroup has one wave per SIMD, each running 16
+// rows' bound arithmetic, list building and recheck back to back.  Here the
+// coarse dots come from v_mfma_f32_4x4x4bf16_1k (16 blocks of 4x4x4); in
+// block b (lanes 4b .. 4b+3)
+//     D[lane l][v] = sum_k A[lane 4b+v][k] * B[lane l][k]
+// over the four bf16 k terms of a register.  With lane l supplying residual
+// row l % 4 as A and codebook entry 64w + l (wave w) as B, lane l ends with the
+// dots of its entry with all four rows.  The error bound of the 16-row kernel
+// holds as it stands: it covers any fp32 accumulation order of the D exact
+// bf16 products.  After one barrier wave v owns row v: its survivors are four
+// wave-uniform ballots over the row's 256 lower bounds, rechecked four at a
+// time (one candidate per 16-lane group, dot16 chain j in lane j), and the
+// group holding the winner updates the row's residual.  B operands come from
+// the 16x16x16 fragment layout of the prep: entry k's 4 bf16 at d = 4s are
+// fragment lane (k % 16) + 16 (s % 4) of tile k / 16, k-step s / 4, i.e.
+// 16 s uint2 past its step-0 slot.
+constexpr int kR4 = 4;
+// Codes of the first kCodeStage stages are kept in LDS and stored once at
+// the end: a global store inside the stage loop would make the next stage's
+// wait for its operands also wait for the store's acknowledgement.
+constexpr int kCodeStage = 64;
+
+template <int D>
+struct Enc4Shared {
+  float r[kR4][D];
+  uint16_t rb[kR4][D + 8];  // bf16(r); the pitch puts the four rows in different banks
+  float rn[kR4];
+  float2 gb[kR4][256];      // per row, per entry: (lower, upper) bound of the coarse distance
+  uint8_t code[kR4][kCodeStage];  // the rows' codes, written out after the last stage
+};
+
+template <int D>
+struct Enc4Stage {
+  uint4 b[D / 8];  // B operands of steps 2p (x, y) and 2p + 1 (z, w)
+  float cn, scn;
+};
+
+// Stage m's operands of lane l of wave q: entry 64q + l (quarters past K load
+// the last quarter, results ignored), one coalesced 16-byte load per step pair.
+template <int D>
+__device__ __forceinline__ void enc4_load_stage(Enc4Stage<D>& st, const uint4* __restrict__ frag4,
+                                                const float* __restrict__ cn,
+                                                const float* __restrict__ scn, int m, int NQ,
+                                                int K, int qc, int kc, int lane) {
+  const uint4* f = frag4 + (((int64_t)m * NQ + qc) * (D / 8)) * 64 + lane;
+#pragma unroll
+  for (int pp = 0; pp < D / 8; ++pp) st.b[pp] = f[64 * pp];
+  st.cn = cn[(int64_t)m * K + kc];
+  st.scn = scn[(int64_t)m * K + kc];
+}
+
+// Minimum over the 64 lanes of a wave (wave-uniform).
+__device__ __forceinline__ float wave_min64(float a) {
+  a = row_min16(a);
+  const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0));
+  const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 16));
+  const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 32));
+  const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 48));
+  return fminf(fminf(a0, a1), fminf(a2, a3));
+}
+
+// Lowest set bit of the 256-bit mask m[0..3] (wave-uniform), cleared; -1 if empty.
+__device__ __forceinline__ int pop_lowest(uint64_t& m0, uint64_t& m1, uint64_t& m2, uint64_t& m3) {
+  if (m0) { const int b = __builtin_ctzll(m0); m0 &= m0 - 1; return b; }
+  if (m1) { const int b = __builtin_ctzll(m1); m1 &= m1 - 1; return 64 + b; }
+  if (m2) { const int b = __builtin_ctzll(m2); m2 &= m2 - 1; return 128 + b; }
+  if (m3) { const int b = __builtin_ctzll(m3); m3 &= m3 - 1; return 192 + b; }
+  return -1;
+}
+
+// Pull slice (block / 8) % 16 of codebook m (fp32) into L2 ahead of the exact
+// recheck: the workgroups of one XCD (block ids equal mod 8) take different
+// slices.  One word per 32 bytes; consumed a stage later through a sink.
+template <int D>
+__device__ __forceinline__ uint32_t enc4_prefetch_l2(const float* __restrict__ cb, int m, int K,
+                                                     int tid) {
+  const int64_t words = (int64_t)K * D;
+  const int64_t slice = (words + 15) / 16;
+  const int64_t stride = slice / 256 > 8 ? slice / 256 : 8;
+  int64_t w = ((blockIdx.x >> 3) & 15) * slice + (int64_t)tid * stride;
+  w = w < words - 1 ? w : words - 1;
+  return __builtin_bit_cast(uint32_t, cb[(int64_t)m * words + w]);
+}
+
+template <int D>
+__device__ __forceinline__ void enc4_stage(Enc4Shared<D>& s, const Enc4Stage<D>& st,
+                                           const float* __restrict__ cb,
+                                           const float* __restrict__ cn, int m, int K, int row0,
+                                           int N, const RowMap& rm, bool own, int k, int wave,
+                                           int lane) {
+  constexpr int S4 = D / 4, L = D / 16;
+  // ---- coarse pass: lane l, entry k = 64 wave + l, all four rows
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  {
+    const uint16_t* ar = s.rb[lane & 3];
+#pragma unroll
+    for (int t = 0; t < S4; t += 2) {
+      const uint4 aa = *reinterpret_cast<const uint4*>(ar + 4 * t);
+      const uint4 bb = st.b[t / 2];
+      acc0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+          __builtin_bit_cast(bf16x4_t, make_uint2(aa.x, aa.y)),
+          __builtin_bit_cast(bf16x4_t, make_uint2(bb.x, bb.y)), acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+          __builtin_bit_cast(bf16x4_t, make_uint2(aa.z, aa.w)),
+          __builtin_bit_cast(bf16x4_t, make_uint2(bb.z, bb.w)), acc1, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < kR4; ++v) {
+    const float rn = s.rn[v];
+    const float srn = __builtin_amdgcn_sqrtf(rn);
+    const float A = rn + st.cn;
+    const float dm = acc0[v] + acc1[v];
+    const float g = A - 2.0f * dm;
+    const float eps = 0x1.02p-6f * (srn * st.scn) + 0x1p-21f * (fabsf(A) + 2.0f * fabsf(dm)) +
+                      0x1p-116f * (1.0f + srn + st.scn);
+    s.gb[v][k] = own ? make_float2(g - eps, g + eps) : make_float2(INFINITY, INFINITY);
+  }
+  lds_barrier();
+
+  // ---- exact recheck of row v = wave: U = least upper bound over the row
+  const int v = wave, j = lane & 15, grp = lane >> 4;
+  const float2 b0 = s.gb[v][lane], b1 = s.gb[v][64 + lane];
+  const float2 b2 = s.gb[v][128 + lane], b3 = s.gb[v][192 + lane];
+  const float U = wave_min64(fminf(fminf(b0.y, b1.y), fminf(b2.y, b3.y)));
+  uint64_t mk0 = __ballot(lane < K && !(b0.x > U));
+  uint64_t mk1 = __ballot(64 + lane < K && !(b1.x > U));
+  uint64_t mk2 = __ballot(128 + lane < K && !(b2.x > U));
+  uint64_t mk3 = __ballot(192 + lane < K && !(b3.x > U));
+  float rc[L];
+#pragma unroll
+  for (int t = 0; t < L; t += 4) {
+    const float4 x = *reinterpret_cast<const float4*>(&s.r[v][j * L + t]);
+    rc[t] = x.x;
+    rc[t + 1] = x.y;
+    rc[t + 2] = x.z;
+    rc[t + 3] = x.w;
+  }
+  const float rn = s.rn[v];
+  float bc[L];
+#pragma unroll
+  for (int t = 0; t < L; ++t) bc[t] = 0.f;
+  float best = 0.f;
+  int bk = -1;
+  // Batches of four survivors, one per group, lowest entries first.  Ties go
+  // to the lowest entry; NaN and +inf never win.
+  while (mk0 | mk1 | mk2 | mk3) {
+    const int q0 = pop_lowest(mk0, mk1, mk2, mk3);
+    const int q1 = pop_lowest(mk0, mk1, mk2, mk3);
+    const int q2 = pop_lowest(mk0, mk1, mk2, mk3);
+    const int q3 = pop_lowest(mk0, mk1, mk2, mk3);
+    const int kq = grp == 0 ? q0 : grp == 1 ? q1 : grp == 2 ? q2 : q3;
+    if (kq >= 0) {
+      const float* cr = cb + ((int64_t)m * K + kq) * D + j * L;
+      float c[L];
+#pragma unroll
+      for (int t = 0; t < L; t += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(cr + t);
+        c[t] = x.x;
+        c[t + 1] = x.y;
+        c[t + 2] = x.z;
+        c[t + 3] = x.w;
+      }
+      const float cnk = cn[(int64_t)m * K + kq];
+      float dot = 0.f;
+#pragma unroll
+      for (int t = 0; t < L; ++t) dot = __builtin_fmaf(rc[t], c[t], dot);
+      dot = row_fold16(dot);
+      const float E = (rn + cnk) - 2.0f * dot;
+      if (!(E != E) && E != INFINITY && (bk < 0 || E < best || (E == best && kq < bk))) {
+        best = E;
+        bk = kq;
+#pragma unroll
+        for (int t = 0; t < L; ++t) bc[t] = c[t];
+      }
+    }
+  }
+  // the winning group: lowest (E, entry) over the four groups' bests
+  int gw = -1, code = 0;
+  float ew = 0.f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int kg = __builtin_amdgcn_readlane(bk, 16 * g);
+    const float eg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, best), 16 * g));
+    if (kg >= 0 && (gw < 0 || eg < ew || (eg == ew && kg < code))) {
+      gw = g;
+      ew = eg;
+      code = kg;
+    }
+  }
+  if (gw < 0) {  // no finite distance: code 0, as the strict-< scan from +inf leaves it
+    gw = 0;
+    if (grp == 0) {
+      const float* cr = cb + (int64_t)m * K * D + j * L;
+#pragma unroll
+      for (int t = 0; t < L; ++t) bc[t] = cr[t];
+    }
+  }
+  if (grp == gw) {
+    float a2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < L; t += 4) {
+      float4 r4;
+      r4.x = rc[t] - bc[t];
+      r4.y = rc[t + 1] - bc[t + 1];
+      r4.z = rc[t + 2] - bc[t + 2];
+      r4.w = rc[t + 3] - bc[t + 3];
+      *reinterpret_cast<float4*>(&s.r[v][j * L + t]) = r4;
+      *reinterpret_cast<uint2*>(&s.rb[v][j * L + t]) = bf16x4_bits(r4);
+      a2 = __builtin_fmaf(r4.x, r4.x, a2);
+      a2 = __builtin_fmaf(r4.y, r4.y, a2);
+      a2 = __builtin_fmaf(r4.z, r4.z, a2);
+      a2 = __builtin_fmaf(r4.w, r4.w, a2);
+    }
+    a2 = row_fold16(a2);
+    if (j == 0) {
+      s.rn[v] = a2;
+      if (m < kCodeStage) s.code[v][m] = (uint8_t)code;
+      else if (row0 + v < N && rm.live(row0 + v)) rm.crow(row0 + v)[m] = (uint8_t)code;
+    }
+  }
+  lds_barrier();
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void encode_mfma4_kernel(
+    RowMap rm, int N, const float* __restrict__ cb, int M, int K,
+    const uint4* __restrict__ frag4, const float* __restrict__ cn,
+    const float* __restrict__ scn, float* __restrict__ rnorm) {
+  constexpr int L = D / 16;
+  __shared__ __attribute__((aligned(16))) Enc4Shared<D> s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * kR4;
+  const int NQ = (K + 63) / 64;
+  const int qc = wave < NQ ? wave : NQ - 1;
+  if (rm.ranges) {  // a workgroup with no live row leaves at once (same test in every thread)
+    bool any = false;
+    for (int r = 0; r < kR4; ++r) any = any || (row0 + r < N && rm.live(row0 + r));
+    if (!any) return;
+  }
+  const int k = wave * 64 + lane;
+  const bool own = k < K;
+  const int kc = own ? k : K - 1;  // dead lanes load entry K - 1 (in bounds, ignored)
+  // Stage 0's operands are requested first, so that they arrive with the
+  // rows; stage m + 1's before stage m runs (unconditionally, the last stage
+  // re-requesting itself, so that the compiler's wait counts stay exact).
+  Enc4Stage<D> st0, st1;
+  enc4_load_stage<D>(st0, frag4, cn, scn, 0, NQ, K, qc, kc, lane);
+  for (int i = tid; i < kR4 * D; i += 256) {
+    const int r = i / D, d = i - r * D;
+    const float x = (row0 + r < N && rm.live(row0 + r)) ? rm.xval(row0 + r, d) : 0.f;
+    s.r[r][d] = x;
+    s.rb[r][d] = __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  lds_barrier();
+  if (lane < 16) {  // wave v: dot16 norm of row v
+    const float* rr = s.r[wave] + lane * L;
+    float a2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < L; ++t) a2 = __builtin_fmaf(rr[t], rr[t], a2);
+    a2 = row_fold16(a2);
+    if (lane == 0) s.rn[wave] = a2;
+  }
+  lds_barrier();
+
+  for (int m = 0; m < M; m += 2) {
+    enc4_load_stage<D>(st1, frag4, cn, scn, min(m + 1, M - 1), NQ, K, qc, kc, lane);
+    enc4_stage<D>(s, st0, cb, cn, m, K, row0, N, rm, own, k, wave, lane);
+    if (m + 1 >= M) break;
+    enc4_load_stage<D>(st0, frag4, cn, scn, min(m + 2, M - 1), NQ, K, qc, kc, lane);
+    enc4_stage<D>(s, st1, cb, cn, m + 1, K, row0, N, rm, own, k, wave, lane);
+  }
+  const int mc = M < kCodeStage ? M : kCodeStage;
+  for (int i = tid; i < kR4 * mc; i += 256) {
+    const int r = i / mc, mm = i - r * mc;
+    if (row0 + r < N && rm.live(row0 + r)) rm.crow(row0 + r)[mm] = s.code[r][mm];
+  }
+  if (tid < kR4 && rnorm && row0 + tid < N && rm.live(row0 + tid))
     rnorm[row0 + tid] = sqrtf(s.rn[tid]);
 }
 
@@ -896,6 +1236,10 @@ extern "C" int lap_encode_prepare(const float* codebooks, int M, int K, int D, v
     hipLaunchKernelGGL(encode_prep_frag, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        codebooks, M, K, D, p.frag);
     LAP_LAUNCH_CHECK("encode_prep_frag");
+    const int64_t n4 = (int64_t)M * ((K + 63) / 64) * (D / 8) * 64;
+    hipLaunchKernelGGL(encode_prep_frag4, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                       codebooks, M, K, D, p.frag4);
+    LAP_LAUNCH_CHECK("encode_prep_frag4");
   }
   return LAP_OK;
 }
@@ -914,6 +1258,20 @@ static bool encode_use_tile(int N, int D, int K) {
   DevInfo di;
   const int cus = device_info(&di) == LAP_OK ? di.cu_count : 256;
   return (int64_t)N >= (int64_t)kTileRows * 2 * cus;
+}
+
+// Small encodes (decode flushes) take the 4-row kernel while its workgroups
+// fit twice over on the chip; larger ones the 16-row kernel.
+// LAPRUNE_ENCODE_ROWS=4|16 forces the choice (D = 64 or 128); read at every
+// call, so that one process can run both.
+static bool encode_use_rows4(int N, int D) {
+  if (!(D == 64 || D == 128)) return false;
+  const char* e = getenv("LAPRUNE_ENCODE_ROWS");
+  const int forced = e ? atoi(e) : 0;
+  if (forced == 4 || forced == 16) return forced == 4;
+  DevInfo di;
+  const int cus = device_info(&di) == LAP_OK ? di.cu_count : 256;
+  return (int64_t)(N + kR4 - 1) / kR4 <= 2 * (int64_t)cus;
 }
 
 // Shared checks and launch of both encode entry points.
@@ -947,6 +1305,18 @@ static int run_encode(const RowMap& rm, int N, int D, const float* codebooks, in
                          sizeof(TileShared<128>), st, rm, N, codebooks, M, K, fr, p.cn, p.scn,
                          resid_norm);
     LAP_LAUNCH_CHECK("encode_tile_kernel");
+    return LAP_OK;
+  }
+  if (K % 16 == 0 && encode_impl_mfma() && encode_use_rows4(N, D)) {
+    dim3 g4((N + kR4 - 1) / kR4);
+    const uint4* fr = reinterpret_cast<const uint4*>(p.frag4);
+    if (D == 64)
+      hipLaunchKernelGGL(encode_mfma4_kernel<64>, g4, dim3(256), 0, st, rm, N, codebooks, M, K,
+                         fr, p.cn, p.scn, resid_norm);
+    else
+      hipLaunchKernelGGL(encode_mfma4_kernel<128>, g4, dim3(256), 0, st, rm, N, codebooks, M, K,
+                         fr, p.cn, p.scn, resid_norm);
+    LAP_LAUNCH_CHECK("encode_mfma4_kernel");
     return LAP_OK;
   }
   if (K % 16 == 0 && encode_impl_mfma()) {

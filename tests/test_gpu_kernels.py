@@ -429,7 +429,7 @@ def test_encode_bit_exact(dev, K, orc, N, D):
     assert np.array_equal(rn.cpu().numpy()[rows].view(np.uint32), want_r.view(np.uint32))
 
 
-def test_encode_c3_config(dev, K, orc):
+def test_encode_c3_config(dev, K, orc, encode_rows):
     """BASELINE config C3 exactly: 8 KV heads x 64 post-RoPE keys (pre-RoPE
     bf16 N(0,1) x per-channel U(0.5, 4), rotate-half RoPE with theta 500000
     at positions 131008..131071), 32 x 256 fp32 codebooks N(0, 0.02):
@@ -453,8 +453,29 @@ def test_encode_c3_config(dev, K, orc):
     assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
 
 
+@pytest.fixture(params=["4", "16"])
+def encode_rows(request, monkeypatch):
+    """Runs a test on the 4-row and on the 16-row workgroup kernel (small
+    encodes take the 4-row one by default)."""
+    monkeypatch.setenv("LAPRUNE_ENCODE_ROWS", request.param)
+    return int(request.param)
+
+
+@pytest.mark.parametrize("N,D", [(512, 128), (37, 64), (2048, 128)])
+def test_encode_both_small_kernels(dev, K, orc, N, D, encode_rows):
+    g = _gen(150 + N)
+    M, Kc = 32, 256
+    x = torch.randn(N, D, generator=g) * (torch.rand(D, generator=g) * 3.5 + 0.5)
+    cb = torch.randn(M, Kc, D, generator=g) * 0.02
+    codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
+    torch.cuda.synchronize()
+    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
+    assert np.array_equal(codes.cpu().numpy(), want_c)
+    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+
+
 @pytest.mark.parametrize("Kc,D", [(60, 64), (48, 128), (16, 64), (240, 128)])
-def test_encode_bit_exact_entry_counts(dev, K, orc, Kc, D):
+def test_encode_bit_exact_entry_counts(dev, K, orc, Kc, D, encode_rows):
     """K % 16 != 0 takes the all-VALU search, the rest the MFMA search with
     fewer entry tiles than waves."""
     g = _gen(120 + Kc)
@@ -468,7 +489,7 @@ def test_encode_bit_exact_entry_counts(dev, K, orc, Kc, D):
     assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
 
 
-def test_encode_ties_and_near_ties(dev, K, orc):
+def test_encode_ties_and_near_ties(dev, K, orc, encode_rows):
     """Duplicate entries (exact ties: the lowest index must win) and entries a
     few ulps apart, far inside the bf16 coarse error, so the exact recheck
     decides."""
@@ -492,7 +513,7 @@ def test_encode_ties_and_near_ties(dev, K, orc):
     assert 40 not in set(codes.cpu().numpy().ravel().tolist())  # ties go to entry 7
 
 
-def test_encode_non_finite_rows(dev, K, orc):
+def test_encode_non_finite_rows(dev, K, orc, encode_rows):
     """Rows whose norms overflow or hold NaN take the full exact scan and
     follow the contract (NaN and +inf distances never win; no finite
     distance gives code 0)."""
