@@ -13,6 +13,7 @@ import threading
 import torch
 
 from .. import _native as N
+from .._ops import ops
 
 _ws_lock = threading.Lock()
 _ws_cache: dict = {}
@@ -66,8 +67,7 @@ def aq_lut_build(q: torch.Tensor, codebooks: torch.Tensor, G: int = 1,
         _check(G > 0 and Hq % G == 0, f"Hq={Hq} not divisible by G={G}")
         out = torch.empty((Hq // G, M, K, G), dtype=torch.float16, device=q.device)
     with _device_guard(q):
-        N.call("lap_lut_build", N.ptr(q), N.dtype_code(q.dtype), q.stride(0), N.ptr(cb),
-               N.dtype_code(cb.dtype), Hq, D, M, K, G, lay, N.ptr(out), N.stream_of(q))
+        ops().lut_build(q, cb, G, lay, out)
     return out
 
 
@@ -92,8 +92,7 @@ def aq_lut_gather_grouped(lut: torch.Tensor, codes: torch.Tensor, G: int,
         return out
     _check(grid_y_cap > 0, "grid_y_cap must be positive")
     with _device_guard(lut):
-        N.call("lap_lut_score_grouped", N.ptr(lut_c), N.LUT_HMK, N.ptr(codes), codes.stride(0),
-               codes.stride(1), Hkv, G, T, M, K, N.ptr(out), N.stream_of(lut))
+        ops().score_grouped(lut_c, N.LUT_HMK, codes, G, M, K, out)
     return out
 
 

@@ -2,8 +2,10 @@
 
 Compiles every ``laprune_amd/csrc/*.hip`` with hipcc for gfx950 into
 ``laprune_amd/_lib/liblaprune_hip.so`` (in-tree, so the built library travels
-with the source tree).  No torch extension machinery is involved: the Python
-side binds the C ABI with ctypes.
+with the source tree), then ``csrc/torch_ops.cpp`` (host code: torch custom
+ops over the C ABI) with hipcc against the installed torch headers into
+``laprune_amd/_lib/liblaprune_torch.so``.  No torch extension machinery
+(cpp_extension, hipify) is involved.
 """
 from __future__ import annotations
 
@@ -45,6 +47,34 @@ def lib_path() -> Path:
     return LIBDIR / LIBNAME
 
 
+TORCH_LIBNAME = "liblaprune_torch.so"
+
+
+def torch_lib_path() -> Path:
+    return LIBDIR / TORCH_LIBNAME
+
+
+def build_torch_ops() -> Path:
+    """Compile the torch op binding (host C++) against the installed torch
+    and link it to liblaprune_hip.so (found next to it at load time)."""
+    import torch
+    tp = Path(torch.__file__).resolve().parent
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = LIBDIR / (TORCH_LIBNAME + ".tmp")
+    cmd = [hipcc(), "-x", "c++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-I/opt/rocm/include", f"-I{tp / 'include'}",
+           f"-I{tp / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+           str(CSRC / "torch_ops.cpp"), "-o", str(tmp),
+           f"-L{tp / 'lib'}", "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_hip",
+           f"-L{LIBDIR}", "-llaprune_hip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tp / 'lib'}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch op binding failed to build:\n{res.stderr}")
+    os.replace(tmp, torch_lib_path())
+    return torch_lib_path()
+
+
 def _compile(src: Path, obj: Path) -> None:
     cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -77,8 +107,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, lib_path())
+    build_torch_ops()
     if verbose:
-        print(f"built {lib_path()}")
+        print(f"built {lib_path()} and {torch_lib_path()}")
     return lib_path()
 
 

@@ -27,6 +27,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as N
+from ._ops import ops
 from .aq_kernels import aq_encode_prepare
 
 
@@ -267,12 +268,7 @@ class DecodeKVCache:
             raise RuntimeError("rope_append: pos must be int64 with one position per sequence")
         if q_out.shape != (B, Hq, D) or not q_out.is_contiguous() or q_out.dtype != self.dtype:
             raise RuntimeError("rope_append: q_out must be a contiguous [B, Hq, D] tensor")
-        N.call("lap_rope_append", N.ptr(q), q.stride(0), D, N.ptr(k), k.stride(0), D, N.ptr(v),
-               v.stride(0), D, N.ptr(cos), N.ptr(sin), cos.stride(0), N.dtype_code(self.dtype),
-               B, Hq, self.Hkv, D, N.ptr(pos), N.ptr(self.k), self.k.stride(0),
-               self.k.stride(1), self.k.stride(2), N.ptr(self.v), self.v.stride(0),
-               self.v.stride(1), self.v.stride(2), self.capacity, N.ptr(q_out),
-               N.stream_of(q_out))
+        ops().rope_append(q, k, v, cos, sin, pos, self.k, self.v, self.capacity, q_out)
         return q_out.unsqueeze(2)
 
     def encode_ranges(self, ranges: torch.Tensor) -> None:
@@ -280,12 +276,10 @@ class DecodeKVCache:
         group_size tokens; empty ranges cost a workgroup exit)."""
         if self.cb is None:
             return
-        k, c = self.k, self.codes
-        N.call("lap_encode_keys_ranges", N.ptr(k), N.dtype_code(k.dtype), k.stride(0),
-               k.stride(1), k.stride(2), self.B, self.Hkv, N.ptr(ranges), self.group_size,
-               self.capacity, self.D, N.ptr(self.cb), self.M, self.K, N.ptr(self.prep),
-               self.prep.numel(),
-               N.ptr(c), c.stride(0), c.stride(1), c.stride(2), N.stream_of(k))
+        if self.k.shape[:2] != (self.B, self.Hkv) or self.k.shape[3] != self.D:
+            raise RuntimeError("encode_ranges: key cache shape changed")
+        ops().encode_keys_ranges(self.k, ranges, self.group_size, self.capacity, self.cb,
+                                 self.prep, self.codes)
 
     def keys(self) -> torch.Tensor:
         return self.k[:, :, :self.length]

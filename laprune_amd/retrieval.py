@@ -33,6 +33,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _native as N
+from ._ops import ops
 
 
 @dataclass
@@ -195,6 +196,7 @@ class SparseDecoder:
         ws = N.size_query("lap_decode_step_workspace_size", batch, num_q_heads, num_kv_heads,
                           max(max_tokens, 1), head_dim, self.max_keep, self.key_mode)
         self.ws = torch.zeros(max(ws, 1), dtype=torch.uint8, device=self.dev)
+        self._ops = ops()
         self.last_k = 0
         self._plans = None
         self._plan_key = None
@@ -249,30 +251,24 @@ class SparseDecoder:
         if t_total > self.T_max or t_codes > t_total:
             raise RuntimeError("cache length exceeds the decoder's max_tokens")
         p = self.plan(t_codes, t_total)
-        st = N.stream_of(q)
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
-        N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
-               N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
-               N.ptr(self.lut), st)
+        self._ops.lut_build(qf, self.cb, 4, N.LUT_GMKG, self.lut)
         self.last_k = p["k"]
-        self._decode_step(q, codes, keys, vals, max(t_codes, 1), t_total, p, None, 0, 0, 0, st)
+        self._decode_step(q, codes, keys, vals, max(t_codes, 1), t_total, p, None, 0, 0, 0)
         return self.out.unsqueeze(2)
 
     def _decode_step(self, q, codes, keys, vals, T, T_kv, p, plans, k_cols, max_sink,
-                     max_tail, st) -> None:
-        """lap_decode_step: scoring, top-k and sparse attention after the LUT
-        (one launch for group selection, the kernel chain otherwise)."""
-        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
+                     max_tail) -> None:
+        """lap_decode_step (through the compiled torch op): scoring, top-k
+        and sparse attention after the LUT (one launch for group selection,
+        the kernel chain otherwise)."""
         if p is None:
             p = dict(cand_start=0, cand_end=0, k=0, sink=0, tail_start=0, tail_count=0)
-        N.call("lap_decode_step", N.ptr(self.lut), N.ptr(codes), codes.stride(0), codes.stride(1),
-               codes.stride(2), T, p["cand_start"], p["cand_end"], p["k"], p["sink"],
-               p["tail_start"], p["tail_count"], N.ptr(plans), k_cols, max_sink, max_tail,
-               self.key_mode, N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys), N.ptr(vals),
-               N.dtype_code(q.dtype), B, Hq, Hkv, T_kv, D, keys.stride(0), keys.stride(1),
-               keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
-               1.0 / math.sqrt(D), N.ptr(self.idx), N.I32, N.ptr(self.out), N.ptr(self.ws),
-               self.ws.numel(), st)
+        keys, vals = keys[:, :, :T_kv], vals[:, :, :T_kv]
+        self._ops.decode_step(self.lut, codes, T, p["cand_start"], p["cand_end"], p["k"],
+                              p["sink"], p["tail_start"], p["tail_count"], plans, k_cols,
+                              max_sink, max_tail, self.key_mode, q, keys, vals,
+                              1.0 / math.sqrt(self.D), self.idx, self.out, self.ws)
 
     def fused_status(self) -> tuple[int, int]:
         """(rows whose workgroups spread over XCDs, barrier time-outs) of
@@ -301,18 +297,15 @@ class SparseDecoder:
             self._plans.upload([tuple(p[f] for f in PLAN_FIELDS) for p in plans])
             self._plan_key = key
         pdev = self._plans.dev
-        st = N.stream_of(q)
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
-        N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
-               N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
-               N.ptr(self.lut), st)
+        self._ops.lut_build(qf, self.cb, 4, N.LUT_GMKG, self.lut)
         k_cols = max(p["k"] for p in plans)
         T = max(max(t_codes), 1)
         self.last_k = k_cols
         max_sink = max(p["sink"] for p in plans)
         max_tail = max(p["tail_count"] for p in plans)
         self._decode_step(q, codes, keys, vals, T, keys.shape[2], None, pdev, k_cols, max_sink,
-                          max_tail, st)
+                          max_tail)
         return self.out.unsqueeze(2)
 
     @property
@@ -335,15 +328,12 @@ class SparseDecoder:
             q = q[:, :, 0, :]
         B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
         T = min(codes.shape[2], self.T_max)
-        st = N.stream_of(q)
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
-        N.call("lap_lut_build", N.ptr(qf), N.dtype_code(qf.dtype), qf.stride(0), N.ptr(self.cb),
-               N.dtype_code(self.cb.dtype), B * Hq, D, self.M, self.K, 4, N.LUT_GMKG,
-               N.ptr(self.lut), st)
+        self._ops.lut_build(qf, self.cb, 4, N.LUT_GMKG, self.lut)
         k_cols = self.k_cols
         self.last_k = k_cols
         self._decode_step(q, codes, keys, vals, T, keys.shape[2], None, plans, k_cols,
-                          self.cfg.sink_size, self.max_tail, st)
+                          self.cfg.sink_size, self.max_tail)
         return self.out.unsqueeze(2)
 
     @torch.no_grad()
@@ -372,6 +362,7 @@ class DenseDecoder:
         ws = N.size_query("lap_attn_decode_workspace_size", batch, num_q_heads, head_dim,
                           max(max_tokens, 1))
         self.ws = torch.empty(max(ws, 1), dtype=torch.uint8, device=device)
+        self._ops = ops()
         self._plans = None
         self._plan_key = None
 
@@ -394,12 +385,8 @@ class DenseDecoder:
                 self._plans.upload([(t, t, 0, 0, 0, 0, 0, t) for t in rows])
                 self._plan_key = tuple(rows)
             pdev = self._plans.dev
-            N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1),
-                   N.ptr(keys), N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D,
-                   keys.stride(0), keys.stride(1), keys.stride(2), vals.stride(0),
-                   vals.stride(1), vals.stride(2), None, N.I32, Hkv, 0, N.ptr(pdev), 0,
-                   max(rows), 1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws),
-                   self.ws.numel(), N.stream_of(q))
+            self._ops.attn_decode_ragged(q, keys, vals, None, Hkv, 0, pdev, 0, max(rows),
+                                         1.0 / math.sqrt(D), self.out, self.ws)
             return self.out.unsqueeze(2)
         return self._dense_uniform(q, keys, vals)
 
@@ -413,20 +400,10 @@ class DenseDecoder:
             q = q[:, :, 0, :]
         B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
         T = keys.shape[2]
-        N.call("lap_sparse_attn_decode_ragged", N.ptr(q), q.stride(0), q.stride(1),
-               N.ptr(keys), N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D,
-               keys.stride(0), keys.stride(1), keys.stride(2), vals.stride(0),
-               vals.stride(1), vals.stride(2), None, N.I32, Hkv, 0, N.ptr(plans), 0, T,
-               1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws), self.ws.numel(),
-               N.stream_of(q))
+        self._ops.attn_decode_ragged(q, keys, vals, None, Hkv, 0, plans, 0, T,
+                                     1.0 / math.sqrt(D), self.out, self.ws)
         return self.out.unsqueeze(2)
 
     def _dense_uniform(self, q, keys, vals):
-        B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
-        T = keys.shape[2]
-        N.call("lap_dense_attn_decode", N.ptr(q), q.stride(0), q.stride(1), N.ptr(keys),
-               N.ptr(vals), N.dtype_code(q.dtype), B, Hq, Hkv, T, D, keys.stride(0),
-               keys.stride(1), keys.stride(2), vals.stride(0), vals.stride(1), vals.stride(2),
-               1.0 / math.sqrt(D), N.ptr(self.out), N.ptr(self.ws), self.ws.numel(),
-               N.stream_of(q))
+        self._ops.dense_decode(q, keys, vals, 1.0 / math.sqrt(self.D), self.out, self.ws)
         return self.out.unsqueeze(2)

@@ -159,3 +159,23 @@ def test_decode_step_argument_checks(lib):
     assert lib.lap_decode_step_workspace_size(1, 32, 8, 1024, 128, 132, N.KEY_BF16,
                                               C.byref(need)) == N.LAP_OK
     assert need.value > 0
+
+
+def test_torch_binding_registers_the_hot_ops():
+    """The compiled torch binding loads (no GPU needed) and registers one op
+    per hot entry point, each with its schema."""
+    from laprune_amd._ops import ops
+    o = ops()
+    want = {
+        "lut_build": "Tensor q, Tensor codebooks, int G, int layout, Tensor(a!) out",
+        "decode_step": "Tensor lut, Tensor? codes, int T,",
+        "dense_decode": "Tensor q, Tensor keys, Tensor vals, float scale",
+        "attn_decode_ragged": "Tensor? idx, int H_idx, int k_cols, Tensor plans",
+        "rope_append": "Tensor cos, Tensor sin, Tensor pos",
+        "encode_keys_ranges": "Tensor keys, Tensor ranges, int max_len, int t_cap",
+        "score_grouped": "Tensor lut, int layout, Tensor codes, int G",
+    }
+    for name, frag in want.items():
+        schema = str(getattr(o, name).default._schema)
+        assert schema.startswith(f"laprune::{name}("), schema
+        assert frag in schema, (name, schema)
