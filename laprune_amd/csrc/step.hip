@@ -634,6 +634,16 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   float* sw = sl + kMaxWR * kG;       // [kMaxWR * 4] weights (0 past WR)
   float* stl = sw + kMaxWR * kG;      // [4] sum of l * weight
   float* so = stl + kG;               // [kTH] half sums of o
+  // o's loads go out with (m, l)'s, so the merge waits for one round trip
+  constexpr int kHalf = kMaxWR / 2;
+  const int half = tid / (kG * kDh), e = tid % (kG * kDh);
+  const int g_o = e / kDh, d_o = e - g_o * kDh;
+  float v[kHalf];
+#pragma unroll
+  for (int u = 0; u < kHalf; ++u) {
+    const int s2 = min(half * kHalf + u, a.WR - 1);
+    v[u] = ld_dev(rp + ((int64_t)s2 * kG + g_o) * (kDh + 2) + 2 + d_o);
+  }
   if (tid < kMaxWR * kG) {
     const bool in = tid < a.WR * kG;
     sm[tid] = in ? ld_dev(rp + (int64_t)tid * (kDh + 2)) : -INFINITY;
@@ -653,18 +663,10 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     stl[tid] = l;
   }
   {
-    constexpr int kHalf = kMaxWR / 2;
-    const int half = tid / (kG * kDh), e = tid % (kG * kDh);
-    const int g = e / kDh, d = e - g * kDh;
-    float v[kHalf];
-#pragma unroll
-    for (int u = 0; u < kHalf; ++u) {
-      const int s2 = min(half * kHalf + u, a.WR - 1);
-      v[u] = ld_dev(rp + ((int64_t)s2 * kG + g) * (kDh + 2) + 2 + d);
-    }
     float o = 0.f;
 #pragma unroll
-    for (int u = 0; u < kHalf; ++u) o = __builtin_fmaf(v[u], sw[(half * kHalf + u) * kG + g], o);
+    for (int u = 0; u < kHalf; ++u)
+      o = __builtin_fmaf(v[u], sw[(half * kHalf + u) * kG + g_o], o);
     so[tid] = o;
   }
   __syncthreads();
