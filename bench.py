@@ -404,6 +404,38 @@ def ragged_leg(args, dev, cb) -> dict:
     }
 
 
+def _graph_us(body, n: int, reps: int, stream) -> float:
+    """Per-call time of `body(j)`, j < n, captured back to back in one graph
+    and replayed `reps` times (HIP events on the launch stream)."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for j in range(n):
+            body(j)
+    g.replay()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) * 1e3 / (reps * n)
+
+
+def score_floors(score_only, stream, reps: int) -> dict:
+    """Where the scorer's time goes: the same launch replayed on one code set,
+    whose 32 MiB then stay in the 256 MB Infinity Cache, takes HBM out of the
+    loop; what remains is the kernel's own compute, LDS and launch cost."""
+    one_set = _graph_us(lambda j: score_only(0), N_CODE_SETS, reps, stream)
+    return {"same_set_us": round(one_set, 3),
+            "hbm_floor_us": round(CODE_BYTES / (HBM_PEAK_GBS * 1e3), 3),
+            "note": ("same_set_us: the scorer launch replayed on one code set "
+                     "(Infinity-Cache resident), graph-replayed back to back like "
+                     "score_kernel_us; hbm_floor_us: the code bytes at the 8 TB/s peak")}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -572,6 +604,7 @@ def main():
     torch.cuda.synchronize()
     score_us = ev0.elapsed_time(ev1) * 1e3 / (reps * n_sets)
     score_gbs = CODE_BYTES / (score_us * 1e-6) / 1e9
+    floors = None if args.eager else score_floors(score_only, stream, reps)
 
     # ---- C3 encode: one flush of 512 post-RoPE key rows (HIP events)
     log("timing the C3 encode")
@@ -626,6 +659,7 @@ def main():
         "sdpa_step_us": None if sdpa_s is None else round(sdpa_s * 1e6, 2),
         "speedup_vs_sdpa": None if sdpa_s is None else round(sdpa_s / sparse_s, 3),
         "score_kernel_us": round(score_us, 3),
+        "score_floors": floors,
         "selection_check": ok,
         "encode": {
             "workload": "C3: 8 KV heads x 64-token flush = 512 post-RoPE key rows, D=128, "
