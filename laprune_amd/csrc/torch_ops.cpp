@@ -46,6 +46,20 @@ void check(int status, const char* fn) {
 void* ptr(const at::Tensor& t) { return t.data_ptr(); }
 void* ptr(const std::optional<at::Tensor>& t) { return t ? t->data_ptr() : nullptr; }
 
+// Every tensor of a call on the GPU, on one device: the dispatcher routes a
+// call with any GPU tensor here, and a host pointer handed to a kernel
+// would fault.
+void same_gpu(const char* op, std::initializer_list<const at::Tensor*> ts) {
+  const at::Tensor* first = nullptr;
+  for (const at::Tensor* t : ts) {
+    if (!t) continue;
+    TORCH_CHECK(t->is_cuda(), op, ": every tensor must be on the GPU");
+    if (!first) first = t;
+    TORCH_CHECK(t->device() == first->device(), op, ": tensors on different devices");
+  }
+}
+const at::Tensor* opt(const std::optional<at::Tensor>& t) { return t ? &*t : nullptr; }
+
 // q [Hq, D] (row stride free), codebooks [M, K, D] contiguous -> out (fp16
 // table, layout LAP_LUT_HMK or LAP_LUT_GMKG).  Replaces the reference's
 // torch.matmul LUT (laprune/llm/aq_kv.py:681-682).
@@ -54,6 +68,7 @@ void lut_build(const at::Tensor& q, const at::Tensor& cb, int64_t G, int64_t lay
   TORCH_CHECK(q.dim() == 2 && cb.dim() == 3 && q.stride(1) == 1 && cb.is_contiguous() &&
                   out.is_contiguous(),
               "laprune::lut_build: q [Hq, D] with unit inner stride, contiguous codebooks and out");
+  same_gpu("laprune::lut_build", {&q, &cb, &out});
   check(lap_lut_build(ptr(q), dtype_code(q), q.stride(0), ptr(cb), dtype_code(cb),
                       (int)q.size(0), (int)q.size(1), (int)cb.size(0), (int)cb.size(1), (int)G,
                       (int)layout, ptr(out), stream_of(q)),
@@ -72,6 +87,9 @@ void decode_step(const at::Tensor& lut, const std::optional<at::Tensor>& codes, 
                  const at::Tensor& ws) {
   TORCH_CHECK(q.dim() == 3 && keys.dim() == 4 && vals.dim() == 4,
               "laprune::decode_step: q [B, Hq, D], keys / vals [B, Hkv, T, D]");
+  same_gpu("laprune::decode_step", {&lut, opt(codes), opt(plans), &q, &keys, &vals, &idx, &out, &ws});
+  TORCH_CHECK(!codes || codes->scalar_type() == at::kByte, "laprune::decode_step: u8 codes");
+  TORCH_CHECK(!plans || plans->scalar_type() == at::kInt, "laprune::decode_step: int32 plans");
   const int64_t cs_b = codes ? codes->stride(0) : 0, cs_h = codes ? codes->stride(1) : 0,
                 cs_t = codes ? codes->stride(2) : 0;
   check(lap_decode_step(ptr(lut), codes ? static_cast<const uint8_t*>(codes->data_ptr()) : nullptr,
@@ -90,6 +108,9 @@ void decode_step(const at::Tensor& lut, const std::optional<at::Tensor>& codes, 
 // Dense split-K decode over all T keys (the comparator of record).
 void dense_decode(const at::Tensor& q, const at::Tensor& keys, const at::Tensor& vals,
                   double scale, const at::Tensor& out, const at::Tensor& ws) {
+  TORCH_CHECK(q.dim() == 3 && keys.dim() == 4 && vals.dim() == 4,
+              "laprune::dense_decode: q [B, Hq, D], keys / vals [B, Hkv, T, D]");
+  same_gpu("laprune::dense_decode", {&q, &keys, &vals, &out, &ws});
   check(lap_dense_attn_decode(ptr(q), q.stride(0), q.stride(1), ptr(keys), ptr(vals),
                               dtype_code(q), (int)q.size(0), (int)q.size(1), (int)keys.size(1),
                               (int)keys.size(2), (int)q.size(2), keys.stride(0), keys.stride(1),
@@ -104,6 +125,9 @@ void attn_decode_ragged(const at::Tensor& q, const at::Tensor& keys, const at::T
                         const std::optional<at::Tensor>& idx, int64_t H_idx, int64_t k_cols,
                         const at::Tensor& plans, int64_t max_sink, int64_t max_tail,
                         double scale, const at::Tensor& out, const at::Tensor& ws) {
+  TORCH_CHECK(q.dim() == 3 && keys.dim() == 4 && vals.dim() == 4,
+              "laprune::attn_decode_ragged: q [B, Hq, D], keys / vals [B, Hkv, T, D]");
+  same_gpu("laprune::attn_decode_ragged", {&q, &keys, &vals, opt(idx), &plans, &out, &ws});
   check(lap_sparse_attn_decode_ragged(
             ptr(q), q.stride(0), q.stride(1), ptr(keys), ptr(vals), dtype_code(q),
             (int)q.size(0), (int)q.size(1), (int)keys.size(1), (int)keys.size(2),
@@ -122,6 +146,10 @@ void rope_append(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                  const at::Tensor& cos, const at::Tensor& sin, const at::Tensor& pos,
                  const at::Tensor& cache_k, const at::Tensor& cache_v, int64_t t_cap,
                  const at::Tensor& q_out) {
+  TORCH_CHECK(q_out.dim() == 3 && cache_k.dim() == 4 && cache_v.dim() == 4,
+              "laprune::rope_append: q_out [B, Hq, D], caches [B, Hkv, T, D]");
+  same_gpu("laprune::rope_append", {&q, &k, &v, &cos, &sin, &pos, &cache_k, &cache_v, &q_out});
+  TORCH_CHECK(pos.scalar_type() == at::kLong, "laprune::rope_append: int64 positions");
   const int D = (int)cos.size(-1);
   check(lap_rope_append(ptr(q), q.stride(0), D, ptr(k), k.stride(0), D, ptr(v), v.stride(0), D,
                         ptr(cos), ptr(sin), cos.stride(0), dtype_code(q_out),
@@ -138,6 +166,11 @@ void rope_append(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
 void encode_keys_ranges(const at::Tensor& keys, const at::Tensor& ranges, int64_t max_len,
                         int64_t t_cap, const at::Tensor& cb, const at::Tensor& prep,
                         const at::Tensor& codes) {
+  TORCH_CHECK(keys.dim() == 4 && codes.dim() == 4 && cb.dim() == 3,
+              "laprune::encode_keys_ranges: keys / codes [B, Hkv, T, *], codebooks [M, K, D]");
+  TORCH_CHECK(cb.scalar_type() == at::kFloat, "laprune::encode_keys_ranges: fp32 codebooks");
+  TORCH_CHECK(ranges.scalar_type() == at::kInt, "laprune::encode_keys_ranges: int32 ranges");
+  same_gpu("laprune::encode_keys_ranges", {&keys, &ranges, &cb, &prep, &codes});
   check(lap_encode_keys_ranges(ptr(keys), dtype_code(keys), keys.stride(0), keys.stride(1),
                                keys.stride(2), (int)keys.size(0), (int)keys.size(1),
                                static_cast<const int32_t*>(ptr(ranges)), (int)max_len, (int)t_cap,
@@ -153,6 +186,9 @@ void encode_keys_ranges(const at::Tensor& keys, const at::Tensor& ranges, int64_
 // aq_kernels/aq_lut_gqa.cu:460-534): codes [Hkv, T, M], out fp16 [Hkv*G, T].
 void score_grouped(const at::Tensor& lut, int64_t layout, const at::Tensor& codes, int64_t G,
                    int64_t M, int64_t K, const at::Tensor& out) {
+  TORCH_CHECK(codes.dim() == 3 && codes.scalar_type() == at::kByte,
+              "laprune::score_grouped: codes u8 [Hkv, T, M]");
+  same_gpu("laprune::score_grouped", {&lut, &codes, &out});
   check(lap_lut_score_grouped(ptr(lut), (int)layout, static_cast<const uint8_t*>(ptr(codes)),
                               codes.stride(0), codes.stride(1), (int)codes.size(0), (int)G,
                               (int)codes.size(1), (int)M, (int)K, ptr(out), stream_of(out)),
