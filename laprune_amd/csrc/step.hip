@@ -332,6 +332,11 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     }
   }
   __syncthreads();
+  // The query fragments are waited for here, where nothing else is in
+  // flight: left to the compiler, their first use in A waits for every
+  // global operation issued before it.
+#pragma unroll
+  for (int ks = 0; ks < kDh / 16; ++ks) asm volatile("" : "+v"(qpre[ks]));
   // This chunk's level-1 count of bin tid (the sum of the copies), added to
   // the row's histogram.
   uint32_t h1 = 0;
@@ -373,8 +378,8 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       t2[kL2] = my_gt1;
     }
     wg_row_barrier(a, r, 1);
-    // Every chunk has read the row histogram: clear it for the next call.
-    if (c == 0) a.hist[(int64_t)r * kL1 + tid] = 0u;
+    // Every chunk has read the row histogram; chunk 0 clears it for the next
+    // call once its merge arrival is out (out_stores).
 
     // ------------------------------------------------------------ H2
     // The row's level-2 tables: the threshold tau = (b1, b2), the ties at
@@ -492,7 +497,6 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       if (lane == 0) s_cnt2[j][wave] = (uint32_t)__popcll(ms[j]);
     }
     __syncthreads();
-    const int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols;
     uint32_t sel_base = 0;
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
@@ -504,26 +508,35 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
         all += v;
       }
       const uint32_t q = sel_base + before + lanes_below(ms[j]);
-      if (sel[j] && q < (uint32_t)kKeepMax && base + q < (uint32_t)pr.k) {
-        const int col = t0 + j * kTH + tid;
-        lds.keep[q] = col;
-        if (a.idx_i64) put_idx<int64_t>(a.idx, irow + base + q, col);
-        else put_idx<int32_t>(a.idx, irow + base + q, col);
-      }
+      if (sel[j] && q < (uint32_t)kKeepMax && base + q < (uint32_t)pr.k)
+        lds.keep[q] = t0 + j * kTH + tid;
       sel_base += all;
     }
     n_sel = min(n_sel, (uint32_t)kKeepMax);
   }
-  if (a.plans) {  // ragged rows: pad [k, k_cols) with -1, split over the row's workgroups
-    const int pad = a.k_cols - pr.k;
-    const int ps = (pad + a.WR - 1) / a.WR;
-    const int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols + pr.k;
-    for (int i = c * ps + tid; i < min(pad, (c + 1) * ps); i += kTH) {
-      if (a.idx_i64) put_idx<int64_t>(a.idx, irow + i, -1);
-      else put_idx<int32_t>(a.idx, irow + i, -1);
+  lds_barrier();  // the keep list
+
+  // The stores nothing in this launch reads: this chunk's part of the index
+  // row (from the keep list, which stays in LDS to the end), its share of a
+  // ragged row's -1 padding, and chunk 0's clearing of the row histogram.
+  // They are issued after the merge arrival, so that no wait on the way
+  // there (every wait drains all earlier memory operations) includes them.
+  auto out_stores = [&]() {
+    const int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols;
+    for (int p = tid; p < (int)n_sel && base + (uint32_t)p < (uint32_t)pr.k; p += kTH) {
+      if (a.idx_i64) put_idx<int64_t>(a.idx, irow + base + p, lds.keep[p]);
+      else put_idx<int32_t>(a.idx, irow + base + p, lds.keep[p]);
     }
-  }
-  lds_barrier();  // the keep list; the index stores may still be in flight
+    if (a.plans) {  // ragged rows: pad [k, k_cols) with -1, split over the row's workgroups
+      const int pad = a.k_cols - pr.k;
+      const int ps = (pad + a.WR - 1) / a.WR;
+      for (int i = c * ps + tid; i < min(pad, (c + 1) * ps); i += kTH) {
+        if (a.idx_i64) put_idx<int64_t>(a.idx, irow + pr.k + i, -1);
+        else put_idx<int32_t>(a.idx, irow + pr.k + i, -1);
+      }
+    }
+    if (select && c == 0) a.hist[(int64_t)r * kL1 + tid] = 0u;
+  };
 
   // ---------------------------------------------------------------- A
   // This workgroup attends over its own selection and every WR-th entry
@@ -559,7 +572,7 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane);
     attn_step<DT, kG, kDh>(ws, st, a.scale_log2, lane);
   }
-  lds_barrier();  // the keep list is no longer read; lds.o may follow it
+  lds_barrier();  // every wave's attention is done; lds.o (after the keep list) is free
   {
     const int rq = lane >> 4, cq = lane & 15;
     if (lane < kG) {
@@ -600,7 +613,10 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       pp[2 + d] = o;
     }
   }
-  if (a.WR == 1) return;
+  if (a.WR == 1) {
+    out_stores();
+    return;
+  }
 
   // ---------------------------------------------------------------- E
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -624,7 +640,10 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     s_flag = last ? 1u : 0u;
   }
   __syncthreads();
-  if (!s_flag) return;
+  if (!s_flag) {
+    out_stores();
+    return;
+  }
   // The row's partials: (m, l) of every (split, head) into LDS, the split
   // weights 2^(m - M) per head, then o summed over the splits by two threads
   // per output (each with its splits' loads all in flight).
@@ -645,9 +664,13 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     v[u] = ld_dev(rp + ((int64_t)s2 * kG + g_o) * (kDh + 2) + 2 + d_o);
   }
   if (tid < kMaxWR * kG) {
+    // (m, l) as one 8-byte load (a partial's head record starts 8-byte
+    // aligned): two loads would each be waited for in turn
     const bool in = tid < a.WR * kG;
-    sm[tid] = in ? ld_dev(rp + (int64_t)tid * (kDh + 2)) : -INFINITY;
-    sl[tid] = in ? ld_dev(rp + (int64_t)tid * (kDh + 2) + 1) : 0.f;
+    const int sg = min(tid, a.WR * kG - 1);
+    const uint2 ml = ld_dev2(reinterpret_cast<const uint2*>(rp + (int64_t)sg * (kDh + 2)));
+    sm[tid] = in ? __uint_as_float(ml.x) : -INFINITY;
+    sl[tid] = in ? __uint_as_float(ml.y) : 0.f;
   }
   __syncthreads();
   if (tid < kMaxWR * kG) {
@@ -676,6 +699,7 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     const float l = stl[g];
     a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
   }
+  out_stores();
 }
 
 inline _Float16 f16_one() { return (_Float16)1.0f; }
