@@ -53,13 +53,18 @@ struct KvStep {
   uint4 k[NK];
   uint32_t v[4][NV];
   int tv[4];  // cache rows of keys 4r + e (-1: invalid)
+  int mk[4];  // heads that keep keys 4r + e (bit c: head c), read by masked steps
 };
 
+// tok: lane j < 16 holds key j's cache row (-1: none); mask: its head bits
+// (masked steps only).
 template <int D>
 __device__ __forceinline__ void kv_issue(KvStep<D>& st, const uint16_t* __restrict__ kb,
                                          const uint16_t* __restrict__ vb, int64_t k_st,
-                                         int64_t v_st, int tok, int lane) {
+                                         int64_t v_st, int tok, int lane, int mask = 0) {
   const int r = lane >> 4, c = lane & 15;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) st.mk[e] = __shfl(mask, 4 * r + e, 64);
   const uint4* kp = reinterpret_cast<const uint4*>(kb + (int64_t)(tok < 0 ? 0 : tok) * k_st +
                                                    r * (D / 4));
 #pragma unroll
@@ -93,8 +98,10 @@ struct WaveState {
   float m, l;           // running max / sum of head lane % 16 (equal in its 4 lanes)
 };
 
-// One step: scores by MFMA, online-softmax update, p.V by MFMA.
-template <int DT, int HPR, int D>
+// One step: scores by MFMA, online-softmax update, p.V by MFMA.  MASK: key
+// 4r + e counts for head c only where bit c of its mask is set (each head
+// attends over its own subset of the step's keys).
+template <int DT, int HPR, int D, bool MASK = false>
 __device__ __forceinline__ void attn_step(WaveState<DT, HPR, D>& ws, const KvStep<D>& st,
                                           float scale_log2, int lane) {
   const int r = lane >> 4, c = lane & 15;
@@ -109,7 +116,8 @@ __device__ __forceinline__ void attn_step(WaveState<DT, HPR, D>& ws, const KvSte
   float mx = -INFINITY;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    sc[e] = (c < HPR && st.tv[e] >= 0) ? sacc[e] * scale_log2 : -INFINITY;
+    const bool kept = c < HPR && st.tv[e] >= 0 && (!MASK || ((st.mk[e] >> c) & 1));
+    sc[e] = kept ? sacc[e] * scale_log2 : -INFINITY;
     mx = fmaxf(mx, sc[e]);
   }
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));

@@ -98,8 +98,11 @@ struct StepArgs {
   uint16_t* out;         // [B][Hkv * 4][128]
   uint32_t* status;      // [0] rows spread over XCDs, [1] barrier time-outs
   uint32_t* bar;         // [R][3][kBarWords]
-  uint32_t* hist;        // [R][1024] level-1 counts of the row (zero between calls)
-  uint32_t* t2;          // [R][WR][kT2] per chunk: level-2 counts, keys above b1
+  uint32_t* hist;        // [R][4][1024] level-1 counts of the row's selection rows
+                         // (row r only, or its 4 heads with per-head selection;
+                         // zero between calls)
+  uint32_t* t2;          // [R][WR][4][kT2] per chunk and selection row: level-2
+                         // counts, keys above b1
   float* part;           // [R][WR][4][kDh + 2] (m, l, o)
   int nxcc, RX, WR;
   _Float16 one;
@@ -244,6 +247,148 @@ struct Lds {
   int* keep;                 // H2, A: [kKeepMax]
   float* o;                  // A: [kWaves][4][kDh]
 };
+
+// The end of a row's step, shared by both fused kernels: the waves' (m, l,
+// o) combined in LDS into the workgroup's partial, then the row's last
+// workgroup to arrive merges the partials (E) and writes the output.
+// out_stores issues the stores nothing in the launch reads (index rows and
+// the like); every workgroup calls it once, after its merge arrival.
+template <int DT, typename Stores>
+__device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, kDh>& ws,
+                                           const Lds& lds, float (&s_m)[kWaves][4],
+                                           float (&s_l)[kWaves][4], uint32_t& s_flag, int r,
+                                           int c, int b, int h0, bool select,
+                                           Stores&& out_stores) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  lds_barrier();  // every wave's attention is done; lds.o (after the keep list) is free
+  {
+    const int rq = lane >> 4, cq = lane & 15;
+    if (lane < kG) {
+      s_m[wave][lane] = ws.m;
+      s_l[wave][lane] = ws.l;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int g = 4 * rq + e;
+      if (g < kG)
+#pragma unroll
+        for (int ch = 0; ch < kDh / 16; ++ch)
+          lds.o[(wave * kG + g) * kDh + cq * (kDh / 16) + ch] = ws.acc[ch][e];
+    }
+  }
+  lds_barrier();
+  float* mypart = a.part + ((int64_t)r * a.WR + c) * kG * (kDh + 2);
+  if (tid < kG * kDh) {
+    const int g = tid / kDh, d = tid - g * kDh;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][g]);
+    float l = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = (M == -INFINITY || s_m[w][g] == -INFINITY) ? 0.f : exp2f(s_m[w][g] - M);
+      l += s_l[w][g] * wt;
+      o += lds.o[(w * kG + g) * kDh + d] * wt;
+    }
+    if (a.WR == 1) {
+      a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
+    } else {
+      float* pp = mypart + g * (kDh + 2);
+      if (d == 0) {
+        pp[0] = M;
+        pp[1] = l;
+      }
+      pp[2 + d] = o;
+    }
+  }
+  if (a.WR == 1) {
+    out_stores();
+    return;
+  }
+
+  // ---------------------------------------------------------------- E
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    // blk[0..1]: the row counter of row_arrive; blk[2] collects the XCDs
+    // the row ran on, which the last arrival checks and clears
+    uint32_t* blk = a.bar + ((int64_t)r * 3 + 2) * kBarWords;
+    if (!select) {  // rows that select recorded it before B1
+      record_xcd(a, r);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // recorded before arriving
+    }
+    bool last;
+    row_arrive(blk, a.WR, &last);
+    if (last) {
+      const uint32_t seen = ld_dev(blk + 2);
+      if (__popc(seen) > 1)
+        __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(blk + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_flag = last ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_flag) {
+    out_stores();
+    return;
+  }
+  // The row's partials: (m, l) of every (split, head) into LDS, the split
+  // weights 2^(m - M) per head, then o summed over the splits by two threads
+  // per output (each with its splits' loads all in flight).
+  const float* rp = a.part + (int64_t)r * a.WR * kG * (kDh + 2);
+  float* sm = lds.o;                  // [kMaxWR * 4] m
+  float* sl = sm + kMaxWR * kG;       // [kMaxWR * 4] l
+  float* sw = sl + kMaxWR * kG;       // [kMaxWR * 4] weights (0 past WR)
+  float* stl = sw + kMaxWR * kG;      // [4] sum of l * weight
+  float* so = stl + kG;               // [kTH] half sums of o
+  // o's loads go out with (m, l)'s, so the merge waits for one round trip
+  constexpr int kHalf = kMaxWR / 2;
+  const int half = tid / (kG * kDh), e = tid % (kG * kDh);
+  const int g_o = e / kDh, d_o = e - g_o * kDh;
+  float v[kHalf];
+#pragma unroll
+  for (int u = 0; u < kHalf; ++u) {
+    const int s2 = min(half * kHalf + u, a.WR - 1);
+    v[u] = ld_dev(rp + ((int64_t)s2 * kG + g_o) * (kDh + 2) + 2 + d_o);
+  }
+  if (tid < kMaxWR * kG) {
+    // (m, l) as one 8-byte load (a partial's head record starts 8-byte
+    // aligned): two loads would each be waited for in turn
+    const bool in = tid < a.WR * kG;
+    const int sg = min(tid, a.WR * kG - 1);
+    const uint2 ml = ld_dev2(reinterpret_cast<const uint2*>(rp + (int64_t)sg * (kDh + 2)));
+    sm[tid] = in ? __uint_as_float(ml.x) : -INFINITY;
+    sl[tid] = in ? __uint_as_float(ml.y) : 0.f;
+  }
+  __syncthreads();
+  if (tid < kMaxWR * kG) {
+    const int g = tid % kG;
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < a.WR; ++s2) M = fmaxf(M, sm[s2 * kG + g]);
+    sw[tid] = (sm[tid] == -INFINITY || M == -INFINITY) ? 0.f : exp2f(sm[tid] - M);
+  }
+  __syncthreads();
+  if (tid < kG) {
+    float l = 0.f;
+    for (int s2 = 0; s2 < a.WR; ++s2) l += sl[s2 * kG + tid] * sw[s2 * kG + tid];
+    stl[tid] = l;
+  }
+  {
+    float o = 0.f;
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u)
+      o = __builtin_fmaf(v[u], sw[(half * kHalf + u) * kG + g_o], o);
+    so[tid] = o;
+  }
+  __syncthreads();
+  if (tid < kG * kDh) {
+    const int g = tid / kDh, d = tid - g * kDh;
+    const float o = so[tid] + so[tid + kG * kDh];
+    const float l = stl[g];
+    a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
+  }
+  out_stores();
+}
 
 template <int DT, int TOK>
 __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
@@ -572,134 +717,464 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane);
     attn_step<DT, kG, kDh>(ws, st, a.scale_log2, lane);
   }
-  lds_barrier();  // every wave's attention is done; lds.o (after the keep list) is free
+  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, out_stores);
+}
+
+// Inclusive prefix sum within each row of 16 lanes (DPP row shifts); the
+// rows must be whole (all 16 lanes active).
+__device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  return x;
+}
+
+// The level-1 bins of four selection rows at once: per head h, the unique bin
+// b of h[h][0..1023] with S(b) >= target > S(b+1); s_res[h] = {b, S(b+1)}.
+// 1024 threads, one bin each; 1 <= target <= S(0) for every head.
+__device__ __forceinline__ void select_bin1024x4(const uint32_t* h, uint32_t target,
+                                                 uint32_t (&s_wsum)[kG][kWaves],
+                                                 uint32_t (&s_res)[kG][4]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t x[kG], inc[kG];
+#pragma unroll
+  for (int g = 0; g < kG; ++g) {
+    x[g] = h[g * kL1 + kL1 - 1 - tid];
+    inc[g] = wave_inclusive_scan(x[g]);
+    if (lane == 63) s_wsum[g][wave] = inc[g];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < kG; ++g) {
+    uint32_t before = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) before += w < wave ? s_wsum[g][w] : 0u;
+    const uint32_t above = before + inc[g] - x[g];
+    if (above + x[g] >= target && above < target) {
+      s_res[g][0] = kL1 - 1 - tid;
+      s_res[g][1] = above;
+    }
+  }
+  __syncthreads();
+}
+
+// Per-head selection (LAP_SELECT_PER_HEAD, the reference's rule: each query
+// head keeps its own top-k): the phases of step_fused_kernel with the four
+// heads' selections side by side under the same two row barriers.  Scoring
+// keeps four 16-bit keys per token and four level-1 histograms; H and H2
+// resolve the four thresholds together; each head writes its own index row;
+// A attends once over the union of the four selections, each key carrying
+// the bits of the heads that keep it, so one MFMA pass serves every head.
+// The split merge is the group kernel's.
+template <int DT, int TOK>
+__global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
+  static_assert(TOK >= 1 && TOK <= kMaxTok, "TOK");
+  static_assert(kG * kL1 * 4 <= kKeepMax * 4 && kG * kMaxWR * kL2 * 4 <= kKeepMax * 4,
+                "H and H2 tables fit the keep list's half");
+  __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
+  __shared__ uint32_t s_hist[kG * kH1Pitch];
+  __shared__ uint8_t s_kmask[kKeepMax];
+  __shared__ uint32_t s_h2[kG][kL2], s_wsum[kG][kWaves], s_res[kG][4], s_sel[kG][4];
+  constexpr int kLists = (kG + 1) * TOK;
+  static_assert(kWaves == 16, "one 16-lane row per list");
+  __shared__ uint32_t s_wcnt[(kG + 1) * kMaxTok * kWaves], s_ltot[(kG + 1) * kMaxTok];
+  __shared__ uint32_t s_gtw[kG][kWaves];
+  __shared__ uint32_t s_flag;
+  __shared__ float s_m[kWaves][4], s_l[kWaves][4];
+
+  Lds lds;
+  lds.lut = s_big;
+  lds.tot = reinterpret_cast<uint32_t*>(s_big);
+  lds.keep = reinterpret_cast<int*>(s_big);
+  lds.o = reinterpret_cast<float*>(s_big) + kKeepMax;
+
+  const int nx = a.nxcc;
+  const int x = blockIdx.x % nx, slot = blockIdx.x / nx;
+  const int rs = slot / a.WR, c = slot - rs * a.WR;
+  const int r = rs * nx + x;
+  if (rs >= a.RX || r >= a.B * a.Hkv) return;  // no row here
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = r / a.Hkv, hkv = r - b * a.Hkv;
+  const StepRow pr = step_row(a, b);
+  constexpr int CH = TOK * kTH;
+  const int t0 = c * CH, t1 = min(pr.t_end, t0 + CH);
+  const bool select = pr.k > 0;
+  const int h0 = hkv * kG;
+  i16x4 qpre[kDh / 16];
   {
     const int rq = lane >> 4, cq = lane & 15;
-    if (lane < kG) {
-      s_m[wave][lane] = ws.m;
-      s_l[wave][lane] = ws.l;
-    }
+    const uint16_t* qp =
+        a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (cq < kG ? cq : 0)) * a.q_sh + rq * (kDh / 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int g = 4 * rq + e;
-      if (g < kG)
-#pragma unroll
-        for (int ch = 0; ch < kDh / 16; ++ch)
-          lds.o[(wave * kG + g) * kDh + cq * (kDh / 16) + ch] = ws.acc[ch][e];
+    for (int ks = 0; ks < kDh / 16; ++ks) {
+      const uint2 w = *reinterpret_cast<const uint2*>(qp + 4 * ks);  // 8-byte aligned (host check)
+      qpre[ks] = cq < kG ? __builtin_bit_cast(i16x4, w) : i16x4{0, 0, 0, 0};
     }
-  }
-  lds_barrier();
-  float* mypart = a.part + ((int64_t)r * a.WR + c) * kG * (kDh + 2);
-  if (tid < kG * kDh) {
-    const int g = tid / kDh, d = tid - g * kDh;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][g]);
-    float l = 0.f, o = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float wt = (M == -INFINITY || s_m[w][g] == -INFINITY) ? 0.f : exp2f(s_m[w][g] - M);
-      l += s_l[w][g] * wt;
-      o += lds.o[(w * kG + g) * kDh + d] * wt;
-    }
-    if (a.WR == 1) {
-      a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
-    } else {
-      float* pp = mypart + g * (kDh + 2);
-      if (d == 0) {
-        pp[0] = M;
-        pp[1] = l;
-      }
-      pp[2 + d] = o;
-    }
-  }
-  if (a.WR == 1) {
-    out_stores();
-    return;
   }
 
-  // ---------------------------------------------------------------- E
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    // blk[0..1]: the row counter of row_arrive; blk[2] collects the XCDs
-    // the row ran on, which the last arrival checks and clears
-    uint32_t* blk = a.bar + ((int64_t)r * 3 + 2) * kBarWords;
-    if (!select) {  // rows that select recorded it before B1
-      record_xcd(a, r);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // recorded before arriving
-    }
-    bool last;
-    row_arrive(blk, a.WR, &last);
-    if (last) {
-      const uint32_t seen = ld_dev(blk + 2);
-      if (__popc(seen) > 1)
-        __hip_atomic_fetch_add(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(blk + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    s_flag = last ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_flag) {
-    out_stores();
-    return;
-  }
-  // The row's partials: (m, l) of every (split, head) into LDS, the split
-  // weights 2^(m - M) per head, then o summed over the splits by two threads
-  // per output (each with its splits' loads all in flight).
-  const float* rp = a.part + (int64_t)r * a.WR * kG * (kDh + 2);
-  float* sm = lds.o;                  // [kMaxWR * 4] m
-  float* sl = sm + kMaxWR * kG;       // [kMaxWR * 4] l
-  float* sw = sl + kMaxWR * kG;       // [kMaxWR * 4] weights (0 past WR)
-  float* stl = sw + kMaxWR * kG;      // [4] sum of l * weight
-  float* so = stl + kG;               // [kTH] half sums of o
-  // o's loads go out with (m, l)'s, so the merge waits for one round trip
-  constexpr int kHalf = kMaxWR / 2;
-  const int half = tid / (kG * kDh), e = tid % (kG * kDh);
-  const int g_o = e / kDh, d_o = e - g_o * kDh;
-  float v[kHalf];
+  // ---------------------------------------------------------------- S
+  // kp[j]: the four heads' keys of stage j's token (heads 0, 1 in .x, 2, 3
+  // in .y); inw bit j: the token is a candidate.
+  uint2 kp[TOK];
+  uint32_t inw = 0;
+  for (int i = tid; i < kG * kH1Pitch; i += kTH) s_hist[i] = 0;
+  if (select && t0 < t1) {
+    constexpr int kFill = kLutBytes / 16 / kTH;
+    const uint4* src = reinterpret_cast<const uint4*>(a.lut + (int64_t)r * (kG * kM * kK));
+    u32x4 f[kFill];
 #pragma unroll
-  for (int u = 0; u < kHalf; ++u) {
-    const int s2 = min(half * kHalf + u, a.WR - 1);
-    v[u] = ld_dev(rp + ((int64_t)s2 * kG + g_o) * (kDh + 2) + 2 + d_o);
-  }
-  if (tid < kMaxWR * kG) {
-    // (m, l) as one 8-byte load (a partial's head record starts 8-byte
-    // aligned): two loads would each be waited for in turn
-    const bool in = tid < a.WR * kG;
-    const int sg = min(tid, a.WR * kG - 1);
-    const uint2 ml = ld_dev2(reinterpret_cast<const uint2*>(rp + (int64_t)sg * (kDh + 2)));
-    sm[tid] = in ? __uint_as_float(ml.x) : -INFINITY;
-    sl[tid] = in ? __uint_as_float(ml.y) : 0.f;
-  }
-  __syncthreads();
-  if (tid < kMaxWR * kG) {
-    const int g = tid % kG;
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < a.WR; ++s2) M = fmaxf(M, sm[s2 * kG + g]);
-    sw[tid] = (sm[tid] == -INFINITY || M == -INFINITY) ? 0.f : exp2f(sm[tid] - M);
-  }
-  __syncthreads();
-  if (tid < kG) {
-    float l = 0.f;
-    for (int s2 = 0; s2 < a.WR; ++s2) l += sl[s2 * kG + tid] * sw[s2 * kG + tid];
-    stl[tid] = l;
-  }
-  {
-    float o = 0.f;
+    for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * kTH + tid);
+    const uint8_t* crow = a.codes + (int64_t)b * a.cs_b + (int64_t)hkv * a.cs_h;
+    u32x4 cc[TOK][2];
+    auto request = [&](int j) {
+      const int t = min(t0 + j * kTH + tid, t1 - 1);
+      const uint8_t* p = crow + (int64_t)t * a.cs_t;
+      cc[j][0] = gload16_ordered(p);
+      cc[j][1] = gload16_ordered(p + 16);
+    };
+    request(0);
 #pragma unroll
-    for (int u = 0; u < kHalf; ++u)
-      o = __builtin_fmaf(v[u], sw[(half * kHalf + u) * kG + g_o], o);
-    so[tid] = o;
+    for (int i = 0; i < kFill; ++i) {
+      vm_wait(kFill - 1 - i + 2, f[i]);
+      lds.lut[i * kTH + tid] = as_uint4(f[i]);
+    }
+    lds_barrier();
+    const char* tab = reinterpret_cast<const char*>(lds.lut);
+#pragma unroll
+    for (int j = 0; j < TOK; ++j) {
+      vm_wait(0, cc[j][0], cc[j][1]);
+      if (j + 1 < TOK) request(j + 1);
+      float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
+      score_token(tab, as_uint4(cc[j][0]), as_uint4(cc[j][1]), a.one, e0, e1, e2, e3);
+      const int t = t0 + j * kTH + tid;
+      kp[j] = make_uint2(0u, 0u);
+      if (t < t1 && t >= pr.cs && t < pr.ce) {
+        const uint32_t k0 = key_of_score(e0, a.key_bf16), k1 = key_of_score(e1, a.key_bf16);
+        const uint32_t k2 = key_of_score(e2, a.key_bf16), k3 = key_of_score(e3, a.key_bf16);
+        kp[j] = make_uint2(k0 | (k1 << 16), k2 | (k3 << 16));
+        inw |= 1u << j;
+        atomicAdd(&s_hist[0 * kH1Pitch + (k0 >> kLoBits)], 1u);
+        atomicAdd(&s_hist[1 * kH1Pitch + (k1 >> kLoBits)], 1u);
+        atomicAdd(&s_hist[2 * kH1Pitch + (k2 >> kLoBits)], 1u);
+        atomicAdd(&s_hist[3 * kH1Pitch + (k3 >> kLoBits)], 1u);
+      }
+    }
   }
   __syncthreads();
-  if (tid < kG * kDh) {
-    const int g = tid / kDh, d = tid - g * kDh;
-    const float o = so[tid] + so[tid + kG * kDh];
-    const float l = stl[g];
-    a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
+#pragma unroll
+  for (int ks = 0; ks < kDh / 16; ++ks) asm volatile("" : "+v"(qpre[ks]));
+  auto key = [&](int j, int g) -> uint32_t {
+    const uint32_t w = g < 2 ? kp[j].x : kp[j].y;
+    return (g & 1) ? (w >> 16) : (w & 0xffffu);
+  };
+  // This chunk's level-1 counts of bin tid, added to the four rows' histograms.
+  uint32_t h1[kG] = {0u, 0u, 0u, 0u};
+  if (select) {
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      h1[g] = s_hist[g * kH1Pitch + tid];
+      if (h1[g])
+        __hip_atomic_fetch_add(a.hist + ((int64_t)r * kG + g) * kL1 + tid, h1[g],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
-  out_stores();
+
+  // ---------------------------------------------------------------- B1, H
+  uint32_t n_sel = 0;
+  if (select) {
+    if (tid == 0) record_xcd(a, r);  // complete before B2's arrival
+    wg_row_barrier(a, r, 0);
+    uint32_t* tot = lds.tot;  // [kG][kL1]
+    uint32_t hv[kG];
+#pragma unroll
+    for (int g = 0; g < kG; ++g) hv[g] = ld_dev(a.hist + ((int64_t)r * kG + g) * kL1 + tid);
+#pragma unroll
+    for (int g = 0; g < kG; ++g) tot[g * kL1 + tid] = hv[g];
+    if (tid < kG * kL2) (&s_h2[0][0])[tid] = 0;
+    __syncthreads();
+    select_bin1024x4(tot, (uint32_t)pr.k, s_wsum, s_res);
+    uint32_t b1[kG], gt1[kG];
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      b1[g] = s_res[g][0];
+      gt1[g] = s_res[g][1];
+    }
+#pragma unroll
+    for (int j = 0; j < TOK; ++j)
+      if ((inw >> j) & 1)
+#pragma unroll
+        for (int g = 0; g < kG; ++g)
+          if ((key(j, g) >> kLoBits) == b1[g]) atomicAdd(&s_h2[g][key(j, g) & (kL2 - 1)], 1u);
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      uint32_t gt = (uint32_t)tid > b1[g] ? h1[g] : 0u;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) gt += __shfl_xor(gt, d, 64);
+      if (lane == 0) s_gtw[g][wave] = gt;
+    }
+    __syncthreads();
+    uint32_t* t2 = a.t2 + ((int64_t)r * a.WR + c) * kG * kT2;  // [kG][kT2] of this chunk
+    if (tid < kG * kL2) t2[(tid / kL2) * kT2 + tid % kL2] = (&s_h2[0][0])[tid];
+    if (tid >= kG * kL2 && tid < kG * kL2 + kG) {
+      const int g = tid - kG * kL2;
+      uint32_t my_gt1 = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) my_gt1 += s_gtw[g][w];
+      t2[g * kT2 + kL2] = my_gt1;
+    }
+    wg_row_barrier(a, r, 1);
+
+    // ------------------------------------------------------------ H2
+    // Thread (head hh = tid / 256, chunk cc = tid / 8 % 32, q = tid % 8)
+    // holds bins 8q .. 8q + 7 of chunk cc's level-2 table of head hh (and,
+    // for q = 0, the chunk's count above b1).
+    uint32_t* st2 = lds.tot;                              // [kG][kMaxWR][kL2]
+    uint32_t* s_cgt = reinterpret_cast<uint32_t*>(lds.o);  // [kG][kMaxWR] keys above tau
+    uint32_t* s_cti = s_cgt + kG * kMaxWR;                 // [kG][kMaxWR] ties at tau
+    const int hh = tid >> 8, cc = (tid >> 3) & 31, qq = tid & 7;
+    const bool cin = cc < a.WR;
+    uint32_t v8[8], g1;
+    {
+      const uint32_t* src2 = a.t2 + (((int64_t)r * a.WR + min(cc, a.WR - 1)) * kG + hh) * kT2;
+      uint2 pr2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pr2[i] = ld_dev2(reinterpret_cast<const uint2*>(src2 + 8 * qq + 2 * i));
+      g1 = ld_dev(src2 + kL2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v8[2 * i] = cin ? pr2[i].x : 0u;
+        v8[2 * i + 1] = cin ? pr2[i].y : 0u;
+      }
+      g1 = cin && qq == 0 ? g1 : 0u;
+      uint32_t* dst = st2 + (hh * kMaxWR + cc) * kL2 + 8 * qq;
+      *reinterpret_cast<uint4*>(dst) = make_uint4(v8[0], v8[1], v8[2], v8[3]);
+      *reinterpret_cast<uint4*>(dst + 4) = make_uint4(v8[4], v8[5], v8[6], v8[7]);
+    }
+    __syncthreads();
+    if (tid < kG * kL2) {
+      const int g = tid / kL2, bin = tid % kL2;
+      uint32_t t = 0;
+      for (int c2 = 0; c2 < a.WR; ++c2) t += st2[(g * kMaxWR + c2) * kL2 + bin];
+      s_h2[g][bin] = t;
+    }
+    __syncthreads();
+    if (wave < kG) {  // wave g: head g's level-2 bin
+      const int g = wave;
+      const uint32_t k2 = (uint32_t)pr.k - gt1[g];
+      const uint32_t xv = s_h2[g][kL2 - 1 - lane];
+      const uint32_t inc = wave_inclusive_scan(xv);
+      if (inc >= k2 && inc - xv < k2) {
+        s_res[g][2] = kL2 - 1 - lane;
+        s_res[g][3] = inc - xv;
+      }
+    }
+    __syncthreads();
+    uint32_t tau[kG];
+#pragma unroll
+    for (int g = 0; g < kG; ++g) tau[g] = (b1[g] << kLoBits) | s_res[g][2];
+    {
+      // per chunk and head: keys above tau and ties at tau, over its 8 threads
+      uint32_t b2 = s_res[0][2];
+#pragma unroll
+      for (int g = 1; g < kG; ++g) b2 = hh == g ? s_res[g][2] : b2;
+      uint32_t gsum = g1, ti = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t bin = (uint32_t)(8 * qq + i);
+        gsum += bin > b2 ? v8[i] : 0u;
+        ti += bin == b2 ? v8[i] : 0u;
+      }
+#pragma unroll
+      for (int d = 4; d >= 1; d >>= 1) {
+        gsum += __shfl_xor(gsum, d, 64);
+        ti += __shfl_xor(ti, d, 64);
+      }
+      if (qq == 0) {
+        s_cgt[hh * kMaxWR + cc] = gsum;
+        s_cti[hh * kMaxWR + cc] = ti;
+      }
+    }
+    __syncthreads();
+    if (wave < kG) {  // wave g: where head g's selection of this chunk starts
+      const int g = wave;
+      const uint32_t need = (uint32_t)pr.k - gt1[g] - s_res[g][3];  // ties at tau to take, >= 1
+      const uint32_t gv = lane < c ? s_cgt[g * kMaxWR + lane] : 0u;
+      const uint32_t tv = lane < c ? s_cti[g * kMaxWR + lane] : 0u;
+      uint32_t gs = gv, ts = tv;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        gs += __shfl_xor(gs, d, 64);
+        ts += __shfl_xor(ts, d, 64);
+      }
+      if (lane == 0) {
+        const uint32_t my_ties = s_cti[g * kMaxWR + c];
+        const uint32_t tk = ts >= need ? 0u : min(my_ties, need - ts);
+        uint32_t taken_before;  // min(need, ts), explicit (see step_fused_kernel)
+        asm volatile("v_min_u32 %0, %1, %2" : "=v"(taken_before) : "v"(need), "v"(ts));
+        s_sel[g][0] = tk;
+        s_sel[g][1] = gs + taken_before;
+        s_sel[g][2] = my_ties;
+      }
+    }
+    __syncthreads();
+
+    // Ordered compaction, per head (its index row) and of the union (the
+    // keep list of A, with each key's head bits).
+    uint32_t take[kG], base[kG], ties[kG];
+    bool partial = false;
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      take[g] = s_sel[g][0];
+      base[g] = s_sel[g][1];
+      ties[g] = s_sel[g][2];
+      partial |= take[g] > 0 && take[g] < ties[g];
+    }
+    // Positions come from per-wave counts: list l = g * TOK + j (g < 4: head
+    // g's selection, or its ties at tau; g = 4: the union) counts its
+    // stage-j tokens per wave, then one 16-lane row scan per list gives each
+    // wave's exclusive prefix and the list's total.
+    auto scan_lists = [&]() {
+      __syncthreads();
+      if (tid < kLists * kWaves) {
+        const uint32_t xw = s_wcnt[tid];
+        const uint32_t inc = row16_inclusive_scan(xw);
+        s_wcnt[tid] = inc - xw;
+        if ((tid & (kWaves - 1)) == kWaves - 1) s_ltot[tid / kWaves] = inc;
+      }
+      __syncthreads();
+    };
+    // the chunk's ties at tau, for heads that take only some of them (their
+    // ranks, lowest columns first)
+    if (partial) {
+#pragma unroll
+      for (int g = 0; g < kG; ++g) {
+        if (!(take[g] > 0 && take[g] < ties[g])) continue;
+#pragma unroll
+        for (int j = 0; j < TOK; ++j) {
+          const uint64_t mt = __ballot(((inw >> j) & 1) && key(j, g) == tau[g]);
+          if (lane == 0) s_wcnt[(g * TOK + j) * kWaves + wave] = (uint32_t)__popcll(mt);
+        }
+      }
+      scan_lists();
+    }
+    uint32_t selb = 0;  // bit 4 j + g: stage j's token selected by head g
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      const bool part = take[g] > 0 && take[g] < ties[g];
+      uint32_t tie_base = 0;
+#pragma unroll
+      for (int j = 0; j < TOK; ++j) {
+        const bool in = (inw >> j) & 1;
+        const uint32_t kj = key(j, g);
+        bool sj;
+        if (part) {
+          const uint64_t mt = __ballot(in && kj == tau[g]);
+          const uint32_t rank = tie_base + s_wcnt[(g * TOK + j) * kWaves + wave] + lanes_below(mt);
+          sj = in && (kj > tau[g] || (kj == tau[g] && rank < take[g]));
+          tie_base += s_ltot[g * TOK + j];
+        } else {
+          sj = in && (kj > tau[g] || (take[g] > 0 && kj == tau[g]));
+        }
+        selb |= (sj ? 1u : 0u) << (4 * j + g);
+      }
+    }
+    auto chosen = [&](int j, int g) -> bool {
+      return g < kG ? ((selb >> (4 * j + g)) & 1u) != 0u : ((selb >> (4 * j)) & 0xfu) != 0u;
+    };
+    if (partial) __syncthreads();  // the tie prefixes are read
+#pragma unroll
+    for (int j = 0; j < TOK; ++j)
+#pragma unroll
+      for (int g = 0; g <= kG; ++g) {
+        const uint64_t m = __ballot(chosen(j, g));
+        if (lane == 0) s_wcnt[(g * TOK + j) * kWaves + wave] = (uint32_t)__popcll(m);
+      }
+    scan_lists();
+    uint32_t lbase[kG + 1] = {0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < TOK; ++j) {
+      const int col = t0 + j * kTH + tid;
+#pragma unroll
+      for (int g = 0; g <= kG; ++g) {
+        const bool sj = chosen(j, g);
+        const uint64_t m = __ballot(sj);
+        const uint32_t q = lbase[g] + s_wcnt[(g * TOK + j) * kWaves + wave] + lanes_below(m);
+        if (sj) {
+          if (g < kG) {
+            if (base[g] + q < (uint32_t)pr.k) {
+              const int64_t irow = ((int64_t)b * a.Hkv * kG + h0 + g) * a.k_cols + base[g];
+              if (a.idx_i64) put_idx<int64_t>(a.idx, irow + q, col);
+              else put_idx<int32_t>(a.idx, irow + q, col);
+            }
+          } else if (q < (uint32_t)kKeepMax) {
+            lds.keep[q] = col;
+            s_kmask[q] = (uint8_t)((selb >> (4 * j)) & 0xfu);
+          }
+        }
+        lbase[g] += s_ltot[g * TOK + j];
+      }
+    }
+    n_sel = min(lbase[kG], (uint32_t)kKeepMax);
+  }
+  lds_barrier();  // the keep list
+
+  // Index-row padding of ragged rows and the histogram clear, after the
+  // merge arrival (the index rows themselves were written above).
+  auto out_stores = [&]() {
+    if (a.plans) {  // pad [k, k_cols) of the four rows with -1, split over the workgroups
+      const int pad = a.k_cols - pr.k;
+      const int ps = (pad + a.WR - 1) / a.WR;
+      for (int i = c * ps + tid; i < min(pad, (c + 1) * ps); i += kTH) {
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          const int64_t irow = ((int64_t)b * a.Hkv * kG + h0 + g) * a.k_cols + pr.k;
+          if (a.idx_i64) put_idx<int64_t>(a.idx, irow + i, -1);
+          else put_idx<int32_t>(a.idx, irow + i, -1);
+        }
+      }
+    }
+    if (select && c == 0) {
+#pragma unroll
+      for (int g = 0; g < kG; ++g) a.hist[((int64_t)r * kG + g) * kL1 + tid] = 0u;
+    }
+  };
+
+  // ---------------------------------------------------------------- A
+  // This workgroup attends over the union of its heads' selections (each
+  // head scores only its own keys) and every WR-th entry (from c) of the
+  // row's sink ++ local tail, which every head keeps.
+  const uint16_t* kb = a.kc + (int64_t)b * a.k_sb + (int64_t)hkv * a.k_sh;
+  const uint16_t* vb = a.vc + (int64_t)b * a.v_sb + (int64_t)hkv * a.v_sh;
+  WaveState<DT, kG, kDh> ws;
+#pragma unroll
+  for (int ks = 0; ks < kDh / 16; ++ks) {
+    ws.qf[ks] = qpre[ks];
+    ws.acc[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  ws.m = -INFINITY;
+  ws.l = 0.f;
+  const int n_fix = pr.sink + pr.tail_count;
+  const int n_st = n_fix > c ? (n_fix - c + a.WR - 1) / a.WR : 0;
+  const int n_loc = (int)n_sel + n_st;
+  const int nsteps = (n_loc + kKeys - 1) / kKeys;
+  for (int i = wave; i < nsteps; i += kWaves) {
+    const int p = i * kKeys + (lane & 15);
+    int tok = -1, msk = 0;
+    if (p < (int)n_sel) {
+      tok = lds.keep[p];
+      msk = s_kmask[p];
+    } else if (p < n_loc) {
+      const int jt = c + (p - (int)n_sel) * a.WR;
+      tok = jt < pr.sink ? jt : pr.tail_start + (jt - pr.sink);
+      msk = 0xf;
+    }
+    if (tok < 0 || tok >= pr.t_total) tok = -1;
+    KvStep<kDh> st;
+    kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane, msk);
+    attn_step<DT, kG, kDh, true>(ws, st, a.scale_log2, lane);
+  }
+  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, out_stores);
 }
 
 inline _Float16 f16_one() { return (_Float16)1.0f; }
@@ -778,19 +1253,22 @@ StepWs carve_step(void* base, int R, int WR, int head_rows) {
   };
   w.status = reinterpret_cast<uint32_t*>(take(kStatusBytes));
   w.bar = reinterpret_cast<uint32_t*>(take((size_t)head_rows * 3 * kBarWords * 4));
-  w.hist = reinterpret_cast<uint32_t*>(take((size_t)head_rows * kL1 * 4));
-  w.t2 = reinterpret_cast<uint32_t*>(take((size_t)R * WR * kT2 * 4));
+  w.hist = reinterpret_cast<uint32_t*>(take((size_t)head_rows * kG * kL1 * 4));
+  w.t2 = reinterpret_cast<uint32_t*>(take((size_t)R * WR * kG * kT2 * 4));
   w.part = reinterpret_cast<float*>(take((size_t)R * WR * kG * (kDh + 2) * 4));
   w.bytes = off;
   return w;
 }
 
 template <int DT>
-void launch_fused_dt(const StepArgs& a, int tok, int grid, hipStream_t st) {
+void launch_fused_dt(const StepArgs& a, int tok, int grid, bool per_head, hipStream_t st) {
   switch (tok) {
-#define LAP_STEP(TK)                                                                     \
-  case TK:                                                                               \
-    hipLaunchKernelGGL((step_fused_kernel<DT, TK>), dim3(grid), dim3(kTH), 0, st, a);    \
+#define LAP_STEP(TK)                                                                       \
+  case TK:                                                                                 \
+    if (per_head)                                                                          \
+      hipLaunchKernelGGL((step_fused_ph_kernel<DT, TK>), dim3(grid), dim3(kTH), 0, st, a); \
+    else                                                                                   \
+      hipLaunchKernelGGL((step_fused_kernel<DT, TK>), dim3(grid), dim3(kTH), 0, st, a);    \
     break;
     LAP_STEP(1) LAP_STEP(2) LAP_STEP(3) LAP_STEP(4) LAP_STEP(5) LAP_STEP(6) LAP_STEP(7)
     LAP_STEP(8)
@@ -820,7 +1298,7 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
                       int tail_count, const lap_row_plan* plans, int k_cols, int max_sink,
                       int max_tail, int key_bf16, float scale, void* out_idx, int idx_dtype,
                       void* out, void* workspace, size_t ws_bytes, int head_rows,
-                      const char* who, hipStream_t st) {
+                      bool per_head, const char* who, hipStream_t st) {
   const int R = B * Hkv;
   const int keep_max = plans ? k_cols + max_sink + max_tail : k + sink + tail_count;
   FusedPlan fp;
@@ -853,9 +1331,9 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
   a.status = w.status; a.bar = w.bar; a.hist = w.hist; a.t2 = w.t2; a.part = w.part;
   a.nxcc = fp.nxcc; a.RX = fp.RX; a.WR = fp.WR;
   a.one = f16_one();
-  if (dtype == LAP_DTYPE_F16) launch_fused_dt<LAP_DTYPE_F16>(a, fp.tok, fp.grid, st);
-  else launch_fused_dt<LAP_DTYPE_BF16>(a, fp.tok, fp.grid, st);
-  LAP_LAUNCH_CHECK("step_fused_kernel");
+  if (dtype == LAP_DTYPE_F16) launch_fused_dt<LAP_DTYPE_F16>(a, fp.tok, fp.grid, per_head, st);
+  else launch_fused_dt<LAP_DTYPE_BF16>(a, fp.tok, fp.grid, per_head, st);
+  LAP_LAUNCH_CHECK(per_head ? "step_fused_ph_kernel" : "step_fused_kernel");
   return LAP_OK;
 }
 
@@ -937,13 +1415,14 @@ int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
     LAP_CHECK_CODE(workspace && workspace_bytes >= fused + cw.ret + cw.attn, LAP_ERR_WORKSPACE,
                    "%s: workspace of %zu bytes needed", who, fused + cw.ret + cw.attn);
   hipStream_t st = as_stream(stream);
-  if (km == key_mode && D == 128) {
+  if (D == 128) {
     s = decode_step_fused(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, q, q_sb,
                           q_sh, keys, vals, dtype, B, Hkv, T_kv, k_sb, k_sh, k_st, v_sb, v_sh,
                           v_st, T, cand_start, cand_end, k_eff, sink_count, tail_start,
                           tail_count, plans, plans ? k_cols : k_eff, max_sink, max_tail,
                           km == LAP_KEY_BF16, scale, out_idx, idx_dtype, out, workspace,
-                          std::min(workspace_bytes, fused), head_rows, who, st);
+                          std::min(workspace_bytes, fused), head_rows,
+                          (key_mode & LAP_SELECT_PER_HEAD) != 0, who, st);
     if (s != LAP_ERR_UNSUPPORTED) return s;
     clear_error();
   }

@@ -1,7 +1,9 @@
-"""The one-launch decode step (lap_decode_step, group selection) on the GPU.
+"""The one-launch decode step (lap_decode_step) on the GPU, with group
+selection (top-k of the group max) and with the reference's per-head
+selection (each query head's own top-k, aq_evaluation.py:185-205).
 
 Every case checks the selected indices bit for bit against the oracle's
-top-k of the oracle's scores (aq_evaluation.py:185-205 with the group max),
+top-k of the oracle's scores,
 the attention output within 1e-2 of float64 softmax over the keep set
 (:210-251), and that the step's health counters stay zero (no workgroup ran
 off its row's XCD, no barrier gave up).  Shapes cover the C2 size (131072
@@ -38,15 +40,16 @@ def _inputs(seed, B, T, dt, zero_codes=False, dev=None):
     return cb, codes, kk, vv, q
 
 
-def _want_idx(orc, cb, codes_b, q_b, plan, key_bf16):
+def _want_idx(orc, cb, codes_b, q_b, plan, key_bf16, per_head=False):
     lut = orc.lut_build(q_b.float().numpy(), cb.numpy())
     s = orc.score_grouped(lut, codes_b[:, :plan["t_codes"]].numpy(), 4)
-    return orc.topk(s, plan["k"], 4, plan["cand_start"], plan["cand_end"], key_bf16=key_bf16)
+    return orc.topk(s, plan["k"], 1 if per_head else 4, plan["cand_start"], plan["cand_end"],
+                    key_bf16=key_bf16)
 
 
-def _check_attn(orc, out, q, kk, vv, want_b, b, t_total):
+def _check_attn(orc, out, q, kk, vv, want_b, b, t_total, per_head=False):
     def keep(bb, h):
-        return orc.keep_list(want_b[h // 4], t_total, SINK, LOCAL)
+        return orc.keep_list(want_b[h if per_head else h // 4], t_total, SINK, LOCAL)
 
     ref = orc.attn_decode_f64(q[b:b + 1, :, 0].double().numpy(),
                               kk[b:b + 1, :, :t_total].double().cpu().numpy(),
@@ -55,46 +58,58 @@ def _check_attn(orc, out, q, kk, vv, want_b, b, t_total):
     assert _rel(got, ref) < 1e-2, b
 
 
-def _decoder(cb, dev, B, T, dt, key_dt, topk=None, mask_out=0.98):
+def _decoder(cb, dev, B, T, dt, key_dt, topk=None, mask_out=0.98, select="group"):
     from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
     cfg = RetrievalConfig(topk=topk, mask_out=mask_out, sink_size=SINK, local_window=LOCAL,
-                          select="group", score_dtype=key_dt)
+                          select=select, score_dtype=key_dt)
     return SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg, dtype=dt)
 
 
-@pytest.mark.parametrize("B,T,tc,dt,key_dt,topk,zero", [
-    (1, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False),  # C2: 32 x 4096
-    (1, 131072, 131008, torch.bfloat16, torch.bfloat16, None, False),  # reference budget 2621
-    (1, 131072, 131072, torch.float16, torch.float16, 2048, True),     # all ties
-    (1, 40003, 39936, torch.bfloat16, torch.float16, 700, False),      # 32 x 2048, partial last
-    (1, 300, 256, torch.bfloat16, torch.bfloat16, 16, False),          # one workgroup per row
-    (1, 8192, 8192, torch.float16, torch.bfloat16, None, False),       # C1 size: 8 x 1024
-    (2, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False),  # two rows per XCD: 16 x 8192
+@pytest.mark.parametrize("B,T,tc,dt,key_dt,topk,zero,select", [
+    (1, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False, "group"),  # C2: 32 x 4096
+    (1, 131072, 131008, torch.bfloat16, torch.bfloat16, None, False, "group"),  # budget 2621
+    (1, 131072, 131072, torch.float16, torch.float16, 2048, True, "group"),     # all ties
+    (1, 40003, 39936, torch.bfloat16, torch.float16, 700, False, "group"),  # partial last chunk
+    (1, 300, 256, torch.bfloat16, torch.bfloat16, 16, False, "group"),      # one workgroup per row
+    (1, 8192, 8192, torch.float16, torch.bfloat16, None, False, "group"),   # C1 size: 8 x 1024
+    (2, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False, "group"),  # 2 rows per XCD
+    # per-head selection (the reference's rule)
+    (1, 131072, 131008, torch.bfloat16, torch.bfloat16, None, False, "head"),  # k = 2621
+    (1, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False, "head"),
+    (1, 131072, 131072, torch.float16, torch.float16, 2048, True, "head"),     # all ties
+    (1, 40003, 39936, torch.bfloat16, torch.float16, 700, False, "head"),
+    (1, 300, 256, torch.bfloat16, torch.bfloat16, 16, False, "head"),
+    (1, 8192, 8192, torch.float16, torch.bfloat16, None, False, "head"),       # C1: k = 163
+    (2, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False, "head"),
 ])
-def test_step_uniform(dev, orc, B, T, tc, dt, key_dt, topk, zero):
-    cb, codes, kk, vv, q = _inputs(700 + T % 997 + B, B, T, dt, zero, dev)
-    dec = _decoder(cb, dev, B, T, dt, key_dt, topk)
+def test_step_uniform(dev, orc, B, T, tc, dt, key_dt, topk, zero, select):
+    per_head = select == "head"
+    cb, codes, kk, vv, q = _inputs(700 + T % 997 + B + 3 * per_head, B, T, dt, zero, dev)
+    dec = _decoder(cb, dev, B, T, dt, key_dt, topk, select=select)
     out = dec.step(q.to(dev), codes.to(dev)[:, :, :tc], kk, vv, t_codes=tc, t_total=T).clone()
     sel = dec.selected().cpu().numpy()
+    assert sel.shape[1] == (Hq if per_head else Hkv)
     p = dict(t_codes=tc, **dec.plan(tc, T))
     for b in range(B):
-        want = _want_idx(orc, cb, codes[b], q[b, :, 0], p, key_dt == torch.bfloat16)
+        want = _want_idx(orc, cb, codes[b], q[b, :, 0], p, key_dt == torch.bfloat16, per_head)
         assert np.array_equal(sel[b].astype(np.int64), want), b
-        _check_attn(orc, out, q, kk, vv, want, b, T)
+        _check_attn(orc, out, q, kk, vv, want, b, T, per_head)
     assert dec.fused_status() == (0, 0)
 
 
-def test_step_keep_everything(dev, orc):
+@pytest.mark.parametrize("select", ["group", "head"])
+def test_step_keep_everything(dev, orc, select):
     """mask_out = 0: every candidate is selected, so the step is dense
-    attention over the whole cache (a 131007-entry selection)."""
+    attention over the whole cache (a 131007-entry selection per row)."""
     T = 131072
     cb, codes, kk, vv, q = _inputs(720, 1, T, torch.bfloat16, dev=dev)
-    dec = _decoder(cb, dev, 1, T, torch.bfloat16, torch.bfloat16, None, mask_out=0.0)
+    dec = _decoder(cb, dev, 1, T, torch.bfloat16, torch.bfloat16, None, mask_out=0.0,
+                   select=select)
     tc = T - 1
     out = dec.step(q.to(dev), codes.to(dev)[:, :, :tc], kk, vv, t_codes=tc, t_total=T).clone()
     p = dec.plan(tc, T)
     sel = dec.selected().cpu().numpy()
-    want = np.tile(np.arange(p["cand_start"], p["cand_end"]), (Hkv, 1))
+    want = np.tile(np.arange(p["cand_start"], p["cand_end"]), (Hq if select == "head" else Hkv, 1))
     assert np.array_equal(sel[0].astype(np.int64), want)
     ref = orc.attn_decode_f64(q[:, :, 0].double().numpy(), kk.double().cpu().numpy(),
                               vv.double().cpu().numpy(), lambda b, h: np.arange(T))
@@ -102,14 +117,16 @@ def test_step_keep_everything(dev, orc):
     assert dec.fused_status() == (0, 0)
 
 
-def test_step_ragged_plans_and_graph(dev, orc):
+@pytest.mark.parametrize("select", ["group", "head"])
+def test_step_ragged_plans_and_graph(dev, orc, select):
     """B = 2 ragged lengths through device plans (fixed launch arguments),
     eager and replayed from a captured graph, then replayed again after the
     host rewrites the plans."""
     from laprune_amd.retrieval import PLAN_FIELDS
     B, T = 2, 65536
-    cb, codes, kk, vv, q = _inputs(730, B, T, torch.bfloat16, dev=dev)
-    dec = _decoder(cb, dev, B, T, torch.bfloat16, torch.bfloat16, 1024)
+    per_head = select == "head"
+    cb, codes, kk, vv, q = _inputs(730 + per_head, B, T, torch.bfloat16, dev=dev)
+    dec = _decoder(cb, dev, B, T, torch.bfloat16, torch.bfloat16, 1024, select=select)
     qd, cd = q.to(dev), codes.to(dev)
 
     def run_plans(t_total):
@@ -121,10 +138,10 @@ def test_step_ragged_plans_and_graph(dev, orc):
     def check(plans, t_total, out):
         idx = dec.idx.cpu().numpy()
         for b, p in enumerate(plans):
-            want = _want_idx(orc, cb, codes[b], q[b, :, 0], p, True)
+            want = _want_idx(orc, cb, codes[b], q[b, :, 0], p, True, per_head)
             assert np.array_equal(idx[b, :, :p["k"]].astype(np.int64), want), b
             assert np.all(idx[b, :, p["k"]:dec.k_cols] == -1), b
-            _check_attn(orc, out, q, kk, vv, want, b, t_total[b])
+            _check_attn(orc, out, q, kk, vv, want, b, t_total[b], per_head)
 
     t1 = [65536, 40001]
     plans1, pd1 = run_plans(t1)
