@@ -210,15 +210,32 @@ constexpr int kH1Pitch = kL1 + 1;  // copies of one bin in different banks
 constexpr int kT2 = kL2 + 4;       // per-chunk table: level-2 counts, keys above b1
 constexpr uint32_t kNoKey = 0xffffffffu;  // a thread's token outside the window
 
+// Inclusive prefix sum within each row of 16 lanes (DPP row shifts); the
+// rows must be whole (all 16 lanes active).
+__device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  return x;
+}
+
 // The unique bin b of h[0..1023] with S(b) >= target > S(b+1), S(i) =
 // sum_{j >= i} h[j]: s_res = {b, S(b+1)}.  1024 threads, one bin each;
 // 1 <= target <= S(0).
 __device__ __forceinline__ void select_bin1024(const uint32_t* h, uint32_t target,
                                                uint32_t* s_wsum, uint32_t* s_res) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t x = h[kL1 - 1 - tid];
-  uint32_t total;
-  const uint32_t above = block_exclusive_scan<kTH>(x, s_wsum, &total);
+  const uint32_t inc = wave_inclusive_scan(x);
+  if (lane == 63) s_wsum[wave] = inc;
+  __syncthreads();
+  if (tid < kWaves) {  // the waves' sums to their exclusive prefix, in place
+    const uint32_t v = s_wsum[tid];
+    s_wsum[tid] = row16_inclusive_scan(v) - v;
+  }
+  __syncthreads();
+  const uint32_t above = s_wsum[wave] + inc - x;
   if (above + x >= target && above < target) {
     s_res[0] = kL1 - 1 - tid;
     s_res[1] = above;
@@ -240,6 +257,23 @@ __device__ __forceinline__ void select_bin64(const uint32_t* h, uint32_t target,
   __syncthreads();
 }
 
+// Per-wave counts of TOK-stage token lists to positions: s_wcnt[l][w] holds
+// list l's count in wave w; afterwards it holds the exclusive prefix over
+// the waves, and s_ltot[l] the list's total.  One 16-lane row per list.
+template <int LISTS>
+__device__ __forceinline__ void scan_wave_counts(uint32_t* s_wcnt, uint32_t* s_ltot) {
+  static_assert(kWaves == 16, "one 16-lane row per list");
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if (tid < LISTS * kWaves) {
+    const uint32_t xw = s_wcnt[tid];
+    const uint32_t inc = row16_inclusive_scan(xw);
+    s_wcnt[tid] = inc - xw;
+    if ((tid & (kWaves - 1)) == kWaves - 1) s_ltot[tid / kWaves] = inc;
+  }
+  __syncthreads();
+}
+
 // LDS carve of the 64 KiB region that holds the table during S.
 struct Lds {
   uint4* lut;                // S: [kLutBytes / 16]
@@ -250,18 +284,19 @@ struct Lds {
 
 // The end of a row's step, shared by both fused kernels: the waves' (m, l,
 // o) combined in LDS into the workgroup's partial, then the row's last
-// workgroup to arrive merges the partials (E) and writes the output.
+// workgroup to arrive merges the partials (E) and writes the output.  Waves
+// nw.. ran no attention step (their state is empty) and are left out.
 // out_stores issues the stores nothing in the launch reads (index rows and
 // the like); every workgroup calls it once, after its merge arrival.
 template <int DT, typename Stores>
 __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, kDh>& ws,
                                            const Lds& lds, float (&s_m)[kWaves][4],
                                            float (&s_l)[kWaves][4], uint32_t& s_flag, int r,
-                                           int c, int b, int h0, bool select,
+                                           int c, int b, int h0, bool select, int nw,
                                            Stores&& out_stores) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   lds_barrier();  // every wave's attention is done; lds.o (after the keep list) is free
-  {
+  if (wave < nw) {
     const int rq = lane >> 4, cq = lane & 15;
     if (lane < kG) {
       s_m[wave][lane] = ws.m;
@@ -280,15 +315,20 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
   float* mypart = a.part + ((int64_t)r * a.WR + c) * kG * (kDh + 2);
   if (tid < kG * kDh) {
     const int g = tid / kDh, d = tid - g * kDh;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][g]);
-    float l = 0.f, o = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    float M = -INFINITY, l = 0.f, o = 0.f;
+    auto add = [&](int w) {
       const float wt = (M == -INFINITY || s_m[w][g] == -INFINITY) ? 0.f : exp2f(s_m[w][g] - M);
       l += s_l[w][g] * wt;
       o += lds.o[(w * kG + g) * kDh + d] * wt;
+    };
+    if (nw == kWaves) {  // every wave attended: unrolled, the LDS reads batched
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][g]);
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) add(w);
+    } else {
+      for (int w = 0; w < nw; ++w) M = fmaxf(M, s_m[w][g]);
+      for (int w = 0; w < nw; ++w) add(w);
     }
     if (a.WR == 1) {
       a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
@@ -332,15 +372,17 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     out_stores();
     return;
   }
-  // The row's partials: (m, l) of every (split, head) into LDS, the split
-  // weights 2^(m - M) per head, then o summed over the splits by two threads
-  // per output (each with its splits' loads all in flight).
+  // The row's partials: thread t < 128 holds (m, l) of split t / 4, head
+  // t % 4 (waves 0 and 1); per head, the max M over the splits and the sum
+  // of l * 2^(m - M) are reduced over the lanes of one head and then over
+  // the two waves.  o is summed over the splits by two threads per output
+  // (each with its splits' loads all in flight).
+  static_assert(kMaxWR * kG == 128, "waves 0 and 1 hold the (split, head) records");
   const float* rp = a.part + (int64_t)r * a.WR * kG * (kDh + 2);
-  float* sm = lds.o;                  // [kMaxWR * 4] m
-  float* sl = sm + kMaxWR * kG;       // [kMaxWR * 4] l
-  float* sw = sl + kMaxWR * kG;       // [kMaxWR * 4] weights (0 past WR)
-  float* stl = sw + kMaxWR * kG;      // [4] sum of l * weight
-  float* so = stl + kG;               // [kTH] half sums of o
+  float* sw = lds.o;                  // [kMaxWR * 4] weights (0 past WR)
+  float* so = sw + kMaxWR * kG;       // [kTH] half sums of o
+  float* sx = so + kTH;               // [2][4] per-wave max of m
+  float* slw = sx + 2 * kG;           // [2][4] per-wave sum of l * weight
   // o's loads go out with (m, l)'s, so the merge waits for one round trip
   constexpr int kHalf = kMaxWR / 2;
   const int half = tid / (kG * kDh), e = tid % (kG * kDh);
@@ -351,28 +393,32 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     const int s2 = min(half * kHalf + u, a.WR - 1);
     v[u] = ld_dev(rp + ((int64_t)s2 * kG + g_o) * (kDh + 2) + 2 + d_o);
   }
+  float mt = -INFINITY, lt = 0.f;
   if (tid < kMaxWR * kG) {
     // (m, l) as one 8-byte load (a partial's head record starts 8-byte
     // aligned): two loads would each be waited for in turn
     const bool in = tid < a.WR * kG;
     const int sg = min(tid, a.WR * kG - 1);
     const uint2 ml = ld_dev2(reinterpret_cast<const uint2*>(rp + (int64_t)sg * (kDh + 2)));
-    sm[tid] = in ? __uint_as_float(ml.x) : -INFINITY;
-    sl[tid] = in ? __uint_as_float(ml.y) : 0.f;
+    mt = in ? __uint_as_float(ml.x) : -INFINITY;
+    lt = in ? __uint_as_float(ml.y) : 0.f;
+    float mx = mt;  // lanes xor 4 .. 32 share the head lane % 4
+#pragma unroll
+    for (int dd = 4; dd <= 32; dd <<= 1) mx = fmaxf(mx, __shfl_xor(mx, dd, 64));
+    if (lane < kG) sx[wave * kG + lane] = mx;
   }
   __syncthreads();
   if (tid < kMaxWR * kG) {
     const int g = tid % kG;
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < a.WR; ++s2) M = fmaxf(M, sm[s2 * kG + g]);
-    sw[tid] = (sm[tid] == -INFINITY || M == -INFINITY) ? 0.f : exp2f(sm[tid] - M);
+    const float M = fmaxf(sx[g], sx[kG + g]);
+    const float wt = (mt == -INFINITY || M == -INFINITY) ? 0.f : exp2f(mt - M);
+    sw[tid] = wt;
+    float lw = lt * wt;
+#pragma unroll
+    for (int dd = 4; dd <= 32; dd <<= 1) lw += __shfl_xor(lw, dd, 64);
+    if (lane < kG) slw[wave * kG + lane] = lw;
   }
   __syncthreads();
-  if (tid < kG) {
-    float l = 0.f;
-    for (int s2 = 0; s2 < a.WR; ++s2) l += sl[s2 * kG + tid] * sw[s2 * kG + tid];
-    stl[tid] = l;
-  }
   {
     float o = 0.f;
 #pragma unroll
@@ -384,7 +430,7 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
   if (tid < kG * kDh) {
     const int g = tid / kDh, d = tid - g * kDh;
     const float o = so[tid] + so[tid + kG * kDh];
-    const float l = stl[g];
+    const float l = slw[g] + slw[kG + g];
     a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
   }
   out_stores();
@@ -394,11 +440,11 @@ template <int DT, int TOK>
 __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   static_assert(TOK >= 1 && TOK <= kMaxTok, "TOK");
   static_assert(kKeepMax * 4 + kWaves * 4 * kDh * 4 <= kLutBytes, "LDS carve");
-  static_assert(kMaxWR * 4 * 3 + 4 + kTH <= kWaves * 4 * kDh && kG * kDh * 2 == kTH, "E carve");
+  static_assert(kMaxWR * 4 + kTH + 4 * kG <= kWaves * 4 * kDh && kG * kDh * 2 == kTH, "E carve");
   __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
   __shared__ uint32_t s_hist[kHC * kH1Pitch];
-  __shared__ uint32_t s_h2[kL2], s_wsum[kWaves], s_res[4], s_cnt[kMaxTok][kWaves];
-  __shared__ uint32_t s_cnt2[kMaxTok][kWaves];
+  __shared__ uint32_t s_h2[kL2], s_wsum[kWaves], s_res[4], s_gtw[kWaves];
+  __shared__ uint32_t s_wcnt[kMaxTok * kWaves], s_ltot[kMaxTok];
   __shared__ uint32_t s_flag;
   __shared__ float s_m[kWaves][4], s_l[kWaves][4];
 
@@ -512,14 +558,14 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     uint32_t gt = (uint32_t)tid > b1 ? h1 : 0u;
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) gt += __shfl_xor(gt, d, 64);
-    if (lane == 0) s_cnt[0][wave] = gt;
+    if (lane == 0) s_gtw[wave] = gt;
     __syncthreads();
     uint32_t* t2 = a.t2 + ((int64_t)r * a.WR + c) * kT2;
     if (tid < kL2) t2[tid] = s_h2[tid];
     if (tid == kL2) {
       uint32_t my_gt1 = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) my_gt1 += s_cnt[0][w];
+      for (int w = 0; w < kWaves; ++w) my_gt1 += s_gtw[w];
       t2[kL2] = my_gt1;
     }
     wg_row_barrier(a, r, 1);
@@ -617,45 +663,32 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
 #pragma unroll
       for (int j = 0; j < TOK; ++j) {
         mt[j] = __ballot(kv[j] != kNoKey && kv[j] == tau);
-        if (lane == 0) s_cnt[j][wave] = (uint32_t)__popcll(mt[j]);
+        if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(mt[j]);
       }
-      __syncthreads();
+      scan_wave_counts<TOK>(s_wcnt, s_ltot);
       uint32_t tie_base = 0;
 #pragma unroll
       for (int j = 0; j < TOK; ++j) {
-        uint32_t before = 0, all = 0;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          const uint32_t v = s_cnt[j][w];
-          before += w < wave ? v : 0u;
-          all += v;
-        }
-        const uint32_t rank = tie_base + before + lanes_below(mt[j]);
+        const uint32_t rank = tie_base + s_wcnt[j * kWaves + wave] + lanes_below(mt[j]);
         sel[j] = kv[j] != kNoKey && (kv[j] > tau || (kv[j] == tau && rank < take));
-        tie_base += all;
+        tie_base += s_ltot[j];
       }
+      __syncthreads();  // the tie prefixes are read
     }
     uint64_t ms[TOK];
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
       ms[j] = __ballot(sel[j]);
-      if (lane == 0) s_cnt2[j][wave] = (uint32_t)__popcll(ms[j]);
+      if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(ms[j]);
     }
-    __syncthreads();
+    scan_wave_counts<TOK>(s_wcnt, s_ltot);
     uint32_t sel_base = 0;
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
-      uint32_t before = 0, all = 0;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const uint32_t v = s_cnt2[j][w];
-        before += w < wave ? v : 0u;
-        all += v;
-      }
-      const uint32_t q = sel_base + before + lanes_below(ms[j]);
+      const uint32_t q = sel_base + s_wcnt[j * kWaves + wave] + lanes_below(ms[j]);
       if (sel[j] && q < (uint32_t)kKeepMax && base + q < (uint32_t)pr.k)
         lds.keep[q] = t0 + j * kTH + tid;
-      sel_base += all;
+      sel_base += s_ltot[j];
     }
     n_sel = min(n_sel, (uint32_t)kKeepMax);
   }
@@ -717,17 +750,8 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane);
     attn_step<DT, kG, kDh>(ws, st, a.scale_log2, lane);
   }
-  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, out_stores);
-}
-
-// Inclusive prefix sum within each row of 16 lanes (DPP row shifts); the
-// rows must be whole (all 16 lanes active).
-__device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t x) {
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true);  // row_shr:1
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true);  // row_shr:2
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true);  // row_shr:4
-  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true);  // row_shr:8
-  return x;
+  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
+                 out_stores);
 }
 
 // The level-1 bins of four selection rows at once: per head h, the unique bin
@@ -745,12 +769,15 @@ __device__ __forceinline__ void select_bin1024x4(const uint32_t* h, uint32_t tar
     if (lane == 63) s_wsum[g][wave] = inc[g];
   }
   __syncthreads();
+  if (tid < kG * kWaves) {  // per head, the waves' sums to their exclusive prefix
+    uint32_t* f = &s_wsum[0][0];
+    const uint32_t v = f[tid];
+    f[tid] = row16_inclusive_scan(v) - v;
+  }
+  __syncthreads();
 #pragma unroll
   for (int g = 0; g < kG; ++g) {
-    uint32_t before = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) before += w < wave ? s_wsum[g][w] : 0u;
-    const uint32_t above = before + inc[g] - x[g];
+    const uint32_t above = s_wsum[g][wave] + inc[g] - x[g];
     if (above + x[g] >= target && above < target) {
       s_res[g][0] = kL1 - 1 - tid;
       s_res[g][1] = above;
@@ -1034,16 +1061,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
     // g's selection, or its ties at tau; g = 4: the union) counts its
     // stage-j tokens per wave, then one 16-lane row scan per list gives each
     // wave's exclusive prefix and the list's total.
-    auto scan_lists = [&]() {
-      __syncthreads();
-      if (tid < kLists * kWaves) {
-        const uint32_t xw = s_wcnt[tid];
-        const uint32_t inc = row16_inclusive_scan(xw);
-        s_wcnt[tid] = inc - xw;
-        if ((tid & (kWaves - 1)) == kWaves - 1) s_ltot[tid / kWaves] = inc;
-      }
-      __syncthreads();
-    };
+    auto scan_lists = [&]() { scan_wave_counts<kLists>(s_wcnt, s_ltot); };
     // the chunk's ties at tau, for heads that take only some of them (their
     // ranks, lowest columns first)
     if (partial) {
@@ -1174,7 +1192,8 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
     kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane, msk);
     attn_step<DT, kG, kDh, true>(ws, st, a.scale_log2, lane);
   }
-  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, out_stores);
+  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
+                 out_stores);
 }
 
 inline _Float16 f16_one() { return (_Float16)1.0f; }
