@@ -341,9 +341,9 @@ int lap_sparse_attn_decode_ragged(const void* q, int64_t q_sb, int64_t q_sh,
  *          be NULL when the call selects nothing: k = 0, or k_cols = 0)
  *   T      code columns scored (the grid; plans clamp to it), T_kv K/V rows
  *   q, K, V as lap_sparse_attn_decode; G = Hq / Hkv must be 4
- * Group selection with D = 128 runs as one launch (per KV row, the
- * workgroups of one XCD score, select and attend, and the last merges);
- * other shapes run the kernel chain.  Workspace: lap_decode_step_workspace_size
+ * With D = 128, group and per-head selection run as one launch (per KV
+ * row, the workgroups of one XCD score, select and attend, and the last
+ * merges); other shapes run the kernel chain.  Workspace: lap_decode_step_workspace_size
  * with keep_max = k + sink + tail (ragged: k_cols + max_sink + max_tail).  It
  * must be zero-filled once before its first use; every call leaves its
  * barrier words at zero again.  Calls that share a workspace must be ordered

@@ -260,8 +260,8 @@ class SparseDecoder:
     def _decode_step(self, q, codes, keys, vals, T, T_kv, p, plans, k_cols, max_sink,
                      max_tail) -> None:
         """lap_decode_step (through the compiled torch op): scoring, top-k
-        and sparse attention after the LUT (one launch for group selection,
-        the kernel chain otherwise)."""
+        and sparse attention after the LUT (one launch for group and
+        per-head selection at D = 128, the kernel chain otherwise)."""
         if p is None:
             p = dict(cand_start=0, cand_end=0, k=0, sink=0, tail_start=0, tail_count=0)
         keys, vals = keys[:, :, :T_kv], vals[:, :, :T_kv]
