@@ -67,7 +67,8 @@ namespace {
 
 constexpr int kTH = 1024;
 constexpr int kWaves = kTH / 64;
-constexpr int kMaxTok = 8;          // tokens per thread (chunk = TOK * 1024)
+constexpr int kMaxTok = 16;         // tokens per thread (chunk = TOK * 1024)
+constexpr int kMaxTokPH = 8;        // the same with per-head selection
 constexpr int kHC = 4;              // level-1 histogram copies
 constexpr int kDh = 128;            // head dim of the fused path
 constexpr int kKeepMax = 8192;      // a workgroup's own selection (32 KiB of LDS)
@@ -659,33 +660,33 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       for (int j = 0; j < TOK; ++j)
         sel[j] = kv[j] != kNoKey && (kv[j] > tau || (all_ties && kv[j] == tau));
     } else {
-      uint64_t mt[TOK];
 #pragma unroll
       for (int j = 0; j < TOK; ++j) {
-        mt[j] = __ballot(kv[j] != kNoKey && kv[j] == tau);
-        if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(mt[j]);
+        const uint64_t mt = __ballot(kv[j] != kNoKey && kv[j] == tau);
+        if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(mt);
       }
       scan_wave_counts<TOK>(s_wcnt, s_ltot);
       uint32_t tie_base = 0;
 #pragma unroll
       for (int j = 0; j < TOK; ++j) {
-        const uint32_t rank = tie_base + s_wcnt[j * kWaves + wave] + lanes_below(mt[j]);
+        const uint64_t mt = __ballot(kv[j] != kNoKey && kv[j] == tau);
+        const uint32_t rank = tie_base + s_wcnt[j * kWaves + wave] + lanes_below(mt);
         sel[j] = kv[j] != kNoKey && (kv[j] > tau || (kv[j] == tau && rank < take));
         tie_base += s_ltot[j];
       }
       __syncthreads();  // the tie prefixes are read
     }
-    uint64_t ms[TOK];
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
-      ms[j] = __ballot(sel[j]);
-      if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(ms[j]);
+      const uint64_t ms = __ballot(sel[j]);
+      if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(ms);
     }
     scan_wave_counts<TOK>(s_wcnt, s_ltot);
     uint32_t sel_base = 0;
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
-      const uint32_t q = sel_base + s_wcnt[j * kWaves + wave] + lanes_below(ms[j]);
+      const uint64_t ms = __ballot(sel[j]);
+      const uint32_t q = sel_base + s_wcnt[j * kWaves + wave] + lanes_below(ms);
       if (sel[j] && q < (uint32_t)kKeepMax && base + q < (uint32_t)pr.k)
         lds.keep[q] = t0 + j * kTH + tid;
       sel_base += s_ltot[j];
@@ -796,7 +797,7 @@ __device__ __forceinline__ void select_bin1024x4(const uint32_t* h, uint32_t tar
 // The split merge is the group kernel's.
 template <int DT, int TOK>
 __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
-  static_assert(TOK >= 1 && TOK <= kMaxTok, "TOK");
+  static_assert(TOK >= 1 && TOK <= kMaxTokPH, "TOK");
   static_assert(kG * kL1 * 4 <= kKeepMax * 4 && kG * kMaxWR * kL2 * 4 <= kKeepMax * 4,
                 "H and H2 tables fit the keep list's half");
   __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
@@ -805,7 +806,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   __shared__ uint32_t s_h2[kG][kL2], s_wsum[kG][kWaves], s_res[kG][4], s_sel[kG][4];
   constexpr int kLists = (kG + 1) * TOK;
   static_assert(kWaves == 16, "one 16-lane row per list");
-  __shared__ uint32_t s_wcnt[(kG + 1) * kMaxTok * kWaves], s_ltot[(kG + 1) * kMaxTok];
+  __shared__ uint32_t s_wcnt[(kG + 1) * kMaxTokPH * kWaves], s_ltot[(kG + 1) * kMaxTokPH];
   __shared__ uint32_t s_gtw[kG][kWaves];
   __shared__ uint32_t s_flag;
   __shared__ float s_m[kWaves][4], s_l[kWaves][4];
@@ -1225,7 +1226,10 @@ int xcd_info(XcdInfo* out) {
 struct FusedPlan {
   int nxcc, RX, WR, tok, grid;
 };
-bool fused_plan(int R, int T, int keep_max, FusedPlan* p) {
+// k_sel bounds a workgroup's own selection (the call's k, or k_cols): a
+// chunk longer than the LDS keep list needs k_sel <= kKeepMax.  Chunks of 9
+// to 16 tokens per thread run as 16 (group selection only).
+bool fused_plan(int R, int T, bool per_head, int k_sel, FusedPlan* p) {
   static const int mode = [] {
     const char* e = getenv("LAPRUNE_FUSED");
     return e ? atoi(e) : 1;
@@ -1239,9 +1243,10 @@ bool fused_plan(int R, int T, int keep_max, FusedPlan* p) {
   WR = std::min(WR, std::max(1, (T + kTH - 1) / kTH));
   if (WR < 1) return false;
   const int ch = (T + WR - 1) / WR;
-  const int tok = (ch + kTH - 1) / kTH;
-  if (tok < 1 || tok > kMaxTok) return false;
-  (void)keep_max;  // a workgroup keeps at most its chunk's tokens: tok * 1024 <= kKeepMax
+  int tok = (ch + kTH - 1) / kTH;
+  if (tok > 8) tok = 16;
+  if (tok < 1 || tok > (per_head ? kMaxTokPH : kMaxTok)) return false;
+  if (tok * kTH > kKeepMax && k_sel > kKeepMax) return false;
   *p = FusedPlan{xi.nxcc, RX, WR, tok, xi.nxcc * RX * WR};
   return true;
 }
@@ -1292,6 +1297,9 @@ void launch_fused_dt(const StepArgs& a, int tok, int grid, bool per_head, hipStr
     LAP_STEP(1) LAP_STEP(2) LAP_STEP(3) LAP_STEP(4) LAP_STEP(5) LAP_STEP(6) LAP_STEP(7)
     LAP_STEP(8)
 #undef LAP_STEP
+    case 16:  // group selection only (fused_plan)
+      hipLaunchKernelGGL((step_fused_kernel<DT, 16>), dim3(grid), dim3(kTH), 0, st, a);
+      break;
   }
 }
 
@@ -1300,10 +1308,10 @@ void launch_fused_dt(const StepArgs& a, int tok, int grid, bool per_head, hipStr
 // Bytes at the start of a lap_decode_step workspace that only the fused
 // kernel uses: the status words, barrier lines and row histograms (kept zero
 // between calls, whatever path a call takes) and, when the fused kernel applies to this
-// shape, its level-2 tables and partials.
-size_t decode_step_fused_bytes(int R, int T, int keep_max, int head_rows) {
+// shape (with either selection), its level-2 tables and partials.
+size_t decode_step_fused_bytes(int R, int T, int head_rows) {
   FusedPlan fp;
-  if (!fused_plan(R, T, keep_max, &fp)) return carve_step(nullptr, R, 0, head_rows).bytes;
+  if (!fused_plan(R, T, false, 0, &fp)) return carve_step(nullptr, R, 0, head_rows).bytes;
   return carve_step(nullptr, R, fp.WR, head_rows).bytes;
 }
 
@@ -1319,9 +1327,8 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
                       void* out, void* workspace, size_t ws_bytes, int head_rows,
                       bool per_head, const char* who, hipStream_t st) {
   const int R = B * Hkv;
-  const int keep_max = plans ? k_cols + max_sink + max_tail : k + sink + tail_count;
   FusedPlan fp;
-  if (!fused_plan(R, T, keep_max, &fp)) return LAP_ERR_UNSUPPORTED;
+  if (!fused_plan(R, T, per_head, plans ? k_cols : k, &fp)) return LAP_ERR_UNSUPPORTED;
   if (!score_g4_supported(codes, cs_b, cs_h, cs_t)) return LAP_ERR_UNSUPPORTED;
   // query fragments are read as 8-byte vectors
   if ((reinterpret_cast<uintptr_t>(q) & 7) || (q_sb & 3) || (q_sh & 3)) return LAP_ERR_UNSUPPORTED;
@@ -1429,7 +1436,7 @@ int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
   ChainWs cw;
   int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
   if (s != LAP_OK) return s;
-  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max, head_rows), 256);
+  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, head_rows), 256);
   if (need_all)
     LAP_CHECK_CODE(workspace && workspace_bytes >= fused + cw.ret + cw.attn, LAP_ERR_WORKSPACE,
                    "%s: workspace of %zu bytes needed", who, fused + cw.ret + cw.attn);
@@ -1487,7 +1494,7 @@ extern "C" int lap_decode_step_workspace_size(int B, int Hq, int Hkv, int T, int
   ChainWs cw;
   int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
   if (s != LAP_OK) return s;
-  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, keep_max, B * Hkv), 256);
+  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, B * Hkv), 256);
   *bytes = fused + cw.ret + cw.attn;
   return LAP_OK;
 }

@@ -10,7 +10,8 @@ off its row's XCD, no barrier gave up).  Shapes cover the C2 size (131072
 columns, 32 workgroups per KV row), rows served by one workgroup (no split
 merge), chunks of one to eight tokens per thread, two rows per XCD (B = 2),
 fp16 and bf16, all-equal scores (ties: lowest columns win), keep-everything
-budgets, ragged device plans and graph replays with rewritten plans.
+budgets, ragged device plans and graph replays with rewritten plans; B = 16
+at 32768 columns takes two workgroups per row and 16 tokens per thread.
 """
 import numpy as np
 import pytest
@@ -73,6 +74,7 @@ def _decoder(cb, dev, B, T, dt, key_dt, topk=None, mask_out=0.98, select="group"
     (1, 300, 256, torch.bfloat16, torch.bfloat16, 16, False, "group"),      # one workgroup per row
     (1, 8192, 8192, torch.float16, torch.bfloat16, None, False, "group"),   # C1 size: 8 x 1024
     (2, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False, "group"),  # 2 rows per XCD
+    (16, 32768, 32768, torch.bfloat16, torch.bfloat16, 1024, False, "group"),  # 16 tokens/thread
     # per-head selection (the reference's rule)
     (1, 131072, 131008, torch.bfloat16, torch.bfloat16, None, False, "head"),  # k = 2621
     (1, 131072, 131072, torch.bfloat16, torch.bfloat16, 2048, False, "head"),
