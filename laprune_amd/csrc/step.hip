@@ -283,6 +283,84 @@ struct Lds {
   float* o;                  // A: [kWaves][4][kDh]
 };
 
+// The row a workgroup serves (KV row r, its chunk c of the row's TOK * 1024
+// columns), or false when the grid has no row for it.
+struct StepPos {
+  int r, c, b, hkv, h0, t0, t1;
+  StepRow pr;
+};
+template <int TOK>
+__device__ __forceinline__ bool step_pos(const StepArgs& a, StepPos* p) {
+  const int nx = a.nxcc;
+  const int x = blockIdx.x % nx, slot = blockIdx.x / nx;
+  const int rs = slot / a.WR, c = slot - rs * a.WR;
+  const int r = rs * nx + x;
+  if (rs >= a.RX || r >= a.B * a.Hkv) return false;
+  p->r = r;
+  p->c = c;
+  p->b = r / a.Hkv;
+  p->hkv = r - p->b * a.Hkv;
+  p->h0 = p->hkv * kG;
+  p->pr = step_row(a, p->b);
+  p->t0 = c * TOK * kTH;
+  p->t1 = min(p->pr.t_end, p->t0 + TOK * kTH);
+  return true;
+}
+
+// The query fragments of the attention phase (A-operand layout of
+// attn_core.h), requested at the start so that their latency hides behind S.
+__device__ __forceinline__ void load_q_frags(const StepArgs& a, int b, int h0, int lane,
+                                             i16x4 (&qpre)[kDh / 16]) {
+  const int rq = lane >> 4, cq = lane & 15;
+  const uint16_t* qp =
+      a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (cq < kG ? cq : 0)) * a.q_sh + rq * (kDh / 4);
+#pragma unroll
+  for (int ks = 0; ks < kDh / 16; ++ks) {
+    const uint2 w = *reinterpret_cast<const uint2*>(qp + 4 * ks);  // 8-byte aligned (host check)
+    qpre[ks] = cq < kG ? __builtin_bit_cast(i16x4, w) : i16x4{0, 0, 0, 0};
+  }
+}
+
+// S: the row's table into LDS, then TOK stages of 1024 tokens scored with one
+// stage's code rows in flight ahead (the scorer's pipeline, score_core.h);
+// body(j, t, e0, e1, e2, e3) gets stage j's token t and its four head scores.
+// Tokens past the chunk end load its last row (in bounds); the body sees
+// their column t >= t1.
+template <int TOK, typename Body>
+__device__ __forceinline__ void score_chunk(const StepArgs& a, const StepPos& p,
+                                            uint4* __restrict__ lut_lds, Body&& body) {
+  const int tid = threadIdx.x;
+  constexpr int kFill = kLutBytes / 16 / kTH;
+  const uint4* src = reinterpret_cast<const uint4*>(a.lut + (int64_t)p.r * (kG * kM * kK));
+  u32x4 f[kFill];
+#pragma unroll
+  for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * kTH + tid);
+  const uint8_t* crow = a.codes + (int64_t)p.b * a.cs_b + (int64_t)p.hkv * a.cs_h;
+  u32x4 cc[TOK][2];
+  auto request = [&](int j) {
+    const int t = min(p.t0 + j * kTH + tid, p.t1 - 1);
+    const uint8_t* q = crow + (int64_t)t * a.cs_t;
+    cc[j][0] = gload16_ordered(q);
+    cc[j][1] = gload16_ordered(q + 16);
+  };
+  request(0);
+#pragma unroll
+  for (int i = 0; i < kFill; ++i) {
+    vm_wait(kFill - 1 - i + 2, f[i]);
+    lut_lds[i * kTH + tid] = as_uint4(f[i]);
+  }
+  lds_barrier();
+  const char* tab = reinterpret_cast<const char*>(lut_lds);
+#pragma unroll
+  for (int j = 0; j < TOK; ++j) {
+    vm_wait(0, cc[j][0], cc[j][1]);
+    if (j + 1 < TOK) request(j + 1);
+    float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
+    score_token(tab, as_uint4(cc[j][0]), as_uint4(cc[j][1]), a.one, e0, e1, e2, e3);
+    body(j, p.t0 + j * kTH + tid, e0, e1, e2, e3);
+  }
+}
+
 // The end of a row's step, shared by both fused kernels: the waves' (m, l,
 // o) combined in LDS into the workgroup's partial, then the row's last
 // workgroup to arrive merges the partials (E) and writes the output.  Waves
@@ -455,31 +533,14 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   lds.keep = reinterpret_cast<int*>(s_big);
   lds.o = reinterpret_cast<float*>(s_big) + kKeepMax;
 
-  const int nx = a.nxcc;
-  const int x = blockIdx.x % nx, slot = blockIdx.x / nx;
-  const int rs = slot / a.WR, c = slot - rs * a.WR;
-  const int r = rs * nx + x;
-  if (rs >= a.RX || r >= a.B * a.Hkv) return;  // no row here
+  StepPos ps;
+  if (!step_pos<TOK>(a, &ps)) return;  // no row here
+  const int r = ps.r, c = ps.c, b = ps.b, hkv = ps.hkv, h0 = ps.h0, t0 = ps.t0, t1 = ps.t1;
+  const StepRow pr = ps.pr;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = r / a.Hkv, hkv = r - b * a.Hkv;
-  const StepRow pr = step_row(a, b);
-  constexpr int CH = TOK * kTH;
-  const int t0 = c * CH, t1 = min(pr.t_end, t0 + CH);
   const bool select = pr.k > 0;
-  const int h0 = hkv * kG;
-  // The query fragments of the attention phase (A-operand layout of
-  // attn_core.h), requested now so that their latency hides behind S.
   i16x4 qpre[kDh / 16];
-  {
-    const int rq = lane >> 4, cq = lane & 15;
-    const uint16_t* qp =
-        a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (cq < kG ? cq : 0)) * a.q_sh + rq * (kDh / 4);
-#pragma unroll
-    for (int ks = 0; ks < kDh / 16; ++ks) {
-      const uint2 w = *reinterpret_cast<const uint2*>(qp + 4 * ks);  // 8-byte aligned (host check)
-      qpre[ks] = cq < kG ? __builtin_bit_cast(i16x4, w) : i16x4{0, 0, 0, 0};
-    }
-  }
+  load_q_frags(a, b, h0, lane, qpre);
 
   // ---------------------------------------------------------------- S
   uint32_t kv[TOK];
@@ -487,41 +548,14 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   for (int j = 0; j < TOK; ++j) kv[j] = kNoKey;
   for (int i = tid; i < kHC * kH1Pitch; i += kTH) s_hist[i] = 0;
   if (select && t0 < t1) {
-    constexpr int kFill = kLutBytes / 16 / kTH;
-    const uint4* src = reinterpret_cast<const uint4*>(a.lut + (int64_t)r * (kG * kM * kK));
-    u32x4 f[kFill];
-#pragma unroll
-    for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * kTH + tid);
-    const uint8_t* crow = a.codes + (int64_t)b * a.cs_b + (int64_t)hkv * a.cs_h;
-    u32x4 cc[TOK][2];
-    auto request = [&](int j) {
-      const int t = min(t0 + j * kTH + tid, t1 - 1);
-      const uint8_t* p = crow + (int64_t)t * a.cs_t;
-      cc[j][0] = gload16_ordered(p);
-      cc[j][1] = gload16_ordered(p + 16);
-    };
-    request(0);
-#pragma unroll
-    for (int i = 0; i < kFill; ++i) {
-      vm_wait(kFill - 1 - i + 2, f[i]);
-      lds.lut[i * kTH + tid] = as_uint4(f[i]);
-    }
-    lds_barrier();
-    const char* tab = reinterpret_cast<const char*>(lds.lut);
     const int copy = (int)(__lane_id() % kHC) * kH1Pitch;
-#pragma unroll
-    for (int j = 0; j < TOK; ++j) {
-      vm_wait(0, cc[j][0], cc[j][1]);
-      if (j + 1 < TOK) request(j + 1);
-      float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
-      score_token(tab, as_uint4(cc[j][0]), as_uint4(cc[j][1]), a.one, e0, e1, e2, e3);
-      const int t = t0 + j * kTH + tid;
+    score_chunk<TOK>(a, ps, lds.lut, [&](int j, int t, float e0, float e1, float e2, float e3) {
       if (t < t1 && t >= pr.cs && t < pr.ce) {
         const uint32_t key = key_of_score(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)), a.key_bf16);
         kv[j] = key;
         atomicAdd(&s_hist[copy + (key >> kLoBits)], 1u);
       }
-    }
+    });
   }
   __syncthreads();
   // The query fragments are waited for here, where nothing else is in
@@ -817,29 +851,14 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   lds.keep = reinterpret_cast<int*>(s_big);
   lds.o = reinterpret_cast<float*>(s_big) + kKeepMax;
 
-  const int nx = a.nxcc;
-  const int x = blockIdx.x % nx, slot = blockIdx.x / nx;
-  const int rs = slot / a.WR, c = slot - rs * a.WR;
-  const int r = rs * nx + x;
-  if (rs >= a.RX || r >= a.B * a.Hkv) return;  // no row here
+  StepPos ps;
+  if (!step_pos<TOK>(a, &ps)) return;  // no row here
+  const int r = ps.r, c = ps.c, b = ps.b, hkv = ps.hkv, h0 = ps.h0, t0 = ps.t0, t1 = ps.t1;
+  const StepRow pr = ps.pr;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = r / a.Hkv, hkv = r - b * a.Hkv;
-  const StepRow pr = step_row(a, b);
-  constexpr int CH = TOK * kTH;
-  const int t0 = c * CH, t1 = min(pr.t_end, t0 + CH);
   const bool select = pr.k > 0;
-  const int h0 = hkv * kG;
   i16x4 qpre[kDh / 16];
-  {
-    const int rq = lane >> 4, cq = lane & 15;
-    const uint16_t* qp =
-        a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (cq < kG ? cq : 0)) * a.q_sh + rq * (kDh / 4);
-#pragma unroll
-    for (int ks = 0; ks < kDh / 16; ++ks) {
-      const uint2 w = *reinterpret_cast<const uint2*>(qp + 4 * ks);  // 8-byte aligned (host check)
-      qpre[ks] = cq < kG ? __builtin_bit_cast(i16x4, w) : i16x4{0, 0, 0, 0};
-    }
-  }
+  load_q_frags(a, b, h0, lane, qpre);
 
   // ---------------------------------------------------------------- S
   // kp[j]: the four heads' keys of stage j's token (heads 0, 1 in .x, 2, 3
@@ -848,34 +867,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   uint32_t inw = 0;
   for (int i = tid; i < kG * kH1Pitch; i += kTH) s_hist[i] = 0;
   if (select && t0 < t1) {
-    constexpr int kFill = kLutBytes / 16 / kTH;
-    const uint4* src = reinterpret_cast<const uint4*>(a.lut + (int64_t)r * (kG * kM * kK));
-    u32x4 f[kFill];
-#pragma unroll
-    for (int i = 0; i < kFill; ++i) f[i] = gload16_ordered(src + i * kTH + tid);
-    const uint8_t* crow = a.codes + (int64_t)b * a.cs_b + (int64_t)hkv * a.cs_h;
-    u32x4 cc[TOK][2];
-    auto request = [&](int j) {
-      const int t = min(t0 + j * kTH + tid, t1 - 1);
-      const uint8_t* p = crow + (int64_t)t * a.cs_t;
-      cc[j][0] = gload16_ordered(p);
-      cc[j][1] = gload16_ordered(p + 16);
-    };
-    request(0);
-#pragma unroll
-    for (int i = 0; i < kFill; ++i) {
-      vm_wait(kFill - 1 - i + 2, f[i]);
-      lds.lut[i * kTH + tid] = as_uint4(f[i]);
-    }
-    lds_barrier();
-    const char* tab = reinterpret_cast<const char*>(lds.lut);
-#pragma unroll
-    for (int j = 0; j < TOK; ++j) {
-      vm_wait(0, cc[j][0], cc[j][1]);
-      if (j + 1 < TOK) request(j + 1);
-      float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
-      score_token(tab, as_uint4(cc[j][0]), as_uint4(cc[j][1]), a.one, e0, e1, e2, e3);
-      const int t = t0 + j * kTH + tid;
+    score_chunk<TOK>(a, ps, lds.lut, [&](int j, int t, float e0, float e1, float e2, float e3) {
       kp[j] = make_uint2(0u, 0u);
       if (t < t1 && t >= pr.cs && t < pr.ce) {
         const uint32_t k0 = key_of_score(e0, a.key_bf16), k1 = key_of_score(e1, a.key_bf16);
@@ -887,7 +879,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
         atomicAdd(&s_hist[2 * kH1Pitch + (k2 >> kLoBits)], 1u);
         atomicAdd(&s_hist[3 * kH1Pitch + (k3 >> kLoBits)], 1u);
       }
-    }
+    });
   }
   __syncthreads();
 #pragma unroll
