@@ -366,8 +366,9 @@ __device__ __forceinline__ void score_chunk(const StepArgs& a, const StepPos& p,
 // workgroup to arrive merges the partials (E) and writes the output.  Waves
 // nw.. ran no attention step (their state is empty) and are left out.
 // out_stores issues the stores nothing in the launch reads (index rows and
-// the like); every workgroup calls it once, after its merge arrival.
-template <int DT, typename Stores>
+// the like); every workgroup calls it once, after its merge arrival (the
+// merging workgroup: with EARLY, as soon as its partial loads are out).
+template <int DT, bool EARLY, typename Stores>
 __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, kDh>& ws,
                                            const Lds& lds, float (&s_m)[kWaves][4],
                                            float (&s_l)[kWaves][4], uint32_t& s_flag, int r,
@@ -472,6 +473,11 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     const int s2 = min(half * kHalf + u, a.WR - 1);
     v[u] = ld_dev(rp + ((int64_t)s2 * kG + g_o) * (kDh + 2) + 2 + d_o);
   }
+  // EARLY: this workgroup's own output stores go out behind the loads, so
+  // that their acknowledgements overlap the merge instead of following it
+  // (a kernel that stores little here; per-head selection clears four
+  // histograms, whose stores would hold up the merge's waits instead)
+  if (EARLY) out_stores();
   float mt = -INFINITY, lt = 0.f;
   if (tid < kMaxWR * kG) {
     // (m, l) as one 8-byte load (a partial's head record starts 8-byte
@@ -512,7 +518,7 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     const float l = slw[g] + slw[kG + g];
     a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
   }
-  out_stores();
+  if (!EARLY) out_stores();
 }
 
 template <int DT, int TOK>
@@ -785,7 +791,7 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane);
     attn_step<DT, kG, kDh>(ws, st, a.scale_log2, lane);
   }
-  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
+  finish_row<DT, true>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
                  out_stores);
 }
 
@@ -1185,7 +1191,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
     kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane, msk);
     attn_step<DT, kG, kDh, true>(ws, st, a.scale_log2, lane);
   }
-  finish_row<DT>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
+  finish_row<DT, false>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
                  out_stores);
 }
 
