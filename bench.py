@@ -430,16 +430,32 @@ def _graph_us(body, n: int, reps: int, stream) -> float:
     return ev0.elapsed_time(ev1) * 1e3 / (reps * n)
 
 
-def score_floors(score_only, stream, reps: int) -> dict:
-    """Where the scorer's time goes: the same launch replayed on one code set,
-    whose 32 MiB then stay in the 256 MB Infinity Cache, takes HBM out of the
-    loop; what remains is the kernel's own compute, LDS and launch cost."""
+def score_floors(score_only, floor_empty, floor_stream, stream, reps: int) -> dict:
+    """Where the scorer's time goes, each figure graph-replayed back to back
+    over the rotating code sets like score_kernel_us:
+    * the same launch replayed on one code set, whose 32 MiB then stay in the
+      256 MB Infinity Cache, takes HBM out of the loop; what remains is the
+      kernel's own compute, LDS and launch cost;
+    * an empty kernel with the scorer's grid and LDS (dispatch and drain);
+    * the scorer's reads alone (table into LDS, code rows one stage ahead as
+      the scorer requests them, or all four stages up front), without its
+      lookups and adds."""
     one_set = _graph_us(lambda j: score_only(0), N_CODE_SETS, reps, stream)
+    empty = _graph_us(floor_empty, N_CODE_SETS, reps, stream)
+    reads1 = _graph_us(floor_stream(1), N_CODE_SETS, reps, stream)
+    reads4 = _graph_us(floor_stream(4), N_CODE_SETS, reps, stream)
     return {"same_set_us": round(one_set, 3),
+            "launch_us": round(empty, 3),
+            "reads_us": round(reads1, 3),
+            "reads_all_ahead_us": round(reads4, 3),
             "hbm_floor_us": round(CODE_BYTES / (HBM_PEAK_GBS * 1e3), 3),
             "note": ("same_set_us: the scorer launch replayed on one code set "
-                     "(Infinity-Cache resident), graph-replayed back to back like "
-                     "score_kernel_us; hbm_floor_us: the code bytes at the 8 TB/s peak")}
+                     "(Infinity-Cache resident); launch_us: an empty kernel with the "
+                     "scorer's grid and LDS (lap_floor_empty); reads_us / "
+                     "reads_all_ahead_us: the scorer's table and code reads alone, one "
+                     "stage or all four stages in flight (lap_floor_stream); all "
+                     "graph-replayed back to back like score_kernel_us; hbm_floor_us: "
+                     "the code bytes at the 8 TB/s peak")}
 
 
 def main():
@@ -503,6 +519,18 @@ def main():
         N.call("lap_retrieve_score", N.ptr(dec.lut), N.ptr(c), c.stride(0), c.stride(1),
                c.stride(2), 1, HKV, T, plan["cand_start"], plan["cand_end"], N.KEY_BF16, None,
                N.ptr(ws), ws.numel(), N.stream_of(c))
+
+    floor_out = torch.empty(HKV * ((T + 4095) // 4096), dtype=torch.int32, device=dev)
+
+    def floor_empty(i):
+        N.call("lap_floor_empty", HKV, T, N.stream_of(floor_out))
+
+    def floor_stream(ahead):
+        def run(i):
+            c = codes_sets[i % N_CODE_SETS][:, :, :T]
+            N.call("lap_floor_stream", N.ptr(dec.lut), N.ptr(c), c.stride(1), c.stride(2), HKV,
+                   T, ahead, N.ptr(floor_out), N.stream_of(c))
+        return run
 
     if args.counters:
         # one LUT per set is enough: the scorer's traffic does not depend on it
@@ -593,7 +621,8 @@ def main():
     torch.cuda.synchronize()
     score_us = ev0.elapsed_time(ev1) * 1e3 / (reps * n_sets)
     score_gbs = CODE_BYTES / (score_us * 1e-6) / 1e9
-    floors = None if args.eager else score_floors(score_only, stream, reps)
+    floors = (None if args.eager else
+              score_floors(score_only, floor_empty, floor_stream, stream, reps))
 
     # ---- timed region 1: K full sparse decode steps
     log(f"timing {args.steps} sparse steps")

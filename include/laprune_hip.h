@@ -477,6 +477,24 @@ int lap_rope_append(const void* q, int64_t q_sb, int64_t q_sh,
                     void* cache_v, int64_t cv_sb, int64_t cv_sh, int64_t cv_st,
                     int t_cap, void* q_out, lap_stream_t stream);
 
+/* ======================================================================= *
+ * Measurement kernels (no counterpart in the reference; not on the path).  *
+ * They time what the fused G = 4 scorer's launch shape costs before any   *
+ * scoring: bench.py reports them beside the scorer.  Both take the        *
+ * scorer's grid for R KV rows of T tokens (R * ceil(T / 4096) workgroups   *
+ * of 1024 threads).                                                        *
+ * lap_floor_empty: no work, the scorer's 68 KiB of LDS per workgroup.      *
+ * lap_floor_stream: the scorer's reads without its lookups and adds: each  *
+ *   workgroup copies row r's 64 KiB GMKG table (lut + r * 32768 fp16) into *
+ *   LDS and reads the 32-byte code rows codes + r * cs_r + t * cs_t of its  *
+ *   4096 tokens (t clamped to T - 1), `ahead` (1 or 4) of its four         *
+ *   1024-token stages in flight.  out[i] (u32, one per workgroup) is the    *
+ *   XOR of every 32-bit word the workgroup read.                           *
+ * ======================================================================= */
+int lap_floor_empty(int R, int T, lap_stream_t stream);
+int lap_floor_stream(const void* lut, const void* codes, int64_t cs_r, int64_t cs_t,
+                     int R, int T, int ahead, uint32_t* out, lap_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,6 +93,8 @@ SIGNATURES = {
                         vp, i64, i64, i64, vp, vp],
     "lap_encode_keys_ranges": [vp, i32, i64, i64, i64, i32, i32, vp, i32, i32, i32, vp, i32, i32,
                                vp, sz, vp, i64, i64, i64, vp],
+    "lap_floor_empty": [i32, i32, vp],
+    "lap_floor_stream": [vp, vp, i64, i64, i32, i32, i32, vp, vp],
 }
 
 _lock = threading.Lock()

@@ -179,3 +179,16 @@ def test_torch_binding_registers_the_hot_ops():
         schema = str(getattr(o, name).default._schema)
         assert schema.startswith(f"laprune::{name}("), schema
         assert frag in schema, (name, schema)
+
+
+def test_floor_kernels_check_their_arguments(lib):
+    """The scorer's measurement kernels reject bad shapes before any launch."""
+    from laprune_amd import _native as N
+    al = C.c_void_p(4096)  # never dereferenced: validation fails first
+    st = lib.lap_floor_stream(al, al, 0, 32, 8, 131072, 2, al, None)
+    assert st == N.LAP_ERR_INVALID and "ahead must be 1 or 4" in _err(lib)
+    st = lib.lap_floor_stream(al, al, 0, 16, 8, 131072, 1, al, None)
+    assert st == N.LAP_ERR_INVALID and "32 bytes apart" in _err(lib)
+    st = lib.lap_floor_stream(None, al, 0, 32, 8, 131072, 1, al, None)
+    assert st == N.LAP_ERR_INVALID and "null pointer" in _err(lib)
+    assert lib.lap_floor_empty(0, 10, None) == N.LAP_ERR_INVALID
