@@ -93,8 +93,14 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 __device__ __forceinline__ float h2f(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
-// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32, default mode).
+// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32, default mode),
+// from the fp32 value as rounded.  The empty asm keeps the compiler from
+// folding the instruction that produced f into the conversion: it turns
+// fp16(fmaf(a, b, c)) into v_fma_mixlo_f16, which rounds the exact result to
+// fp16 once, and so differs from fp16(fp32(a * b + c)) where the fp32
+// rounding lands on an fp16 midpoint.
 __device__ __forceinline__ uint16_t f2h(float f) {
+  asm("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 // bf16 bits -> fp32 (exact: the bf16 pattern is the high half of the fp32).
