@@ -106,6 +106,48 @@ __device__ __forceinline__ void emit_keys(const ScoreOut& so, const RowCols& rc,
   }
 }
 
+// The same outputs in two halves, for the pipelined scorer: the histogram
+// counts of token t (LDS atomics, inside the stage loop) and its global
+// stores (fp16 scores, keys), issued after the loop.  A token is held as its
+// four fp16 head scores (two per word) and, for group rows, its key gk
+// (the key of fp16(max of the four fp32 scores), as emit_keys forms it).
+__device__ __forceinline__ uint32_t key_of_f16(const ScoreOut& so, uint16_t h) {
+  return so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(h) : f16_key(h);
+}
+template <int HC>
+__device__ __forceinline__ void count_keys(const ScoreOut& so, const RowCols& rc, int t,
+                                           uint32_t h01, uint32_t h23, uint32_t gk,
+                                           HistRows<HC> s_hist) {
+  if (!so.hist || t < rc.cs || t >= rc.ce) return;
+  const int copy = (int)(__lane_id() % HC) * kHPitch;
+  if (so.per_head) {
+    const uint16_t h[kG] = {(uint16_t)h01, (uint16_t)(h01 >> 16), (uint16_t)h23,
+                            (uint16_t)(h23 >> 16)};
+#pragma unroll
+    for (int g = 0; g < kG; ++g) atomicAdd(&s_hist[g][copy + (key_of_f16(so, h[g]) >> 8)], 1u);
+  } else {
+    atomicAdd(&s_hist[0][copy + (gk >> 8)], 1u);
+  }
+}
+__device__ __forceinline__ void store_token(const ScoreOut& so, int r, int T, int t, uint32_t h01,
+                                            uint32_t h23, uint32_t gk) {
+  const uint16_t h[kG] = {(uint16_t)h01, (uint16_t)(h01 >> 16), (uint16_t)h23,
+                          (uint16_t)(h23 >> 16)};
+  if (so.heads) {
+    uint16_t* hp = so.heads + (int64_t)(r * kG) * T + t;
+#pragma unroll
+    for (int g = 0; g < kG; ++g) hp[g * (int64_t)T] = h[g];
+  }
+  if (!so.keys) return;
+  if (so.per_head) {
+#pragma unroll
+    for (int g = 0; g < kG; ++g)
+      so.keys[((int64_t)r * kG + g) * T + t] = (uint16_t)key_of_f16(so, h[g]);
+  } else {
+    so.keys[(int64_t)r * T + t] = (uint16_t)gk;
+  }
+}
+
 
 // Pipelined fused scorer (either table layout).  A workgroup owns THREADS * TOK
 // consecutive tokens of one KV row; thread tid scores tokens
@@ -199,7 +241,12 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
     s_hist[i / (HC * kHPitch)][i % (HC * kHPitch)] = 0;
   lds_barrier();
 
+  // The scores stay in registers (fp16, two per word) until every stage is
+  // in: a store issued between two stage waits would count in the next
+  // wait (stores and loads share vmcnt), which would then wait for the
+  // store's acknowledgement as well as for the stage.
   const char* lds = reinterpret_cast<const char*>(s_lut);
+  uint32_t h01[TOK], h23[TOK], gk[TOK];
 #pragma unroll
   for (int j = 0; j < TOK; ++j) {
     // Stages requested after stage j so far: j+1 .. min(j+kAhead-1, TOK-1).
@@ -208,16 +255,16 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
     if (j + kAhead < TOK) request(j + kAhead);
     float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
     score_token(lds, as_uint4(c[j][0]), as_uint4(c[j][1]), one, e0, e1, e2, e3);
+    h01[j] = (uint32_t)f2h(e0) | ((uint32_t)f2h(e1) << 16);
+    h23[j] = (uint32_t)f2h(e2) | ((uint32_t)f2h(e3) << 16);
+    gk[j] = so.per_head ? 0u : key_of_f16(so, f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3))));
     const int t = t0 + j * THREADS + tid;
-    if (t >= t1) continue;
-    if (so.heads) {
-      uint16_t* hp = so.heads + (int64_t)(r * kG) * T + t;
-      hp[0] = f2h(e0);
-      hp[(int64_t)T] = f2h(e1);
-      hp[2 * (int64_t)T] = f2h(e2);
-      hp[3 * (int64_t)T] = f2h(e3);
-    }
-    emit_keys<HC>(so, rc, r, T, t, e0, e1, e2, e3, s_hist);
+    if (t < t1) count_keys<HC>(so, rc, t, h01[j], h23[j], gk[j], s_hist);
+  }
+#pragma unroll
+  for (int j = 0; j < TOK; ++j) {
+    const int t = t0 + j * THREADS + tid;
+    if (t < t1) store_token(so, r, T, t, h01[j], h23[j], gk[j]);
   }
 
   if (so.hist) {
