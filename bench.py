@@ -11,17 +11,26 @@ selection = top-2048 per KV group on the max of its 4 query-head scores,
 plus 4 sink and 64 local tokens.
 
 One step = LUT build -> fused score (+ level-1 histogram) -> radix top-k ->
-sparse attention over the kept rows read in place from the cache, captured
-in a HIP graph.  Twelve code/query sets and four K/V sets (~2.5 GB) rotate
-so that the 256 MB Infinity Cache cannot serve the step from cache.
+sparse attention over the kept rows read in place from the cache: two
+launches (the LUT kernel, then the one-launch step), issued eagerly through
+the compiled torch ops, as the reference's decode loop calls its kernels
+once per layer per token (aq_evaluation.py:146-253).  Twelve code/query sets
+and four K/V sets (~2.5 GB) rotate so that the 256 MB Infinity Cache cannot
+serve the step from cache.
 
 ``value``        code bytes / average duration of the fused scorer kernel,
                  timed with HIP events around graph replays on the launch
                  stream, before the step and comparator legs run.
-``ms_per_step``  wall time of one full sparse decode step.
+``ms_per_step``  wall time of one full sparse decode step, K steps issued
+                 back to back eagerly and timed between two synchronisations
+                 (``host_issue_us``: the host's time to issue one step, which
+                 stays below the step's GPU time, so the figure is the GPU's).
 ``dense_step_us`` the same GPU's split-K flash-decode over all 131072 tokens
-                 (this build's own MFMA kernel, the comparator of record).
-                 Both step figures replay one graph per step.
+                 (this build's own MFMA kernel, the comparator of record),
+                 timed the same way.
+``graph_per_step`` the same two steps with one HIP graph replayed per step:
+                 each replay adds about 6 us of GPU time (a graph launch)
+                 to both sides.
 ``in_graph``     the same sparse and dense steps, twelve consecutive steps
                  (one per code/query set) captured in one graph, as a
                  model's decode graph holds its layers: per-step time
@@ -261,7 +270,7 @@ def sdpa_decode_seconds(args, kv_sets, q_sets) -> float | None:
         return None
 
 
-def reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets, dense_s) -> dict:
+def reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets, dense_s, dense_graph_s) -> dict:
     """The reference's own selection at C2: top-k per query head (not per KV
     group) on scores cast to bf16, budget n - int(0.98 n) = 2621 of n = 131004
     candidates (aq_evaluation.py:166, 185-199), then attention over each
@@ -281,34 +290,17 @@ def reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets, dense_s) -> dict:
         return dec.step(q_sets[i % N_CODE_SETS], c[:, :, :T], kk[:, :, :T], vv[:, :, :T])
 
     log("reference-mode leg: per-head selection")
-    for i in range(2):
+    for i in range(max(args.warmup, 2)):
         step(i)
-    torch.cuda.synchronize()
-    if args.eager:
-        run = step
-    else:
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for i in range(2):
-                step(i)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        graphs = []
-        for j in range(N_CODE_SETS):
-            gph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gph):
-                step(j)
-            graphs.append(gph)
-        run = lambda i: graphs[i % N_CODE_SETS].replay()  # noqa: E731
-    for i in range(args.warmup):
-        run(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        run(i)
-    torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / args.steps
+    step_s, host_s = _time_steps(step, args.steps)
+    graph = None
+    if not args.eager:
+        (run,) = _graphs_of([step], N_CODE_SETS)
+        for i in range(args.warmup):
+            run(i)
+        g_s, _ = _time_steps(run, args.steps)
+        graph = {"sparse_step_us": round(g_s * 1e6, 2),
+                 "speedup_vs_dense": round(dense_graph_s / g_s, 3)}
     step(0)
     torch.cuda.synchronize()
     sel = dec.selected()
@@ -319,7 +311,9 @@ def reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets, dense_s) -> dict:
                       f"mask_out 0.98) + {SINK} sink + {LOCAL} local"),
         "k": k,
         "sparse_step_us": round(step_s * 1e6, 2),
+        "host_issue_us": round(host_s * 1e6, 2),
         "speedup_vs_dense": round(dense_s / step_s, 3),
+        "graph_per_step": graph,
         "selection_check": ok,
     }
 
@@ -361,39 +355,23 @@ def ragged_leg(args, dev, cb) -> dict:
     sel = dec.selected()
     ok = bool(sel.shape[-1] == RAG_TOPK and int(sel.min()) >= SINK
               and int((sel < 0).sum()) == 0)
-    if args.eager:
-        run_s, run_d = sparse, dense_
-    else:
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for i in range(2):
-                sparse(i)
-                dense_(i)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        sg, dg = [], []
-        for j in range(RAG_SETS):
-            for fn, lst in ((sparse, sg), (dense_, dg)):
-                gph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(gph):
-                    fn(j)
-                lst.append(gph)
-        run_s = lambda i: sg[i % RAG_SETS].replay()  # noqa: E731
-        run_d = lambda i: dg[i % RAG_SETS].replay()  # noqa: E731
     for i in range(args.warmup):
-        run_s(i)
-        run_d(i)
-    torch.cuda.synchronize()
+        sparse(i)
+        dense_(i)
     out = {}
-    for name, fn in (("sparse", run_s), ("dense", run_d)):
+    for name, fn in (("sparse", sparse), ("dense", dense_)):
         log(f"timing {args.steps} ragged {name} steps")
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(args.steps):
-            fn(i)
-        torch.cuda.synchronize()
-        out[name] = (time.perf_counter() - t0) / args.steps
+        out[name], out[name + "_host"] = _time_steps(fn, args.steps)
+    graph = None
+    if not args.eager:
+        run_s, run_d = _graphs_of([sparse, dense_], RAG_SETS)
+        for i in range(args.warmup):
+            run_s(i)
+            run_d(i)
+        g_s, _ = _time_steps(run_s, args.steps)
+        g_d, _ = _time_steps(run_d, args.steps)
+        graph = {"sparse_step_us": round(g_s * 1e6, 2), "dense_step_us": round(g_d * 1e6, 2),
+                 "speedup_vs_dense": round(g_d / g_s, 3)}
     kv_bytes = sum(lens) * HKV * D * 2 * 2
     return {
         "workload": ("C5 layer: batch 16, context lengths uniform in [16384, 32768] (seeded), "
@@ -402,11 +380,50 @@ def ragged_leg(args, dev, cb) -> dict:
         "lengths": lens,
         "sparse_step_us": round(out["sparse"] * 1e6, 2),
         "dense_step_us": round(out["dense"] * 1e6, 2),
+        "host_issue_us": round(out["sparse_host"] * 1e6, 2),
         "speedup_vs_dense": round(out["dense"] / out["sparse"], 3),
+        "graph_per_step": graph,
         "dense_hbm_gbs": round(kv_bytes / out["dense"] / 1e9, 1),
         "score_code_bytes": sum(t_codes) * HKV * M,
         "selection_check": ok,
     }
+
+
+def _time_steps(run, steps: int) -> tuple[float, float]:
+    """(seconds per step, host issue seconds per step) of `steps` calls of
+    run(i) back to back, between two synchronisations."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        run(i)
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, (t1 - t0) / steps
+
+
+def _graphs_of(fns, n: int):
+    """One captured graph per input set j < n for each function fns[f](j),
+    after two warm-up calls on a side stream; returns replay callables."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(2):
+            for fn in fns:
+                fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    out = []
+    for fn in fns:
+        gs = []
+        for j in range(n):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                fn(j)
+            gs.append(gph)
+        out.append(lambda i, gs=gs: gs[i % len(gs)].replay())
+    return out
 
 
 def _graph_us(body, n: int, reps: int, stream) -> float:
@@ -591,9 +608,9 @@ def main():
 
     # ---- scorer kernel duration: HIP events on the launch stream around a
     # graph of back-to-back scorer launches over the rotating code sets,
-    # after as many untimed replays as are timed: after the step legs the
-    # first few hundred launches run up to ~1.4 us slower than the steady
-    # state they then settle to.
+    # after at least 2048 untimed launches (about 27 ms): after other work
+    # the first few hundred launches run up to ~1.4 us slower than the
+    # steady state they then settle to.
     log("timing the scorer kernel")
     reps = max(1, args.steps // n_sets)
     stream = torch.cuda.current_stream()
@@ -609,7 +626,7 @@ def main():
         with torch.cuda.graph(gsc):
             for j in range(n_sets):
                 score_only(j)
-        for _ in range(reps):
+        for _ in range(max(reps, -(-2048 // n_sets))):
             gsc.replay()
         torch.cuda.synchronize()
         ev0 = torch.cuda.Event(enable_timing=True)
@@ -624,23 +641,30 @@ def main():
     floors = (None if args.eager else
               score_floors(score_only, floor_empty, floor_stream, stream, reps))
 
-    # ---- timed region 1: K full sparse decode steps
+    # ---- timed region 1: K full sparse decode steps, issued eagerly
+    for i in range(args.warmup):
+        sparse_step(i)
+        dense_step(i)
     log(f"timing {args.steps} sparse steps")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        run_sparse(i)
-    torch.cuda.synchronize()
-    sparse_s = (time.perf_counter() - t0) / args.steps
+    sparse_s, sparse_host_s = _time_steps(sparse_step, args.steps)
 
     # ---- timed region 2: K dense decode steps on the same GPU
     log(f"timing {args.steps} dense steps")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        run_dense(i)
-    torch.cuda.synchronize()
-    dense_s = (time.perf_counter() - t0) / args.steps
+    dense_s, dense_host_s = _time_steps(dense_step, args.steps)
+
+    # ---- the same two steps, one graph replay per step
+    graph_per_step = None
+    dense_graph_s = dense_s
+    if not args.eager:
+        log(f"timing {args.steps} sparse and dense steps, one graph replay each")
+        g_sparse_s, _ = _time_steps(run_sparse, args.steps)
+        dense_graph_s, _ = _time_steps(run_dense, args.steps)
+        graph_per_step = {
+            "sparse_step_us": round(g_sparse_s * 1e6, 2),
+            "dense_step_us": round(dense_graph_s * 1e6, 2),
+            "speedup_vs_dense": round(dense_graph_s / g_sparse_s, 3),
+            "note": ("each step one HIP graph replay; a replay adds about 6 us of GPU "
+                     "time (the graph launch) to both sides")}
 
     # ---- the same steps back to back inside one graph: N_CODE_SETS steps
     # per replay, each over its own set, the way a model's decode graph holds
@@ -658,8 +682,7 @@ def main():
                     "speedup_vs_dense": round(ig_dense / ig_sparse, 3),
                     "note": ("N_CODE_SETS consecutive steps (each over its own code/query "
                              "set) captured in one graph and replayed; per-step time = "
-                             "replay time / steps.  sparse_step_us and dense_step_us above "
-                             "replay one graph per step and so include a replay's overhead")}
+                             "replay time / steps")}
 
     # ---- stock framework decode: torch SDPA (fused backends only)
     sdpa_s = sdpa_decode_seconds(args, kv_sets, q_sets)
@@ -707,13 +730,17 @@ def main():
                          "top-2048 per KV group (group max) + 4 sink + 64 local; bf16 K/V"),
             "context": T, "batch": 1, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
             "codebooks": M, "entries": K, "topk": TOPK, "sink": SINK, "local": LOCAL,
+            "step_launch": "eager: the LUT kernel, then the one-launch step",
             "graphs": not args.eager,
         },
         "hbm_frac": round(score_gbs / HBM_PEAK_GBS, 4),
         "sparse_step_us": round(sparse_s * 1e6, 2),
         "dense_step_us": round(dense_s * 1e6, 2),
         "speedup_vs_dense": round(dense_s / sparse_s, 3),
+        "host_issue_us": {"sparse": round(sparse_host_s * 1e6, 2),
+                          "dense": round(dense_host_s * 1e6, 2)},
         "dense_hbm_gbs": round(2 * HKV * T * D * 2 / dense_s / 1e9, 1),
+        "graph_per_step": graph_per_step,
         "in_graph": in_graph,
         "sdpa_step_us": None if sdpa_s is None else round(sdpa_s * 1e6, 2),
         "speedup_vs_sdpa": None if sdpa_s is None else round(sdpa_s / sparse_s, 3),
@@ -740,7 +767,7 @@ def main():
     }
     if not args.no_reference_mode:
         result["reference_mode"] = reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets,
-                                                      dense_s)
+                                                      dense_s, dense_graph_s)
     if not args.no_ragged:
         result["ragged"] = ragged_leg(args, dev, cb)
     if not args.no_cpu_baseline:
