@@ -76,41 +76,13 @@ __device__ __forceinline__ void write_empty_hist(const ScoreOut& so, int r, int 
   write_hists<1>(so, nullptr, r, R, chunk, tid, threads);
 }
 
-// Selection keys of token t of KV row r and their level-1 histogram counts
-// (inside the candidate window): the group max of the four fp16 head scores
-// (fp16 rounding is monotone, so fp16(max) == max of the fp16 scores), or
-// with per_head each head's own key.
-template <int HC>
-__device__ __forceinline__ void emit_keys(const ScoreOut& so, const RowCols& rc, int r, int T,
-                                          int t, float e0, float e1, float e2, float e3,
-                                          HistRows<HC> s_hist) {
-  if (!so.keys && !so.hist) return;
-  const bool counted = so.hist && t >= rc.cs && t < rc.ce;
-  const int copy = (int)(__lane_id() % HC) * kHPitch;
-  auto key_of = [&](float e) {
-    const uint16_t h = f2h(e);
-    return so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(h) : f16_key(h);
-  };
-  if (so.per_head) {
-    const float e[kG] = {e0, e1, e2, e3};
-#pragma unroll
-    for (int g = 0; g < kG; ++g) {
-      const uint32_t key = key_of(e[g]);
-      if (so.keys) so.keys[((int64_t)r * kG + g) * T + t] = (uint16_t)key;
-      if (counted) atomicAdd(&s_hist[g][copy + (key >> 8)], 1u);
-    }
-  } else {
-    const uint32_t key = key_of(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)));
-    if (so.keys) so.keys[(int64_t)r * T + t] = (uint16_t)key;
-    if (counted) atomicAdd(&s_hist[0][copy + (key >> 8)], 1u);
-  }
-}
-
-// The same outputs in two halves, for the pipelined scorer: the histogram
-// counts of token t (LDS atomics, inside the stage loop) and its global
-// stores (fp16 scores, keys), issued after the loop.  A token is held as its
-// four fp16 head scores (two per word) and, for group rows, its key gk
-// (the key of fp16(max of the four fp32 scores), as emit_keys forms it).
+// Selection keys and their level-1 histogram counts, in two halves for the
+// pipelined scorer: the counts of token t (LDS atomics over the candidate
+// window, inside the stage loop) and its global stores (fp16 scores, keys),
+// issued after the loop.  A token is held as its four fp16 head scores (two
+// per word) and, for group rows, its key gk: the key of fp16(max of the four
+// fp32 scores), which equals the max of the four fp16 scores' keys since
+// fp16 rounding is monotone.  Per-head rows key each head's own score.
 __device__ __forceinline__ uint32_t key_of_f16(const ScoreOut& so, uint16_t h) {
   return so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(h) : f16_key(h);
 }
