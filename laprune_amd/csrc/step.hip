@@ -838,6 +838,7 @@ __device__ __forceinline__ void select_bin1024x4(const uint32_t* h, uint32_t tar
 template <int DT, int TOK>
 __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   static_assert(TOK >= 1 && TOK <= kMaxTokPH, "TOK");
+  static_assert(kMaxTokPH * kTH <= kKeepMax, "a chunk's union fits the keep list");
   static_assert(kG * kL1 * 4 <= kKeepMax * 4 && kG * kMaxWR * kL2 * 4 <= kKeepMax * 4,
                 "H and H2 tables fit the keep list's half");
   __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
@@ -908,6 +909,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
 
   // ---------------------------------------------------------------- B1, H
   uint32_t n_sel = 0;
+  uint32_t hbase[kG] = {0u, 0u, 0u, 0u};  // where each head's selection of this chunk starts
   if (select) {
     if (tid == 0) record_xcd(a, r);  // complete before B2's arrival
     wg_row_barrier(a, r, 0);
@@ -1053,6 +1055,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
     for (int g = 0; g < kG; ++g) {
       take[g] = s_sel[g][0];
       base[g] = s_sel[g][1];
+      hbase[g] = base[g];
       ties[g] = s_sel[g][2];
       partial |= take[g] > 0 && take[g] < ties[g];
     }
@@ -1096,49 +1099,78 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
         selb |= (sj ? 1u : 0u) << (4 * j + g);
       }
     }
-    auto chosen = [&](int j, int g) -> bool {
-      return g < kG ? ((selb >> (4 * j + g)) & 1u) != 0u : ((selb >> (4 * j)) & 0xfu) != 0u;
-    };
     if (partial) __syncthreads();  // the tie prefixes are read
-#pragma unroll
-    for (int j = 0; j < TOK; ++j)
-#pragma unroll
-      for (int g = 0; g <= kG; ++g) {
-        const uint64_t m = __ballot(chosen(j, g));
-        if (lane == 0) s_wcnt[(g * TOK + j) * kWaves + wave] = (uint32_t)__popcll(m);
-      }
-    scan_lists();
-    uint32_t lbase[kG + 1] = {0u, 0u, 0u, 0u, 0u};
+    // The union (keys any head keeps) in column order, with each key's head
+    // bits: the keep list of A, and the source of the four index rows, which
+    // out_stores writes after the merge arrival (head g's row is the union's
+    // keys with bit g, in order).
 #pragma unroll
     for (int j = 0; j < TOK; ++j) {
-      const int col = t0 + j * kTH + tid;
-#pragma unroll
-      for (int g = 0; g <= kG; ++g) {
-        const bool sj = chosen(j, g);
-        const uint64_t m = __ballot(sj);
-        const uint32_t q = lbase[g] + s_wcnt[(g * TOK + j) * kWaves + wave] + lanes_below(m);
-        if (sj) {
-          if (g < kG) {
-            if (base[g] + q < (uint32_t)pr.k) {
-              const int64_t irow = ((int64_t)b * a.Hkv * kG + h0 + g) * a.k_cols + base[g];
-              if (a.idx_i64) put_idx<int64_t>(a.idx, irow + q, col);
-              else put_idx<int32_t>(a.idx, irow + q, col);
-            }
-          } else if (q < (uint32_t)kKeepMax) {
-            lds.keep[q] = col;
-            s_kmask[q] = (uint8_t)((selb >> (4 * j)) & 0xfu);
-          }
-        }
-        lbase[g] += s_ltot[g * TOK + j];
-      }
+      const uint64_t m = __ballot(((selb >> (4 * j)) & 0xfu) != 0u);
+      if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(m);
     }
-    n_sel = min(lbase[kG], (uint32_t)kKeepMax);
+    scan_wave_counts<TOK>(s_wcnt, s_ltot);
+    uint32_t ubase = 0;
+#pragma unroll
+    for (int j = 0; j < TOK; ++j) {
+      const uint32_t bits = (selb >> (4 * j)) & 0xfu;
+      const uint64_t m = __ballot(bits != 0u);
+      const uint32_t q = ubase + s_wcnt[j * kWaves + wave] + lanes_below(m);
+      if (bits) {
+        lds.keep[q] = t0 + j * kTH + tid;
+        s_kmask[q] = (uint8_t)bits;
+      }
+      ubase += s_ltot[j];
+    }
+    n_sel = ubase;
   }
   lds_barrier();  // the keep list
 
-  // Index-row padding of ragged rows and the histogram clear, after the
-  // merge arrival (the index rows themselves were written above).
+  // The stores nothing in this launch reads, after the merge arrival: the
+  // chunk's part of the four index rows, ragged rows' padding, and the
+  // histogram clear.  Thread t takes union entries [t E, t E + E); its rank
+  // among each head's keys comes from a block scan of per-thread counts
+  // (two heads per word, 16 bits each: a chunk keeps at most 8192 keys).
   auto out_stores = [&]() {
+    if (n_sel > 0) {
+      const int E = ((int)n_sel + kTH - 1) / kTH;
+      const int p0 = min(tid * E, (int)n_sel), p1 = min(p0 + E, (int)n_sel);
+      uint32_t c01 = 0, c23 = 0;
+      for (int p = p0; p < p1; ++p) {
+        const uint32_t m = s_kmask[p];
+        c01 += (m & 1u) | ((m & 2u) << 15);
+        c23 += ((m >> 2) & 1u) | ((m & 8u) << 13);
+      }
+      const uint32_t i01 = wave_inclusive_scan(c01), i23 = wave_inclusive_scan(c23);
+      __syncthreads();  // s_wsum is free again
+      if (lane == 63) {
+        s_wsum[0][wave] = i01;
+        s_wsum[1][wave] = i23;
+      }
+      __syncthreads();
+      if (tid < 2 * kWaves) {  // the waves' sums to their exclusive prefix, one row per pair
+        uint32_t* f = &s_wsum[tid / kWaves][tid % kWaves];
+        const uint32_t v = *f;
+        *f = row16_inclusive_scan(v) - v;
+      }
+      __syncthreads();
+      const uint32_t e01 = s_wsum[0][wave] + i01 - c01, e23 = s_wsum[1][wave] + i23 - c23;
+      uint32_t rk[kG] = {e01 & 0xffffu, e01 >> 16, e23 & 0xffffu, e23 >> 16};
+      for (int p = p0; p < p1; ++p) {
+        const uint32_t m = s_kmask[p];
+        const int col = lds.keep[p];
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          if (!((m >> g) & 1u)) continue;
+          const uint32_t q = hbase[g] + rk[g]++;
+          if (q < (uint32_t)pr.k) {
+            const int64_t i = ((int64_t)b * a.Hkv * kG + h0 + g) * a.k_cols + q;
+            if (a.idx_i64) put_idx<int64_t>(a.idx, i, col);
+            else put_idx<int32_t>(a.idx, i, col);
+          }
+        }
+      }
+    }
     if (a.plans) {  // pad [k, k_cols) of the four rows with -1, split over the workgroups
       const int pad = a.k_cols - pr.k;
       const int ps = (pad + a.WR - 1) / a.WR;
