@@ -243,21 +243,6 @@ __device__ __forceinline__ void select_bin1024(const uint32_t* h, uint32_t targe
   }
   __syncthreads();
 }
-// The same over 64 bins, by wave 0 (every thread synchronises).
-__device__ __forceinline__ void select_bin64(const uint32_t* h, uint32_t target,
-                                             uint32_t* s_res) {
-  if (threadIdx.x < kL2) {
-    const int l = threadIdx.x;
-    const uint32_t x = h[kL2 - 1 - l];
-    const uint32_t inc = wave_inclusive_scan(x);
-    if (inc >= target && inc - x < target) {
-      s_res[0] = kL2 - 1 - l;
-      s_res[1] = inc - x;
-    }
-  }
-  __syncthreads();
-}
-
 // Per-wave counts of TOK-stage token lists to positions: s_wcnt[l][w] holds
 // list l's count in wave w; afterwards it holds the exclusive prefix over
 // the waves, and s_ltot[l] the list's total.  One 16-lane row per list.
@@ -616,74 +601,60 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     // ------------------------------------------------------------ H2
     // The row's level-2 tables: the threshold tau = (b1, b2), the ties at
     // tau to take, and where this chunk's selection starts in the row's.
-    // Thread (chunk cc = tid / 32, q = tid % 32) holds bins 2q, 2q + 1 of
-    // chunk cc's table (and, for q = 0, its count above b1).
-    uint32_t* st2 = reinterpret_cast<uint32_t*>(lds.o);  // [kMaxWR][kL2] level-2 counts
-    uint32_t* s_cgt = st2 + kMaxWR * kL2;                // [kMaxWR] keys above tau per chunk
-    uint32_t* s_cti = s_cgt + kMaxWR;                    // [kMaxWR] ties at tau per chunk
-    const int cc = tid >> 5, qq = tid & 31;
-    const bool cin = cc < a.WR;
-    uint32_t v0, v1, v2;
-    {
-      const uint32_t* src2 = a.t2 + ((int64_t)r * a.WR + min(cc, a.WR - 1)) * kT2;
-      v0 = ld_dev(src2 + 2 * qq);
-      v1 = ld_dev(src2 + 2 * qq + 1);
-      v2 = qq == 0 ? ld_dev(src2 + kL2) : 0u;
-      if (!cin) v0 = v1 = v2 = 0u;
-      st2[cc * kL2 + 2 * qq] = v0;
-      st2[cc * kL2 + 2 * qq + 1] = v1;
-    }
-    __syncthreads();
-    if (tid < kL2) {
-      uint32_t t = 0;
-      for (int c2 = 0; c2 < a.WR; ++c2) t += st2[c2 * kL2 + tid];
-      s_h2[tid] = t;
-    }
-    __syncthreads();
-    const uint32_t k2 = (uint32_t)pr.k - gt1;
-    select_bin64(s_h2, k2, s_res);
-    const uint32_t b2 = s_res[0];
-    tau = (b1 << kLoBits) | b2;
-    const uint32_t need = k2 - s_res[1];  // ties at tau to take, >= 1
-    {
-      // per chunk: keys above tau (above b1, or in b1 with low bits above
-      // b2) and ties at tau, summed over the chunk's 32 threads
-      uint32_t g = v2 + ((uint32_t)(2 * qq) > b2 ? v0 : 0u) + ((uint32_t)(2 * qq + 1) > b2 ? v1 : 0u);
-      uint32_t ti = (uint32_t)(2 * qq) == b2 ? v0 : ((uint32_t)(2 * qq + 1) == b2 ? v1 : 0u);
-#pragma unroll
-      for (int d = 16; d >= 1; d >>= 1) {
-        g += __shfl_xor(g, d, 64);
-        ti += __shfl_xor(ti, d, 64);
-      }
-      if (qq == 0) {
-        s_cgt[cc] = g;
-        s_cti[cc] = ti;
-      }
-    }
-    __syncthreads();
+    // Wave 0 alone: lane l holds bin 63 - l of every chunk's table (chunks
+    // past WR read as zero) and, for l < WR, chunk l's count above b1.  The
+    // row's level-2 histogram, its suffix sums and the per-chunk sums are
+    // then register sums, one scan and two reductions, published with one
+    // barrier.
     if (wave == 0) {
-      const uint32_t g = lane < c ? s_cgt[lane] : 0u, ti = lane < c ? s_cti[lane] : 0u;
-      uint32_t gs = g, ts = ti;
+      const uint32_t k2 = (uint32_t)pr.k - gt1;  // keys to take from bin b1, >= 1
+      const uint32_t* t2r = a.t2 + (int64_t)r * a.WR * kT2;
+      const int bn = kL2 - 1 - lane;
+      uint32_t vt[kMaxWR];
+#pragma unroll
+      for (int c2 = 0; c2 < kMaxWR; ++c2) vt[c2] = ld_dev(t2r + min(c2, a.WR - 1) * kT2 + bn);
+      const uint32_t gt_l = ld_dev(t2r + min(lane, a.WR - 1) * kT2 + kL2);
+      uint32_t tot = 0, before = 0, mine = 0;  // bin bn: the row's, chunks < c, chunk c
+#pragma unroll
+      for (int c2 = 0; c2 < kMaxWR; ++c2) {
+        const uint32_t x = c2 < a.WR ? vt[c2] : 0u;
+        tot += x;
+        before += c2 < c ? x : 0u;
+        mine += c2 == c ? x : 0u;
+      }
+      // S(bn) = keys in b1 with low bits >= bn; b2 = the bin with
+      // S(b2) >= k2 > S(b2 + 1), lane L = 63 - b2
+      const uint32_t inc = wave_inclusive_scan(tot);
+      const uint64_t hit = __ballot(inc >= k2 && inc - tot < k2);
+      const int L = hit ? __builtin_ctzll(hit) : kL2 - 1;
+      const uint32_t need = k2 - (uint32_t)__builtin_amdgcn_readlane((int)(inc - tot), L);
+      const uint32_t ts = (uint32_t)__builtin_amdgcn_readlane((int)before, L);  // ties before c
+      const uint32_t my_ties = (uint32_t)__builtin_amdgcn_readlane((int)mine, L);
+      // keys above tau (above b1, or in b1 with low bits above b2: lanes
+      // below L) in the chunks before c, and in chunk c
+      uint32_t gs = (lane < L ? before : 0u) + (lane < c ? gt_l : 0u);
+      uint32_t mg = (lane < L ? mine : 0u) + (lane == c ? gt_l : 0u);
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) {
         gs += __shfl_xor(gs, d, 64);
-        ts += __shfl_xor(ts, d, 64);
+        mg += __shfl_xor(mg, d, 64);
       }
       if (lane == 0) {
-        const uint32_t my_ties = s_cti[c];
         const uint32_t tk = ts >= need ? 0u : min(my_ties, need - ts);
         // ties taken by the earlier chunks, min(need, ts), from an explicit
         // instruction: hipcc 7.2 at -O3 folds this min (written as min() or
         // as a select) to ts here, which is wrong once the row's ties run out
         uint32_t taken_before;
         asm volatile("v_min_u32 %0, %1, %2" : "=v"(taken_before) : "v"(need), "v"(ts));
+        s_res[0] = (uint32_t)(kL2 - 1 - L);
+        s_res[1] = my_ties;
         s_res[2] = tk;
         s_res[3] = gs + taken_before;
-        s_res[1] = my_ties;
-        s_flag = s_cgt[c] + tk;
+        s_flag = mg + tk;
       }
     }
     __syncthreads();
+    tau = (b1 << kLoBits) | s_res[0];
     take = s_res[2];
     base = s_res[3];
     n_sel = s_flag;
@@ -954,98 +925,51 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
     wg_row_barrier(a, r, 1);
 
     // ------------------------------------------------------------ H2
-    // Thread (head hh = tid / 256, chunk cc = tid / 8 % 32, q = tid % 8)
-    // holds bins 8q .. 8q + 7 of chunk cc's level-2 table of head hh (and,
-    // for q = 0, the chunk's count above b1).
-    uint32_t* st2 = lds.tot;                              // [kG][kMaxWR][kL2]
-    uint32_t* s_cgt = reinterpret_cast<uint32_t*>(lds.o);  // [kG][kMaxWR] keys above tau
-    uint32_t* s_cti = s_cgt + kG * kMaxWR;                 // [kG][kMaxWR] ties at tau
-    const int hh = tid >> 8, cc = (tid >> 3) & 31, qq = tid & 7;
-    const bool cin = cc < a.WR;
-    uint32_t v8[8], g1;
-    {
-      const uint32_t* src2 = a.t2 + (((int64_t)r * a.WR + min(cc, a.WR - 1)) * kG + hh) * kT2;
-      uint2 pr2[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pr2[i] = ld_dev2(reinterpret_cast<const uint2*>(src2 + 8 * qq + 2 * i));
-      g1 = ld_dev(src2 + kL2);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v8[2 * i] = cin ? pr2[i].x : 0u;
-        v8[2 * i + 1] = cin ? pr2[i].y : 0u;
-      }
-      g1 = cin && qq == 0 ? g1 : 0u;
-      uint32_t* dst = st2 + (hh * kMaxWR + cc) * kL2 + 8 * qq;
-      *reinterpret_cast<uint4*>(dst) = make_uint4(v8[0], v8[1], v8[2], v8[3]);
-      *reinterpret_cast<uint4*>(dst + 4) = make_uint4(v8[4], v8[5], v8[6], v8[7]);
-    }
-    __syncthreads();
-    if (tid < kG * kL2) {
-      const int g = tid / kL2, bin = tid % kL2;
-      uint32_t t = 0;
-      for (int c2 = 0; c2 < a.WR; ++c2) t += st2[(g * kMaxWR + c2) * kL2 + bin];
-      s_h2[g][bin] = t;
-    }
-    __syncthreads();
-    if (wave < kG) {  // wave g: head g's level-2 bin
+    // Waves 0..3, wave g for head g: lane l holds bin 63 - l of every
+    // chunk's level-2 table of head g (chunks past WR read as zero) and, for
+    // l < WR, chunk l's count above b1; the sums are those of the group
+    // step's H2, in registers, published with one barrier.
+    if (wave < kG) {
       const int g = wave;
-      const uint32_t k2 = (uint32_t)pr.k - gt1[g];
-      const uint32_t xv = s_h2[g][kL2 - 1 - lane];
-      const uint32_t inc = wave_inclusive_scan(xv);
-      if (inc >= k2 && inc - xv < k2) {
-        s_res[g][2] = kL2 - 1 - lane;
-        s_res[g][3] = inc - xv;
-      }
-    }
-    __syncthreads();
-    uint32_t tau[kG];
+      const uint32_t k2 = (uint32_t)pr.k - gt1[g];  // keys to take from bin b1[g], >= 1
+      const uint32_t* t2r = a.t2 + ((int64_t)r * a.WR * kG + g) * kT2;  // chunk stride kG * kT2
+      const int bn = kL2 - 1 - lane;
+      uint32_t vt[kMaxWR];
 #pragma unroll
-    for (int g = 0; g < kG; ++g) tau[g] = (b1[g] << kLoBits) | s_res[g][2];
-    {
-      // per chunk and head: keys above tau and ties at tau, over its 8 threads
-      uint32_t b2 = s_res[0][2];
+      for (int c2 = 0; c2 < kMaxWR; ++c2)
+        vt[c2] = ld_dev(t2r + (int64_t)min(c2, a.WR - 1) * kG * kT2 + bn);
+      const uint32_t gt_l = ld_dev(t2r + (int64_t)min(lane, a.WR - 1) * kG * kT2 + kL2);
+      uint32_t tot = 0, before = 0, mine = 0;  // bin bn: the row's, chunks < c, chunk c
 #pragma unroll
-      for (int g = 1; g < kG; ++g) b2 = hh == g ? s_res[g][2] : b2;
-      uint32_t gsum = g1, ti = 0;
+      for (int c2 = 0; c2 < kMaxWR; ++c2) {
+        const uint32_t x = c2 < a.WR ? vt[c2] : 0u;
+        tot += x;
+        before += c2 < c ? x : 0u;
+        mine += c2 == c ? x : 0u;
+      }
+      const uint32_t inc = wave_inclusive_scan(tot);
+      const uint64_t hit = __ballot(inc >= k2 && inc - tot < k2);
+      const int L = hit ? __builtin_ctzll(hit) : kL2 - 1;
+      const uint32_t need = k2 - (uint32_t)__builtin_amdgcn_readlane((int)(inc - tot), L);
+      const uint32_t ts = (uint32_t)__builtin_amdgcn_readlane((int)before, L);
+      const uint32_t my_ties = (uint32_t)__builtin_amdgcn_readlane((int)mine, L);
+      uint32_t gs = (lane < L ? before : 0u) + (lane < c ? gt_l : 0u);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t bin = (uint32_t)(8 * qq + i);
-        gsum += bin > b2 ? v8[i] : 0u;
-        ti += bin == b2 ? v8[i] : 0u;
-      }
-#pragma unroll
-      for (int d = 4; d >= 1; d >>= 1) {
-        gsum += __shfl_xor(gsum, d, 64);
-        ti += __shfl_xor(ti, d, 64);
-      }
-      if (qq == 0) {
-        s_cgt[hh * kMaxWR + cc] = gsum;
-        s_cti[hh * kMaxWR + cc] = ti;
-      }
-    }
-    __syncthreads();
-    if (wave < kG) {  // wave g: where head g's selection of this chunk starts
-      const int g = wave;
-      const uint32_t need = (uint32_t)pr.k - gt1[g] - s_res[g][3];  // ties at tau to take, >= 1
-      const uint32_t gv = lane < c ? s_cgt[g * kMaxWR + lane] : 0u;
-      const uint32_t tv = lane < c ? s_cti[g * kMaxWR + lane] : 0u;
-      uint32_t gs = gv, ts = tv;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) {
-        gs += __shfl_xor(gs, d, 64);
-        ts += __shfl_xor(ts, d, 64);
-      }
+      for (int d = 32; d >= 1; d >>= 1) gs += __shfl_xor(gs, d, 64);
       if (lane == 0) {
-        const uint32_t my_ties = s_cti[g * kMaxWR + c];
         const uint32_t tk = ts >= need ? 0u : min(my_ties, need - ts);
         uint32_t taken_before;  // min(need, ts), explicit (see step_fused_kernel)
         asm volatile("v_min_u32 %0, %1, %2" : "=v"(taken_before) : "v"(need), "v"(ts));
+        s_res[g][2] = (uint32_t)(kL2 - 1 - L);
         s_sel[g][0] = tk;
         s_sel[g][1] = gs + taken_before;
         s_sel[g][2] = my_ties;
       }
     }
     __syncthreads();
+    uint32_t tau[kG];
+#pragma unroll
+    for (int g = 0; g < kG; ++g) tau[g] = (b1[g] << kLoBits) | s_res[g][2];
 
     // Ordered compaction, per head (its index row) and of the union (the
     // keep list of A, with each key's head bits).
