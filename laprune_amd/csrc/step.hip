@@ -221,22 +221,24 @@ __device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t x) {
   return x;
 }
 
+// w[0] + ... + w[wave - 1] of kWaves words in LDS, in every lane of the
+// wave (every lane active).
+__device__ __forceinline__ uint32_t waves_before(const uint32_t* w, int wave, int lane) {
+  const int l = lane & (kWaves - 1);
+  const uint32_t v = l < wave ? w[l] : 0u;
+  return (uint32_t)__builtin_amdgcn_readlane((int)row16_inclusive_scan(v), kWaves - 1);
+}
+
 // The unique bin b of h[0..1023] with S(b) >= target > S(b+1), S(i) =
-// sum_{j >= i} h[j]: s_res = {b, S(b+1)}.  1024 threads, one bin each;
-// 1 <= target <= S(0).
-__device__ __forceinline__ void select_bin1024(const uint32_t* h, uint32_t target,
-                                               uint32_t* s_wsum, uint32_t* s_res) {
+// sum_{j >= i} h[j]: s_res = {b, S(b+1)}.  1024 threads, thread tid holding
+// x = h[1023 - tid]; 1 <= target <= S(0).
+__device__ __forceinline__ void select_bin1024(uint32_t x, uint32_t target, uint32_t* s_wsum,
+                                               uint32_t* s_res) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t x = h[kL1 - 1 - tid];
   const uint32_t inc = wave_inclusive_scan(x);
   if (lane == 63) s_wsum[wave] = inc;
   __syncthreads();
-  if (tid < kWaves) {  // the waves' sums to their exclusive prefix, in place
-    const uint32_t v = s_wsum[tid];
-    s_wsum[tid] = row16_inclusive_scan(v) - v;
-  }
-  __syncthreads();
-  const uint32_t above = s_wsum[wave] + inc - x;
+  const uint32_t above = waves_before(s_wsum, wave, lane) + inc - x;
   if (above + x >= target && above < target) {
     s_res[0] = kL1 - 1 - tid;
     s_res[1] = above;
@@ -263,7 +265,6 @@ __device__ __forceinline__ void scan_wave_counts(uint32_t* s_wcnt, uint32_t* s_l
 // LDS carve of the 64 KiB region that holds the table during S.
 struct Lds {
   uint4* lut;                // S: [kLutBytes / 16]
-  uint32_t* tot;             // H: [kL1]
   int* keep;                 // H2, A: [kKeepMax]
   float* o;                  // A: [kWaves][4][kDh]
 };
@@ -520,7 +521,6 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
 
   Lds lds;
   lds.lut = s_big;
-  lds.tot = reinterpret_cast<uint32_t*>(s_big);
   lds.keep = reinterpret_cast<int*>(s_big);
   lds.o = reinterpret_cast<float*>(s_big) + kKeepMax;
 
@@ -573,10 +573,9 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   if (select) {
     if (tid == 0) record_xcd(a, r);  // complete before B2's arrival
     wg_row_barrier(a, r, 0);
-    lds.tot[tid] = ld_dev(a.hist + (int64_t)r * kL1 + tid);
-    if (tid < kL2) s_h2[tid] = 0;
-    __syncthreads();
-    select_bin1024(lds.tot, (uint32_t)pr.k, s_wsum, s_res);
+    const uint32_t hx = ld_dev(a.hist + (int64_t)r * kL1 + kL1 - 1 - tid);
+    if (tid < kL2) s_h2[tid] = 0;  // ordered before H's adds by the selection's barriers
+    select_bin1024(hx, (uint32_t)pr.k, s_wsum, s_res);
     const uint32_t b1 = s_res[0], gt1 = s_res[1];
 #pragma unroll
     for (int j = 0; j < TOK; ++j)
@@ -768,28 +767,22 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
 
 // The level-1 bins of four selection rows at once: per head h, the unique bin
 // b of h[h][0..1023] with S(b) >= target > S(b+1); s_res[h] = {b, S(b+1)}.
-// 1024 threads, one bin each; 1 <= target <= S(0) for every head.
-__device__ __forceinline__ void select_bin1024x4(const uint32_t* h, uint32_t target,
+// 1024 threads, thread tid holding x[h] = h[h][1023 - tid]; 1 <= target <=
+// S(0) for every head.
+__device__ __forceinline__ void select_bin1024x4(const uint32_t (&x)[kG], uint32_t target,
                                                  uint32_t (&s_wsum)[kG][kWaves],
                                                  uint32_t (&s_res)[kG][4]) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t x[kG], inc[kG];
+  uint32_t inc[kG];
 #pragma unroll
   for (int g = 0; g < kG; ++g) {
-    x[g] = h[g * kL1 + kL1 - 1 - tid];
     inc[g] = wave_inclusive_scan(x[g]);
     if (lane == 63) s_wsum[g][wave] = inc[g];
   }
   __syncthreads();
-  if (tid < kG * kWaves) {  // per head, the waves' sums to their exclusive prefix
-    uint32_t* f = &s_wsum[0][0];
-    const uint32_t v = f[tid];
-    f[tid] = row16_inclusive_scan(v) - v;
-  }
-  __syncthreads();
 #pragma unroll
   for (int g = 0; g < kG; ++g) {
-    const uint32_t above = s_wsum[g][wave] + inc[g] - x[g];
+    const uint32_t above = waves_before(s_wsum[g], wave, lane) + inc[g] - x[g];
     if (above + x[g] >= target && above < target) {
       s_res[g][0] = kL1 - 1 - tid;
       s_res[g][1] = above;
@@ -810,8 +803,6 @@ template <int DT, int TOK>
 __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   static_assert(TOK >= 1 && TOK <= kMaxTokPH, "TOK");
   static_assert(kMaxTokPH * kTH <= kKeepMax, "a chunk's union fits the keep list");
-  static_assert(kG * kL1 * 4 <= kKeepMax * 4 && kG * kMaxWR * kL2 * 4 <= kKeepMax * 4,
-                "H and H2 tables fit the keep list's half");
   __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
   __shared__ uint32_t s_hist[kG * kH1Pitch];
   __shared__ uint8_t s_kmask[kKeepMax];
@@ -825,7 +816,6 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
 
   Lds lds;
   lds.lut = s_big;
-  lds.tot = reinterpret_cast<uint32_t*>(s_big);
   lds.keep = reinterpret_cast<int*>(s_big);
   lds.o = reinterpret_cast<float*>(s_big) + kKeepMax;
 
@@ -884,15 +874,12 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   if (select) {
     if (tid == 0) record_xcd(a, r);  // complete before B2's arrival
     wg_row_barrier(a, r, 0);
-    uint32_t* tot = lds.tot;  // [kG][kL1]
     uint32_t hv[kG];
 #pragma unroll
-    for (int g = 0; g < kG; ++g) hv[g] = ld_dev(a.hist + ((int64_t)r * kG + g) * kL1 + tid);
-#pragma unroll
-    for (int g = 0; g < kG; ++g) tot[g * kL1 + tid] = hv[g];
-    if (tid < kG * kL2) (&s_h2[0][0])[tid] = 0;
-    __syncthreads();
-    select_bin1024x4(tot, (uint32_t)pr.k, s_wsum, s_res);
+    for (int g = 0; g < kG; ++g)
+      hv[g] = ld_dev(a.hist + ((int64_t)r * kG + g) * kL1 + kL1 - 1 - tid);
+    if (tid < kG * kL2) (&s_h2[0][0])[tid] = 0;  // ordered before H's adds, as above
+    select_bin1024x4(hv, (uint32_t)pr.k, s_wsum, s_res);
     uint32_t b1[kG], gt1[kG];
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
