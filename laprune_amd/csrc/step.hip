@@ -221,6 +221,12 @@ __device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t x) {
   return x;
 }
 
+// The sum of x over the wave's 64 lanes (every lane active), in every lane:
+// a DPP scan read at lane 63 (no LDS permutes).
+__device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)wave_inclusive_scan(x), 63);
+}
+
 // w[0] + ... + w[wave - 1] of kWaves words in LDS, in every lane of the
 // wave (every lane active).
 __device__ __forceinline__ uint32_t waves_before(const uint32_t* w, int wave, int lane) {
@@ -580,9 +586,7 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
 #pragma unroll
     for (int j = 0; j < TOK; ++j)
       if (kv[j] != kNoKey && (kv[j] >> kLoBits) == b1) atomicAdd(&s_h2[kv[j] & (kL2 - 1)], 1u);
-    uint32_t gt = (uint32_t)tid > b1 ? h1 : 0u;
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) gt += __shfl_xor(gt, d, 64);
+    const uint32_t gt = wave_sum((uint32_t)tid > b1 ? h1 : 0u);
     if (lane == 0) s_gtw[wave] = gt;
     __syncthreads();
     uint32_t* t2 = a.t2 + ((int64_t)r * a.WR + c) * kT2;
@@ -631,13 +635,8 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       const uint32_t my_ties = (uint32_t)__builtin_amdgcn_readlane((int)mine, L);
       // keys above tau (above b1, or in b1 with low bits above b2: lanes
       // below L) in the chunks before c, and in chunk c
-      uint32_t gs = (lane < L ? before : 0u) + (lane < c ? gt_l : 0u);
-      uint32_t mg = (lane < L ? mine : 0u) + (lane == c ? gt_l : 0u);
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) {
-        gs += __shfl_xor(gs, d, 64);
-        mg += __shfl_xor(mg, d, 64);
-      }
+      const uint32_t gs = wave_sum((lane < L ? before : 0u) + (lane < c ? gt_l : 0u));
+      const uint32_t mg = wave_sum((lane < L ? mine : 0u) + (lane == c ? gt_l : 0u));
       if (lane == 0) {
         const uint32_t tk = ts >= need ? 0u : min(my_ties, need - ts);
         // ties taken by the earlier chunks, min(need, ts), from an explicit
@@ -894,9 +893,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
           if ((key(j, g) >> kLoBits) == b1[g]) atomicAdd(&s_h2[g][key(j, g) & (kL2 - 1)], 1u);
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
-      uint32_t gt = (uint32_t)tid > b1[g] ? h1[g] : 0u;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) gt += __shfl_xor(gt, d, 64);
+      const uint32_t gt = wave_sum((uint32_t)tid > b1[g] ? h1[g] : 0u);
       if (lane == 0) s_gtw[g][wave] = gt;
     }
     __syncthreads();
@@ -940,9 +937,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
       const uint32_t need = k2 - (uint32_t)__builtin_amdgcn_readlane((int)(inc - tot), L);
       const uint32_t ts = (uint32_t)__builtin_amdgcn_readlane((int)before, L);
       const uint32_t my_ties = (uint32_t)__builtin_amdgcn_readlane((int)mine, L);
-      uint32_t gs = (lane < L ? before : 0u) + (lane < c ? gt_l : 0u);
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) gs += __shfl_xor(gs, d, 64);
+      const uint32_t gs = wave_sum((lane < L ? before : 0u) + (lane < c ? gt_l : 0u));
       if (lane == 0) {
         const uint32_t tk = ts >= need ? 0u : min(my_ties, need - ts);
         uint32_t taken_before;  // min(need, ts), explicit (see step_fused_kernel)
