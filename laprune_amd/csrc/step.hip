@@ -221,6 +221,14 @@ __device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t x) {
   return x;
 }
 
+// x of lane (i + N) mod 16 in lane i's 16-lane row (DPP row_ror:N, every
+// lane active).
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  static_assert(N >= 1 && N <= 15, "row_ror:1..15");
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xf, 0xf, false));
+}
+
 // The sum of x over the wave's 64 lanes (every lane active), in every lane:
 // a DPP scan read at lane 63 (no LDS permutes).
 __device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
@@ -479,9 +487,12 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     const uint2 ml = ld_dev2(reinterpret_cast<const uint2*>(rp + (int64_t)sg * (kDh + 2)));
     mt = in ? __uint_as_float(ml.x) : -INFINITY;
     lt = in ? __uint_as_float(ml.y) : 0.f;
-    float mx = mt;  // lanes xor 4 .. 32 share the head lane % 4
-#pragma unroll
-    for (int dd = 4; dd <= 32; dd <<= 1) mx = fmaxf(mx, __shfl_xor(mx, dd, 64));
+    // lanes that share the head lane % 4: rotations by 4 and 8 inside each
+    // 16-lane row (DPP), then across rows
+    float mx = fmaxf(mt, row_ror<4>(mt));
+    mx = fmaxf(mx, row_ror<8>(mx));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     if (lane < kG) sx[wave * kG + lane] = mx;
   }
   __syncthreads();
@@ -491,8 +502,10 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     const float wt = (mt == -INFINITY || M == -INFINITY) ? 0.f : exp2f(mt - M);
     sw[tid] = wt;
     float lw = lt * wt;
-#pragma unroll
-    for (int dd = 4; dd <= 32; dd <<= 1) lw += __shfl_xor(lw, dd, 64);
+    lw += row_ror<4>(lw);
+    lw += row_ror<8>(lw);
+    lw += __shfl_xor(lw, 16, 64);
+    lw += __shfl_xor(lw, 32, 64);
     if (lane < kG) slw[wave * kG + lane] = lw;
   }
   __syncthreads();
