@@ -680,20 +680,20 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       const bool all_ties = take > 0;
 #pragma unroll
       for (int j = 0; j < TOK; ++j)
-        sel[j] = kv[j] != kNoKey && (kv[j] > tau || (all_ties && kv[j] == tau));
+        sel[j] = (kv[j] != kNoKey) & ((kv[j] > tau) | (all_ties & (kv[j] == tau)));
     } else {
 #pragma unroll
       for (int j = 0; j < TOK; ++j) {
-        const uint64_t mt = __ballot(kv[j] != kNoKey && kv[j] == tau);
+        const uint64_t mt = __ballot((kv[j] != kNoKey) & (kv[j] == tau));
         if (lane == 0) s_wcnt[j * kWaves + wave] = (uint32_t)__popcll(mt);
       }
       scan_wave_counts<TOK>(s_wcnt, s_ltot);
       uint32_t tie_base = 0;
 #pragma unroll
       for (int j = 0; j < TOK; ++j) {
-        const uint64_t mt = __ballot(kv[j] != kNoKey && kv[j] == tau);
+        const uint64_t mt = __ballot((kv[j] != kNoKey) & (kv[j] == tau));
         const uint32_t rank = tie_base + s_wcnt[j * kWaves + wave] + lanes_below(mt);
-        sel[j] = kv[j] != kNoKey && (kv[j] > tau || (kv[j] == tau && rank < take));
+        sel[j] = (kv[j] != kNoKey) & ((kv[j] > tau) | ((kv[j] == tau) & (rank < take)));
         tie_base += s_ltot[j];
       }
       __syncthreads();  // the tie prefixes are read
@@ -991,7 +991,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
         if (!(take[g] > 0 && take[g] < ties[g])) continue;
 #pragma unroll
         for (int j = 0; j < TOK; ++j) {
-          const uint64_t mt = __ballot(((inw >> j) & 1) && key(j, g) == tau[g]);
+          const uint64_t mt = __ballot(((inw >> j) & 1u) & (key(j, g) == tau[g]));
           if (lane == 0) s_wcnt[(g * TOK + j) * kWaves + wave] = (uint32_t)__popcll(mt);
         }
       }
@@ -1008,12 +1008,12 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
         const uint32_t kj = key(j, g);
         bool sj;
         if (part) {
-          const uint64_t mt = __ballot(in && kj == tau[g]);
+          const uint64_t mt = __ballot(in & (kj == tau[g]));
           const uint32_t rank = tie_base + s_wcnt[(g * TOK + j) * kWaves + wave] + lanes_below(mt);
-          sj = in && (kj > tau[g] || (kj == tau[g] && rank < take[g]));
+          sj = in & ((kj > tau[g]) | ((kj == tau[g]) & (rank < take[g])));
           tie_base += s_ltot[g * TOK + j];
         } else {
-          sj = in && (kj > tau[g] || (take[g] > 0 && kj == tau[g]));
+          sj = in & ((kj > tau[g]) | ((take[g] > 0) & (kj == tau[g])));
         }
         selb |= (sj ? 1u : 0u) << (4 * j + g);
       }
