@@ -56,8 +56,41 @@ struct KvStep {
   int mk[4];  // heads that keep keys 4r + e (bit c: head c), read by masked steps
 };
 
+// The K quarter rows of key lane % 16 (lane row r = lane / 16 reads quarter r).
+template <int D>
+__device__ __forceinline__ void k_issue(KvStep<D>& st, const uint16_t* __restrict__ kb,
+                                        int64_t k_st, int tok, int r) {
+  const uint4* kp = reinterpret_cast<const uint4*>(kb + (int64_t)(tok < 0 ? 0 : tok) * k_st +
+                                                   r * (D / 4));
+#pragma unroll
+  for (int i = 0; i < KvStep<D>::NK; ++i) st.k[i] = kp[i];
+}
+
+// The D/16 values (from c * D/16) of key 4r + e's V row tv.
+template <int D>
+__device__ __forceinline__ void v_issue(KvStep<D>& st, const uint16_t* __restrict__ vb,
+                                        int64_t v_st, int e, int tv, int c) {
+  st.tv[e] = tv;
+  const uint16_t* vp = vb + (int64_t)(tv < 0 ? 0 : tv) * v_st + c * (D / 16);
+  if (KvStep<D>::NV == 2) {
+    const uint2 w = *reinterpret_cast<const uint2*>(vp);
+    st.v[e][0] = w.x;
+    st.v[e][1] = w.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < KvStep<D>::NV; i += 4) {
+      const uint4 w = reinterpret_cast<const uint4*>(vp)[i / 4];
+      st.v[e][i] = w.x;
+      st.v[e][i + 1] = w.y;
+      st.v[e][i + 2] = w.z;
+      st.v[e][i + 3] = w.w;
+    }
+  }
+}
+
 // tok: lane j < 16 holds key j's cache row (-1: none); mask: its head bits
-// (masked steps only).
+// (masked steps only).  Lanes of row r take keys 4r + e's rows and bits
+// from lanes 4r + e.
 template <int D>
 __device__ __forceinline__ void kv_issue(KvStep<D>& st, const uint16_t* __restrict__ kb,
                                          const uint16_t* __restrict__ vb, int64_t k_st,
@@ -65,30 +98,25 @@ __device__ __forceinline__ void kv_issue(KvStep<D>& st, const uint16_t* __restri
   const int r = lane >> 4, c = lane & 15;
 #pragma unroll
   for (int e = 0; e < 4; ++e) st.mk[e] = __shfl(mask, 4 * r + e, 64);
-  const uint4* kp = reinterpret_cast<const uint4*>(kb + (int64_t)(tok < 0 ? 0 : tok) * k_st +
-                                                   r * (D / 4));
+  k_issue<D>(st, kb, k_st, tok, r);
 #pragma unroll
-  for (int i = 0; i < KvStep<D>::NK; ++i) st.k[i] = kp[i];
+  for (int e = 0; e < 4; ++e) v_issue<D>(st, vb, v_st, e, __shfl(tok, 4 * r + e, 64), c);
+}
+
+// The same with keys 4r + e's cache rows tv[e] and head bits mk[e] given by
+// the caller (read where the lane's own key is read, instead of broadcast
+// from lanes < 16 after that read returns).
+template <int D>
+__device__ __forceinline__ void kv_issue_rows(KvStep<D>& st, const uint16_t* __restrict__ kb,
+                                              const uint16_t* __restrict__ vb, int64_t k_st,
+                                              int64_t v_st, int tok, const int (&tv)[4],
+                                              const int (&mk)[4], int lane) {
+  const int r = lane >> 4, c = lane & 15;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int tv = __shfl(tok, 4 * r + e, 64);  // lane j < 16 holds key j's row
-    st.tv[e] = tv;
-    const uint16_t* vp = vb + (int64_t)(tv < 0 ? 0 : tv) * v_st + c * (D / 16);
-    if (KvStep<D>::NV == 2) {
-      const uint2 w = *reinterpret_cast<const uint2*>(vp);
-      st.v[e][0] = w.x;
-      st.v[e][1] = w.y;
-    } else {
+  for (int e = 0; e < 4; ++e) st.mk[e] = mk[e];
+  k_issue<D>(st, kb, k_st, tok, r);
 #pragma unroll
-      for (int i = 0; i < KvStep<D>::NV; i += 4) {
-        const uint4 w = reinterpret_cast<const uint4*>(vp)[i / 4];
-        st.v[e][i] = w.x;
-        st.v[e][i + 1] = w.y;
-        st.v[e][i + 2] = w.z;
-        st.v[e][i + 3] = w.w;
-      }
-    }
-  }
+  for (int e = 0; e < 4; ++e) v_issue<D>(st, vb, v_st, e, tv[e], c);
 }
 
 template <int DT, int HPR, int D>

@@ -756,9 +756,11 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
   const int n_st = n_fix > c ? (n_fix - c + a.WR - 1) / a.WR : 0;
   const int n_loc = (int)n_sel + n_st;
   // local keep position p -> cache row (-1 past the row's rows)
-  auto keep_tok = [&](int p) -> int {
+  // (kept: keep-list entry p when p < n_sel)
+  auto keep_tok = [&](int p, int kept) -> int {
+    if (p >= n_loc) return -1;
     int64_t t;
-    if (p < (int)n_sel) t = lds.keep[p];
+    if (p < (int)n_sel) t = kept;
     else {
       const int jt = c + (p - (int)n_sel) * a.WR;
       t = jt < pr.sink ? jt : (int64_t)pr.tail_start + (jt - pr.sink);
@@ -766,11 +768,19 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
     return (t < 0 || t >= pr.t_total) ? -1 : (int)t;
   };
   const int nsteps = (n_loc + kKeys - 1) / kKeys;
+  const int p4r = 4 * (lane >> 4);
   for (int i = wave; i < nsteps; i += kWaves) {
     const int p = i * kKeys + (lane & 15);
-    const int tok = p < n_loc ? keep_tok(p) : -1;
+    const int tok = keep_tok(p, lds.keep[min(p, kKeepMax - 1)]);
+    // keys 4r .. 4r + 3 of this lane's row r: one 16-byte read (a start past
+    // the keep list means every entry is past n_sel, so the clamp is unused)
+    const int p4 = i * kKeys + p4r;
+    const int4 kq = *reinterpret_cast<const int4*>(lds.keep + min(p4, kKeepMax - 4));
+    const int tv[4] = {keep_tok(p4, kq.x), keep_tok(p4 + 1, kq.y), keep_tok(p4 + 2, kq.z),
+                       keep_tok(p4 + 3, kq.w)};
+    const int mk[4] = {0, 0, 0, 0};
     KvStep<kDh> st;
-    kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane);
+    kv_issue_rows<kDh>(st, kb, vb, a.k_st, a.v_st, tok, tv, mk, lane);
     attn_step<DT, kG, kDh>(ws, st, a.scale_log2, lane);
   }
   finish_row<DT, true>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
@@ -817,7 +827,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   static_assert(kMaxTokPH * kTH <= kKeepMax, "a chunk's union fits the keep list");
   __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
   __shared__ uint32_t s_hist[kG * kH1Pitch];
-  __shared__ uint8_t s_kmask[kKeepMax];
+  __shared__ __attribute__((aligned(16))) uint8_t s_kmask[kKeepMax];
   __shared__ uint32_t s_h2[kG][kL2], s_wsum[kG][kWaves], s_res[kG][4], s_sel[kG][4];
   constexpr int kLists = (kG + 1) * TOK;
   static_assert(kWaves == 16, "one 16-lane row per list");
@@ -1126,20 +1136,35 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   const int n_st = n_fix > c ? (n_fix - c + a.WR - 1) / a.WR : 0;
   const int n_loc = (int)n_sel + n_st;
   const int nsteps = (n_loc + kKeys - 1) / kKeys;
-  for (int i = wave; i < nsteps; i += kWaves) {
-    const int p = i * kKeys + (lane & 15);
-    int tok = -1, msk = 0;
-    if (p < (int)n_sel) {
-      tok = lds.keep[p];
-      msk = s_kmask[p];
-    } else if (p < n_loc) {
+  // key p's cache row (kept: keep-list entry p when p < n_sel)
+  auto keep_tok = [&](int p, int kept) -> int {
+    int tok = -1;
+    if (p < (int)n_sel) tok = kept;
+    else if (p < n_loc) {
       const int jt = c + (p - (int)n_sel) * a.WR;
       tok = jt < pr.sink ? jt : pr.tail_start + (jt - pr.sink);
-      msk = 0xf;
     }
-    if (tok < 0 || tok >= pr.t_total) tok = -1;
+    return (tok < 0 || tok >= pr.t_total) ? -1 : tok;
+  };
+  // key p's head bits (bits: its keep-mask byte when p < n_sel)
+  auto keep_bits = [&](int p, uint32_t bits) -> int {
+    return p < (int)n_sel ? (int)(bits & 0xfu) : (p < n_loc ? 0xf : 0);
+  };
+  const int p4r = 4 * (lane >> 4);
+  for (int i = wave; i < nsteps; i += kWaves) {
+    const int p = i * kKeys + (lane & 15);
+    const int tok = keep_tok(p, lds.keep[min(p, kKeepMax - 1)]);
+    // keys 4r .. 4r + 3 of this lane's row r: one 16-byte read of the keep
+    // list and one word of the masks (clamped as in step_fused_kernel)
+    const int p4 = i * kKeys + p4r, q4 = min(p4, kKeepMax - 4);
+    const int4 kq = *reinterpret_cast<const int4*>(lds.keep + q4);
+    const uint32_t mq = *reinterpret_cast<const uint32_t*>(s_kmask + q4);
+    const int tv[4] = {keep_tok(p4, kq.x), keep_tok(p4 + 1, kq.y), keep_tok(p4 + 2, kq.z),
+                       keep_tok(p4 + 3, kq.w)};
+    const int mk[4] = {keep_bits(p4, mq), keep_bits(p4 + 1, mq >> 8), keep_bits(p4 + 2, mq >> 16),
+                       keep_bits(p4 + 3, mq >> 24)};
     KvStep<kDh> st;
-    kv_issue<kDh>(st, kb, vb, a.k_st, a.v_st, tok, lane, msk);
+    kv_issue_rows<kDh>(st, kb, vb, a.k_st, a.v_st, tok, tv, mk, lane);
     attn_step<DT, kG, kDh, true>(ws, st, a.scale_log2, lane);
   }
   finish_row<DT, false>(a, ws, lds, s_m, s_l, s_flag, r, c, b, h0, select, min(nsteps, kWaves),
