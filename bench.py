@@ -18,9 +18,11 @@ once per layer per token (aq_evaluation.py:146-253).  Twelve code/query sets
 and four K/V sets (~2.5 GB) rotate so that the 256 MB Infinity Cache cannot
 serve the step from cache.
 
-``value``        code bytes / average duration of the fused scorer kernel,
-                 timed with HIP events around graph replays on the launch
-                 stream, before the step and comparator legs run.
+``value``        code bytes / duration of the fused scorer kernel, timed
+                 with HIP events around graph replays on the launch stream,
+                 before the step and comparator legs run: the median of
+                 nine trials of 108 launches (``score_kernel_spread`` has
+                 p10 / p90).
 ``ms_per_step``  wall time of one full sparse decode step, K steps issued
                  back to back eagerly and timed between two synchronisations
                  (``host_issue_us``: the host's time to issue one step, which
@@ -51,6 +53,11 @@ serve the step from cache.
                  per query head on bf16-cast scores, budget 131004 -
                  int(0.98 * 131004) = 2621, each head attending over its own
                  keep set.
+``step_health``  the one-launch step's health counters (KV rows whose
+                 workgroups ran on more than one XCD, row barriers that gave
+                 up) of each leg's decoder after its timed steps; any
+                 non-zero count makes the run exit with status 3 after the
+                 JSON line.
 ``ragged``       one attention layer of configs[4] (C5): batch 16, per-sequence
                  lengths uniform in [16384, 32768] (seeded), top-1024 per KV
                  group + 4 sink + 64 local, the newest < 64 keys of each
@@ -77,6 +84,8 @@ CAP = 128            # extra capacity rows, as the reference's decode cache
 TOPK, SINK, LOCAL = 2048, 4, 64
 N_CODE_SETS, N_KV_SETS = 12, 4
 CODE_BYTES = HKV * T * M  # 33,554,432 algorithmic bytes per scorer launch
+SCORE_TRIALS = 9           # timed trials of the scorer (median reported)
+SCORE_TRIAL_LAUNCHES = 108  # scorer launches per trial (nine replays of 12)
 CALIB_BYTES = 256 << 20   # copy-like calibration kernel: bytes read (= bytes written)
 ENC_TOKENS, ENC_POS0, ROPE_THETA = 64, 131008, 500000.0
 ENC_FLOP = 2 * HKV * ENC_TOKENS * M * K * D  # 1,073,741,824 dot-product flops per flush
@@ -309,6 +318,7 @@ def reference_mode_leg(args, cb, codes_sets, q_sets, kv_sets, dense_s, dense_gra
     return {
         "selection": (f"top-{k} per query head on bf16-cast scores (reference budget rule, "
                       f"mask_out 0.98) + {SINK} sink + {LOCAL} local"),
+        "step_health": list(dec.fused_status()),
         "k": k,
         "sparse_step_us": round(step_s * 1e6, 2),
         "host_issue_us": round(host_s * 1e6, 2),
@@ -386,6 +396,7 @@ def ragged_leg(args, dev, cb) -> dict:
         "dense_hbm_gbs": round(kv_bytes / out["dense"] / 1e9, 1),
         "score_code_bytes": sum(t_codes) * HKV * M,
         "selection_check": ok,
+        "step_health": list(dec.fused_status()),
     }
 
 
@@ -608,19 +619,26 @@ def main():
 
     # ---- scorer kernel duration: HIP events on the launch stream around a
     # graph of back-to-back scorer launches over the rotating code sets,
-    # after at least 2048 untimed launches (about 27 ms): after other work
+    # after at least 2048 untimed launches (about 25 ms): after other work
     # the first few hundred launches run up to ~1.4 us slower than the
-    # steady state they then settle to.
+    # steady state they then settle to.  SCORE_TRIALS trials of at least 108
+    # launches each (independent of --steps, outside the timed step region);
+    # the figure is the median trial, with p10 / p90 beside it.
     log("timing the scorer kernel")
     reps = max(1, args.steps // n_sets)
     stream = torch.cuda.current_stream()
+    trial_reps = max(reps, -(-SCORE_TRIAL_LAUNCHES // n_sets))
+    trials = []
     if args.eager:
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        ev0.record(stream)
-        for i in range(reps * n_sets):
-            score_only(i)
-        ev1.record(stream)
+        for _ in range(SCORE_TRIALS):
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for i in range(trial_reps * n_sets):
+                score_only(i)
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            trials.append(ev0.elapsed_time(ev1) * 1e3 / (trial_reps * n_sets))
     else:
         gsc = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gsc):
@@ -629,17 +647,23 @@ def main():
         for _ in range(max(reps, -(-2048 // n_sets))):
             gsc.replay()
         torch.cuda.synchronize()
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        ev0.record(stream)
-        for _ in range(reps):
-            gsc.replay()
-        ev1.record(stream)
-    torch.cuda.synchronize()
-    score_us = ev0.elapsed_time(ev1) * 1e3 / (reps * n_sets)
+        for _ in range(SCORE_TRIALS):
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for _ in range(trial_reps):
+                gsc.replay()
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            trials.append(ev0.elapsed_time(ev1) * 1e3 / (trial_reps * n_sets))
+    trials.sort()
+    score_us = trials[len(trials) // 2]
+    score_spread = {"trials": len(trials), "launches_per_trial": trial_reps * n_sets,
+                    "p10_us": round(trials[len(trials) // 10], 3),
+                    "p90_us": round(trials[(len(trials) * 9) // 10], 3)}
     score_gbs = CODE_BYTES / (score_us * 1e-6) / 1e9
     floors = (None if args.eager else
-              score_floors(score_only, floor_empty, floor_stream, stream, reps))
+              score_floors(score_only, floor_empty, floor_stream, stream, trial_reps))
 
     # ---- timed region 1: K full sparse decode steps, issued eagerly
     for i in range(args.warmup):
@@ -745,8 +769,10 @@ def main():
         "sdpa_step_us": None if sdpa_s is None else round(sdpa_s * 1e6, 2),
         "speedup_vs_sdpa": None if sdpa_s is None else round(sdpa_s / sparse_s, 3),
         "score_kernel_us": round(score_us, 3),
+        "score_kernel_spread": score_spread,
         "score_floors": floors,
         "selection_check": ok,
+        "step_health": list(dec.fused_status()),
         "encode": {
             "workload": "C3: 8 KV heads x 64-token flush = 512 post-RoPE key rows, D=128, "
                         "32x256 fp32 codebooks N(0,0.02); greedy codes + residual norm",
@@ -775,6 +801,17 @@ def main():
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         result["encode"]["cpu_baseline"] = encode_cpu_baseline(enc_x, cb, 4.0)
     print(json.dumps(result), flush=True)
+    # The one-launch steps' health counters (rows split over XCDs, barrier
+    # time-outs) of every leg: a non-zero count means the timed steps ran
+    # outside the kernel's guarantees, and the run fails.
+    unhealthy = {leg: h for leg, h in [
+        ("c2", result["step_health"]),
+        ("reference_mode", (result.get("reference_mode") or {}).get("step_health", [0, 0])),
+        ("ragged", (result.get("ragged") or {}).get("step_health", [0, 0]))] if any(h)}
+    if unhealthy:
+        print(f"bench.py: one-launch step health counters non-zero (split rows, time-outs): "
+              f"{unhealthy}", file=sys.stderr)
+        sys.exit(3)
 
 
 if __name__ == "__main__":

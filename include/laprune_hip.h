@@ -346,8 +346,10 @@ int lap_sparse_attn_decode_ragged(const void* q, int64_t q_sb, int64_t q_sh,
  * merges); other shapes run the kernel chain.  Workspace: lap_decode_step_workspace_size
  * with keep_max = k + sink + tail (ragged: k_cols + max_sink + max_tail).  It
  * must be zero-filled once before its first use; every call leaves its
- * barrier words at zero again.  Calls that share a workspace must be ordered
- * (same stream). */
+ * barrier words and histograms at zero again.  Their layout does not depend
+ * on the call (it is laid out for 256 KV rows), so a workspace sized for
+ * the largest batch serves every smaller one.  Calls that share a workspace
+ * must be ordered (same stream). */
 int lap_decode_step_workspace_size(int B, int Hq, int Hkv, int T, int D, int keep_max,
                                    int key_mode, size_t* bytes);
 int lap_decode_step(const void* lut_gmkg, const uint8_t* codes,
@@ -394,6 +396,16 @@ int lap_decode_step_noalloc(const void* lut_gmkg, const uint8_t* codes,
                             int64_t k_sb, int64_t k_sh, int64_t k_st,
                             int64_t v_sb, int64_t v_sh, int64_t v_st, float scale,
                             void* out_idx, int idx_dtype, void* out, lap_stream_t stream);
+/* Health counters of lap_decode_step_noalloc's static scratch on the current
+ * device (the two words lap_decode_step_status reads from a workspace), read
+ * after a device synchronisation; zeros before the first call on the
+ * device.  No counterpart in the reference. */
+int lap_decode_step_noalloc_status(uint32_t* split_rows, uint32_t* timeouts);
+/* Zero the static scratch's counters, row barriers and row histograms on
+ * the current device (a fill kernel on `stream`, nothing allocated): the
+ * reset after a call whose counters came back non-zero.  No counterpart in
+ * the reference. */
+int lap_decode_step_noalloc_reset(lap_stream_t stream);
 
 /* ======================================================================= *
  * A6  Greedy AQ encode                                                     *

@@ -83,6 +83,8 @@ SIGNATURES = {
                         i32, i32, vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32, i64, i64,
                         i64, i64, i64, i64, f32, vp, i32, vp, vp, sz, vp],
     "lap_decode_step_status": [vp, sz, pu32, pu32],
+    "lap_decode_step_noalloc_status": [pu32, pu32],
+    "lap_decode_step_noalloc_reset": [vp],
     "lap_decode_step_noalloc": [vp, vp, i64, i64, i64, i32, i32, i32, i32, i32, i32, i32, vp, i32,
                                 i32, i32, i32, vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32,
                                 i64, i64, i64, i64, i64, i64, f32, vp, i32, vp, vp],

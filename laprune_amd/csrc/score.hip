@@ -130,10 +130,12 @@ __device__ __forceinline__ void store_token(const ScoreOut& so, int r, int T, in
 // thread keeps PREF stages in flight: it requests stage j + PREF only when
 // stage j has arrived, so early stages complete early and the lookups of
 // stage j overlap the stream of the later ones.  The table slice is
-// requested first; vector-memory loads return in issue order (vmcnt), so the
-// table is written to LDS while code rows are still in flight, and the
-// barrier after the fill orders LDS only.  The ordered loads and their
-// waits are in score_core.h.
+// requested first and the first stages only once it is in LDS: the lookups
+// are the kernel's bound (random 8-byte LDS reads, about six cycles per wave
+// instruction with bank conflicts), so the table, which every lookup needs,
+// goes first.  The barrier after the fill orders LDS only, and the waves
+// lower their priority stage by stage (stage_prio) so that they finish
+// together.  The ordered loads and their waits are in score_core.h.
 //
 // PH: per-head selection keys (a template parameter, so the two key modes
 // are separate kernels in traces and the key code folds).
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
   constexpr int kAhead = PREF < TOK ? PREF : TOK;  // stages requested up front
   static_assert(kFill * THREADS * 16 == kLutBytes && THREADS >= 256 && kFill % 4 == 0,
                 "bad THREADS");
-  static_assert(kFill + 2 * kAhead <= 23 && 2 * kAhead <= 16, "vmcnt range");
+  static_assert(kFill <= 23 && 2 * kAhead <= 16, "vmcnt range");
   __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
   __shared__ uint32_t s_hist[PH ? kG : 1][HC * kHPitch];
 
@@ -189,26 +191,29 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
   auto request = [&](int j) {
     const int t = min(t0 + j * THREADS + tid, t1 - 1);
     const uint8_t* p = crow + (int64_t)t * cs_t;
-    c[j][0] = gload16_ordered(p);
-    c[j][1] = gload16_ordered(p + 16);
+    c[j][0] = gload16_stream(p);
+    c[j][1] = gload16_stream(p + 16);
   };
-#pragma unroll
-  for (int j = 0; j < kAhead; ++j) request(j);
 
   if constexpr (IL) {
 #pragma unroll
     for (int i = 0; i < kFill; ++i) {
-      vm_wait(kFill - 1 - i + 2 * kAhead, f[i]);
+      vm_wait(kFill - 1 - i, f[i]);
       s_lut[i * THREADS + tid] = as_uint4(f[i]);
     }
   } else {
 #pragma unroll
     for (int j = 0; j < kFill / 4; ++j) {
-      vm_wait(kFill - 4 - 4 * j + 2 * kAhead, f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
+      vm_wait(kFill - 4 - 4 * j, f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
       interleave_heads(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3],
                        &s_lut[(j * THREADS + tid) * 4]);
     }
   }
+  // The first code rows are requested once the table is in: issued together
+  // with the table they compete with it for the memory system, and the table
+  // (which every lookup needs) then arrives later than the rows do.
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j) request(j);
   for (int i = tid; i < key_rows(so) * HC * kHPitch; i += THREADS)
     s_hist[i / (HC * kHPitch)][i % (HC * kHPitch)] = 0;
   lds_barrier();
@@ -225,6 +230,7 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
     const int later = (j + kAhead - 1 < TOK - 1 ? j + kAhead - 1 : TOK - 1) - j;
     vm_wait(2 * later, c[j][0], c[j][1]);
     if (j + kAhead < TOK) request(j + kAhead);
+    stage_prio(j, TOK);
     float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
     score_token(lds, as_uint4(c[j][0]), as_uint4(c[j][1]), one, e0, e1, e2, e3);
     h01[j] = (uint32_t)f2h(e0) | ((uint32_t)f2h(e1) << 16);
@@ -437,9 +443,12 @@ static int g4_plan(int R, int T, G4Plan* p) {
   return LAP_OK;
 }
 
-// Histogram copies: 4 per group row; per-head rows take 4 (82 KiB of LDS)
-// when the launch has at most one workgroup per CU, else 2 (72 KiB, two
-// workgroups per CU).
+// Histogram copies: with at most one workgroup per CU, 16 per group row (80
+// KiB of LDS) and 8 per per-head row (97 KiB); with two workgroups per CU,
+// 4 per group row (68 KiB each) and 2 per per-head row (72 KiB).  The keys
+// of one launch fall in a few high-byte bins, so a wave's 64 atomics land on
+// a few addresses, and the copies spread them (16 copies measured 0.2 us
+// faster than 4 at C2).
 template <int TH, int TK, int PF>
 static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, bool lut_il,
                        const uint8_t* codes, int64_t cs_b, int64_t cs_h, int64_t cs_t, int Hkv,
@@ -448,11 +457,13 @@ static void launch_g4p(dim3 grid, hipStream_t st, const uint16_t* lut, bool lut_
   hipLaunchKernelGGL((score_g4p_kernel<TH, TK, PF, IL, PH, HC>), grid, dim3(TH), 0, st, lut,  \
                      codes, cs_b, cs_h, cs_t, Hkv, R, T, so, f16_one())
   if (lut_il) {
-    if (!so.per_head) LAP_G4P_LAUNCH(true, false, 4);
-    else if (one_per_cu) LAP_G4P_LAUNCH(true, true, 4);
+    if (!so.per_head && one_per_cu) LAP_G4P_LAUNCH(true, false, 16);
+    else if (!so.per_head) LAP_G4P_LAUNCH(true, false, 4);
+    else if (one_per_cu) LAP_G4P_LAUNCH(true, true, 8);
     else LAP_G4P_LAUNCH(true, true, 2);
   } else {
     if (so.per_head) LAP_G4P_LAUNCH(false, true, 2);
+    else if (one_per_cu) LAP_G4P_LAUNCH(false, false, 16);
     else LAP_G4P_LAUNCH(false, false, 4);
   }
 #undef LAP_G4P_LAUNCH

@@ -48,6 +48,27 @@ __device__ __forceinline__ u32x4 gload16_ordered(const void* p) {
   asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
   return v;
 }
+// The same load marked non-temporal: code rows are read once per launch, and
+// the hint keeps the stream from displacing what the caches hold for longer
+// (measured on MI355X: the C2 scorer 0.3 us faster per launch).
+__device__ __forceinline__ u32x4 gload16_stream(const void* p) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(v) : "v"(p));
+  return v;
+}
+
+// Wave priority for stage j of TOK: the stages still ahead, at most 3.  A
+// SIMD serves its waves oldest first, so without it some waves finish their
+// last stage well before others and the table lookups of the last stage
+// run on a few waves with the LDS half idle; lowering a wave's priority as
+// it advances keeps the waves of a workgroup within about one stage.
+__device__ __forceinline__ void stage_prio(int j, int TOK) {
+  const int p = TOK - 1 - j;
+  if (p >= 3) __builtin_amdgcn_s_setprio(3);
+  else if (p == 2) __builtin_amdgcn_s_setprio(2);
+  else if (p == 1) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
 
 template <int N>
 __device__ __forceinline__ void vmw1(u32x4& a) {

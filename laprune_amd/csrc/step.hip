@@ -69,13 +69,20 @@ constexpr int kTH = 1024;
 constexpr int kWaves = kTH / 64;
 constexpr int kMaxTok = 16;         // tokens per thread (chunk = TOK * 1024)
 constexpr int kMaxTokPH = 8;        // the same with per-head selection
-constexpr int kHC = 4;              // level-1 histogram copies
+constexpr int kHC = 16;             // level-1 histogram copies (group selection)
+constexpr int kHCph = 4;            // the same per query head (per-head selection)
 constexpr int kDh = 128;            // head dim of the fused path
 constexpr int kKeepMax = 8192;      // a workgroup's own selection (32 KiB of LDS)
 constexpr int kSpin = 1 << 21;      // polls before a barrier gives up
 constexpr int kBarWords = 16;       // one 64-byte line per barrier
 constexpr int kStatusBytes = 256;
 constexpr int kMaxWR = 32;          // workgroups per row (one per CU of an XCD)
+// Rows the persistent head of a workspace (status words, row barriers, row
+// histograms) is laid out for, whatever the call's B * Hkv: a caller may size
+// one workspace for its largest batch and call with any smaller one, and
+// every call finds row r's persistent words at the same address.  The fused
+// kernel serves at most one row per CU (R <= 256 on MI355X).
+constexpr int kHeadRows = 256;
 
 struct StepArgs {
   const uint16_t* lut;   // [R][M][K][4] fp16 (GMKG)
@@ -340,34 +347,40 @@ __device__ __forceinline__ void score_chunk(const StepArgs& a, const StepPos& p,
   auto request = [&](int j) {
     const int t = min(p.t0 + j * kTH + tid, p.t1 - 1);
     const uint8_t* q = crow + (int64_t)t * a.cs_t;
-    cc[j][0] = gload16_ordered(q);
-    cc[j][1] = gload16_ordered(q + 16);
+    cc[j][0] = gload16_stream(q);
+    cc[j][1] = gload16_stream(q + 16);
   };
-  request(0);
 #pragma unroll
   for (int i = 0; i < kFill; ++i) {
-    vm_wait(kFill - 1 - i + 2, f[i]);
+    vm_wait(kFill - 1 - i, f[i]);
     lut_lds[i * kTH + tid] = as_uint4(f[i]);
   }
+  request(0);  // after the table, as in the scorer (score.hip)
   lds_barrier();
   const char* tab = reinterpret_cast<const char*>(lut_lds);
 #pragma unroll
   for (int j = 0; j < TOK; ++j) {
     vm_wait(0, cc[j][0], cc[j][1]);
     if (j + 1 < TOK) request(j + 1);
+    stage_prio(j, TOK);
     float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
     score_token(tab, as_uint4(cc[j][0]), as_uint4(cc[j][1]), a.one, e0, e1, e2, e3);
     body(j, p.t0 + j * kTH + tid, e0, e1, e2, e3);
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // The end of a row's step, shared by both fused kernels: the waves' (m, l,
 // o) combined in LDS into the workgroup's partial, then the row's last
 // workgroup to arrive merges the partials (E) and writes the output.  Waves
 // nw.. ran no attention step (their state is empty) and are left out.
-// out_stores issues the stores nothing in the launch reads (index rows and
-// the like); every workgroup calls it once, after its merge arrival (the
-// merging workgroup: with EARLY, as soon as its partial loads are out).
+// out_stores(last) issues the stores nothing in the launch reads (index rows
+// and the like); every workgroup calls it once, after its merge arrival (the
+// merging workgroup: with EARLY, as soon as its partial loads are out), and
+// `last` is true for the row's last arrival (or its only workgroup), which
+// clears the row histogram: every workgroup of the row has added to it and
+// read it before arriving, so the clear follows them all even when a barrier
+// of the call timed out.
 template <int DT, bool EARLY, typename Stores>
 __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, kDh>& ws,
                                            const Lds& lds, float (&s_m)[kWaves][4],
@@ -422,7 +435,7 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     }
   }
   if (a.WR == 1) {
-    out_stores();
+    out_stores(true);
     return;
   }
 
@@ -449,7 +462,7 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
   }
   __syncthreads();
   if (!s_flag) {
-    out_stores();
+    out_stores(false);
     return;
   }
   // The row's partials: thread t < 128 holds (m, l) of split t / 4, head
@@ -477,7 +490,7 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
   // that their acknowledgements overlap the merge instead of following it
   // (a kernel that stores little here; per-head selection clears four
   // histograms, whose stores would hold up the merge's waits instead)
-  if (EARLY) out_stores();
+  if (EARLY) out_stores(true);
   float mt = -INFINITY, lt = 0.f;
   if (tid < kMaxWR * kG) {
     // (m, l) as one 8-byte load (a partial's head record starts 8-byte
@@ -523,7 +536,7 @@ __device__ __forceinline__ void finish_row(const StepArgs& a, WaveState<DT, kG, 
     const float l = slw[g] + slw[kG + g];
     a.out[((int64_t)b * a.Hkv * kG + h0 + g) * kDh + d] = st16<DT>(l > 0.f ? o / l : 0.f);
   }
-  if (!EARLY) out_stores();
+  if (!EARLY) out_stores(true);
 }
 
 template <int DT, int TOK>
@@ -611,8 +624,8 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
       t2[kL2] = my_gt1;
     }
     wg_row_barrier(a, r, 1);
-    // Every chunk has read the row histogram; chunk 0 clears it for the next
-    // call once its merge arrival is out (out_stores).
+    // Every chunk has read the row histogram; the row's last merge arrival
+    // clears it for the next call (out_stores).
 
     // ------------------------------------------------------------ H2
     // The row's level-2 tables: the threshold tau = (b1, b2), the ties at
@@ -719,10 +732,11 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
 
   // The stores nothing in this launch reads: this chunk's part of the index
   // row (from the keep list, which stays in LDS to the end), its share of a
-  // ragged row's -1 padding, and chunk 0's clearing of the row histogram.
-  // They are issued after the merge arrival, so that no wait on the way
-  // there (every wait drains all earlier memory operations) includes them.
-  auto out_stores = [&]() {
+  // ragged row's -1 padding, and (last arrival) the clearing of the row
+  // histogram.  They are issued after the merge arrival, so that no wait on
+  // the way there (every wait drains all earlier memory operations) includes
+  // them.
+  auto out_stores = [&](bool last) {
     const int64_t irow = ((int64_t)b * a.Hkv + hkv) * a.k_cols;
     for (int p = tid; p < (int)n_sel && base + (uint32_t)p < (uint32_t)pr.k; p += kTH) {
       if (a.idx_i64) put_idx<int64_t>(a.idx, irow + base + p, lds.keep[p]);
@@ -736,7 +750,7 @@ __global__ __launch_bounds__(kTH) void step_fused_kernel(StepArgs a) {
         else put_idx<int32_t>(a.idx, irow + pr.k + i, -1);
       }
     }
-    if (select && c == 0) a.hist[(int64_t)r * kL1 + tid] = 0u;
+    if (select && last) a.hist[(int64_t)r * kL1 + tid] = 0u;
   };
 
   // ---------------------------------------------------------------- A
@@ -826,7 +840,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   static_assert(TOK >= 1 && TOK <= kMaxTokPH, "TOK");
   static_assert(kMaxTokPH * kTH <= kKeepMax, "a chunk's union fits the keep list");
   __shared__ __attribute__((aligned(16))) uint4 s_big[kLutBytes / 16];
-  __shared__ uint32_t s_hist[kG * kH1Pitch];
+  __shared__ uint32_t s_hist[kG * kHCph * kH1Pitch];
   __shared__ __attribute__((aligned(16))) uint8_t s_kmask[kKeepMax];
   __shared__ uint32_t s_h2[kG][kL2], s_wsum[kG][kWaves], s_res[kG][4], s_sel[kG][4];
   constexpr int kLists = (kG + 1) * TOK;
@@ -855,8 +869,9 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   // in .y); inw bit j: the token is a candidate.
   uint2 kp[TOK];
   uint32_t inw = 0;
-  for (int i = tid; i < kG * kH1Pitch; i += kTH) s_hist[i] = 0;
+  for (int i = tid; i < kG * kHCph * kH1Pitch; i += kTH) s_hist[i] = 0;
   if (select && t0 < t1) {
+    const int copy = (int)(__lane_id() % kHCph) * kH1Pitch;
     score_chunk<TOK>(a, ps, lds.lut, [&](int j, int t, float e0, float e1, float e2, float e3) {
       kp[j] = make_uint2(0u, 0u);
       if (t < t1 && t >= pr.cs && t < pr.ce) {
@@ -864,10 +879,10 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
         const uint32_t k2 = key_of_score(e2, a.key_bf16), k3 = key_of_score(e3, a.key_bf16);
         kp[j] = make_uint2(k0 | (k1 << 16), k2 | (k3 << 16));
         inw |= 1u << j;
-        atomicAdd(&s_hist[0 * kH1Pitch + (k0 >> kLoBits)], 1u);
-        atomicAdd(&s_hist[1 * kH1Pitch + (k1 >> kLoBits)], 1u);
-        atomicAdd(&s_hist[2 * kH1Pitch + (k2 >> kLoBits)], 1u);
-        atomicAdd(&s_hist[3 * kH1Pitch + (k3 >> kLoBits)], 1u);
+        atomicAdd(&s_hist[(0 * kHCph) * kH1Pitch + copy + (k0 >> kLoBits)], 1u);
+        atomicAdd(&s_hist[(1 * kHCph) * kH1Pitch + copy + (k1 >> kLoBits)], 1u);
+        atomicAdd(&s_hist[(2 * kHCph) * kH1Pitch + copy + (k2 >> kLoBits)], 1u);
+        atomicAdd(&s_hist[(3 * kHCph) * kH1Pitch + copy + (k3 >> kLoBits)], 1u);
       }
     });
   }
@@ -883,7 +898,8 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   if (select) {
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
-      h1[g] = s_hist[g * kH1Pitch + tid];
+#pragma unroll
+      for (int cp = 0; cp < kHCph; ++cp) h1[g] += s_hist[(g * kHCph + cp) * kH1Pitch + tid];
       if (h1[g])
         __hip_atomic_fetch_add(a.hist + ((int64_t)r * kG + g) * kL1 + tid, h1[g],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1056,11 +1072,12 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
   lds_barrier();  // the keep list
 
   // The stores nothing in this launch reads, after the merge arrival: the
-  // chunk's part of the four index rows, ragged rows' padding, and the
-  // histogram clear.  Thread t takes union entries [t E, t E + E); its rank
-  // among each head's keys comes from a block scan of per-thread counts
-  // (two heads per word, 16 bits each: a chunk keeps at most 8192 keys).
-  auto out_stores = [&]() {
+  // chunk's part of the four index rows, ragged rows' padding, and (last
+  // arrival) the histogram clear.  Thread t takes union entries [t E, t E +
+  // E); its rank among each head's keys comes from a block scan of
+  // per-thread counts (two heads per word, 16 bits each: a chunk keeps at
+  // most 8192 keys).
+  auto out_stores = [&](bool last) {
     if (n_sel > 0) {
       const int E = ((int)n_sel + kTH - 1) / kTH;
       const int p0 = min(tid * E, (int)n_sel), p1 = min(p0 + E, (int)n_sel);
@@ -1112,7 +1129,7 @@ __global__ __launch_bounds__(kTH) void step_fused_ph_kernel(StepArgs a) {
         }
       }
     }
-    if (select && c == 0) {
+    if (select && last) {
 #pragma unroll
       for (int g = 0; g < kG; ++g) a.hist[((int64_t)r * kG + g) * kL1 + tid] = 0u;
     }
@@ -1302,6 +1319,7 @@ int decode_step_fused(const void* lut_gmkg, const uint8_t* codes, int64_t cs_b, 
                       bool per_head, const char* who, hipStream_t st) {
   const int R = B * Hkv;
   FusedPlan fp;
+  if (R > head_rows) return LAP_ERR_UNSUPPORTED;  // more rows than the head holds: the chain
   if (!fused_plan(R, T, per_head, plans ? k_cols : k, &fp)) return LAP_ERR_UNSUPPORTED;
   if (!score_g4_supported(codes, cs_b, cs_h, cs_t)) return LAP_ERR_UNSUPPORTED;
   // query fragments are read as 8-byte vectors
@@ -1468,7 +1486,7 @@ extern "C" int lap_decode_step_workspace_size(int B, int Hq, int Hkv, int T, int
   ChainWs cw;
   int s = chain_ws(B, Hq, Hkv, T, D, keep_max, key_mode, &cw);
   if (s != LAP_OK) return s;
-  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, B * Hkv), 256);
+  const size_t fused = align_up(decode_step_fused_bytes(B * Hkv, T, kHeadRows), 256);
   *bytes = fused + cw.ret + cw.attn;
   return LAP_OK;
 }
@@ -1500,7 +1518,7 @@ extern "C" int lap_decode_step(
                          tail_count, plans, k_cols, max_sink, max_tail, key_mode, q, q_sb, q_sh,
                          keys, vals, dtype, B, Hq, Hkv, T_kv, D, k_sb, k_sh, k_st, v_sb, v_sh,
                          v_st, scale, out_idx, idx_dtype, out, workspace, workspace_bytes,
-                         B * Hkv, true, stream);
+                         kHeadRows, true, stream);
 }
 
 // ------------------------------------------------------------------------
@@ -1519,7 +1537,7 @@ extern "C" int lap_decode_step(
 namespace {
 
 constexpr size_t kScratchBytes = (size_t)64 << 20;
-constexpr int kScratchRows = 256;
+constexpr int kScratchRows = kHeadRows;
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -1532,6 +1550,14 @@ __global__ void scratch_clear_kernel(uint4* p, size_t n16) {
 std::mutex g_scratch_mu;
 void* g_scratch_dev[64];
 
+int scratch_clear_head(void* p, hipStream_t st) {
+  const size_t head = carve_step(nullptr, kScratchRows, 0, kScratchRows).bytes;
+  hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, st, static_cast<uint4*>(p),
+                     head / 16);
+  LAP_LAUNCH_CHECK("scratch_clear_kernel");
+  return LAP_OK;
+}
+
 int scratch_for_device(hipStream_t st, void** out) {
   int dev = 0;
   LAP_HIP(hipGetDevice(&dev), "hipGetDevice");
@@ -1543,10 +1569,8 @@ int scratch_for_device(hipStream_t st, void** out) {
     LAP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
     LAP_CHECK_CODE(p && (reinterpret_cast<uintptr_t>(p) & 255) == 0, LAP_ERR_HIP,
                    "scratch symbol address %p is not 256-byte aligned", p);
-    const size_t head = carve_step(nullptr, kScratchRows, 0, kScratchRows).bytes;
-    hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, st, static_cast<uint4*>(p),
-                       head / 16);
-    LAP_LAUNCH_CHECK("scratch_clear_kernel");
+    const int s = scratch_clear_head(p, st);
+    if (s != LAP_OK) return s;
     g_scratch_dev[dev] = p;
   }
   *out = g_scratch_dev[dev];
@@ -1581,4 +1605,32 @@ extern "C" int lap_decode_step_noalloc(
     set_error("%s: this shape needs more than the static scratch of %zu bytes (%s)", who,
               kScratchBytes, lap_last_error());
   return s;
+}
+
+// Health counters of the static scratch on the current device (the same
+// two words lap_decode_step_status reads from a workspace), after the device
+// has finished its work; zeros before the first call on the device.
+extern "C" int lap_decode_step_noalloc_status(uint32_t* split_rows, uint32_t* timeouts) {
+  clear_error();
+  LAP_CHECK(split_rows && timeouts, "lap_decode_step_noalloc_status: null pointer");
+  void* p = nullptr;
+  int s = scratch_for_device(nullptr, &p);
+  if (s != LAP_OK) return s;
+  LAP_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  uint32_t h[2] = {0, 0};
+  LAP_HIP(hipMemcpy(h, p, sizeof(h), hipMemcpyDeviceToHost), "status copy");
+  *split_rows = h[0];
+  *timeouts = h[1];
+  return LAP_OK;
+}
+
+// Zero the static scratch's persistent head (counters, row barriers, row
+// histograms) on the current device with a fill kernel on `stream`: the
+// reset after an unhealthy call.  Allocates nothing.
+extern "C" int lap_decode_step_noalloc_reset(lap_stream_t stream) {
+  clear_error();
+  void* p = nullptr;
+  int s = scratch_for_device(as_stream(stream), &p);
+  if (s != LAP_OK) return s;
+  return scratch_clear_head(p, as_stream(stream));
 }

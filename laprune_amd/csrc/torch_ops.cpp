@@ -14,6 +14,7 @@
 #include <ATen/core/Tensor.h>
 #include <c10/hip/HIPStream.h>
 
+#include <algorithm>
 #include <cmath>
 #include <optional>
 
@@ -90,6 +91,34 @@ void decode_step(const at::Tensor& lut, const std::optional<at::Tensor>& codes, 
   same_gpu("laprune::decode_step", {&lut, opt(codes), opt(plans), &q, &keys, &vals, &idx, &out, &ws});
   TORCH_CHECK(!codes || codes->scalar_type() == at::kByte, "laprune::decode_step: u8 codes");
   TORCH_CHECK(!plans || plans->scalar_type() == at::kInt, "laprune::decode_step: int32 plans");
+  // Sizes the kernels index by, checked here so that a mis-sized tensor is
+  // an error and never an out-of-bounds read or write.
+  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2), Hkv = keys.size(1);
+  TORCH_CHECK(keys.scalar_type() == q.scalar_type() && vals.scalar_type() == q.scalar_type() &&
+                  out.scalar_type() == q.scalar_type(),
+              "laprune::decode_step: q, keys, vals and out must share one dtype");
+  TORCH_CHECK(keys.size(0) == B && vals.size(0) == B && vals.size(1) == Hkv &&
+                  vals.size(2) >= keys.size(2) && keys.size(3) == D && vals.size(3) == D,
+              "laprune::decode_step: keys / vals must be [B, Hkv, T_kv, D] of q's B and D");
+  TORCH_CHECK(out.is_contiguous() && out.numel() >= B * Hq * D,
+              "laprune::decode_step: out must be contiguous with at least B * Hq * D elements");
+  TORCH_CHECK(lut.scalar_type() == at::kHalf && lut.is_contiguous() &&
+                  lut.numel() >= B * Hkv * 32 * 256 * 4,
+              "laprune::decode_step: lut must be the contiguous fp16 [B * Hkv, 32, 256, 4] table");
+  const int64_t rows = Hkv * ((key_mode & LAP_SELECT_PER_HEAD) ? 4 : 1);
+  const int64_t cols = plans ? k_cols : std::max<int64_t>(0, std::min(k, cand_end - cand_start));
+  if (cols > 0) {
+    TORCH_CHECK(idx.is_contiguous() && idx.numel() >= B * rows * cols &&
+                    (idx.scalar_type() == at::kInt || idx.scalar_type() == at::kLong),
+                "laprune::decode_step: idx must be contiguous int32/int64 with at least "
+                "B * rows * k elements");
+    TORCH_CHECK(codes && codes->dim() == 4 && codes->size(0) == B && codes->size(1) == Hkv &&
+                    codes->size(2) >= T && codes->size(3) == 32,
+                "laprune::decode_step: codes must be [B, Hkv, >=T, 32]");
+  }
+  TORCH_CHECK(!plans || (plans->is_contiguous() && plans->numel() >= B * 8),
+              "laprune::decode_step: plans must hold B lap_row_plan records (B x 8 int32)");
+  TORCH_CHECK(ws.is_contiguous(), "laprune::decode_step: contiguous workspace");
   const int64_t cs_b = codes ? codes->stride(0) : 0, cs_h = codes ? codes->stride(1) : 0,
                 cs_t = codes ? codes->stride(2) : 0;
   check(lap_decode_step(ptr(lut), codes ? static_cast<const uint8_t*>(codes->data_ptr()) : nullptr,
@@ -111,6 +140,15 @@ void dense_decode(const at::Tensor& q, const at::Tensor& keys, const at::Tensor&
   TORCH_CHECK(q.dim() == 3 && keys.dim() == 4 && vals.dim() == 4,
               "laprune::dense_decode: q [B, Hq, D], keys / vals [B, Hkv, T, D]");
   same_gpu("laprune::dense_decode", {&q, &keys, &vals, &out, &ws});
+  TORCH_CHECK(keys.scalar_type() == q.scalar_type() && vals.scalar_type() == q.scalar_type() &&
+                  out.scalar_type() == q.scalar_type() && out.is_contiguous() &&
+                  out.numel() >= q.size(0) * q.size(1) * q.size(2),
+              "laprune::dense_decode: keys, vals and a contiguous out of B * Hq * D elements in "
+              "q's dtype");
+  TORCH_CHECK(keys.size(0) == q.size(0) && vals.size(0) == q.size(0) &&
+                  vals.size(1) == keys.size(1) && vals.size(2) >= keys.size(2) &&
+                  keys.size(3) == q.size(2) && vals.size(3) == q.size(2),
+              "laprune::dense_decode: keys / vals must be [B, Hkv, T, D] of q's B and D");
   check(lap_dense_attn_decode(ptr(q), q.stride(0), q.stride(1), ptr(keys), ptr(vals),
                               dtype_code(q), (int)q.size(0), (int)q.size(1), (int)keys.size(1),
                               (int)keys.size(2), (int)q.size(2), keys.stride(0), keys.stride(1),
@@ -128,6 +166,16 @@ void attn_decode_ragged(const at::Tensor& q, const at::Tensor& keys, const at::T
   TORCH_CHECK(q.dim() == 3 && keys.dim() == 4 && vals.dim() == 4,
               "laprune::attn_decode_ragged: q [B, Hq, D], keys / vals [B, Hkv, T, D]");
   same_gpu("laprune::attn_decode_ragged", {&q, &keys, &vals, opt(idx), &plans, &out, &ws});
+  TORCH_CHECK(keys.scalar_type() == q.scalar_type() && vals.scalar_type() == q.scalar_type() &&
+                  out.scalar_type() == q.scalar_type() && out.is_contiguous() &&
+                  out.numel() >= q.size(0) * q.size(1) * q.size(2),
+              "laprune::attn_decode_ragged: keys, vals and a contiguous out of B * Hq * D "
+              "elements in q's dtype");
+  TORCH_CHECK(plans.scalar_type() == at::kInt && plans.is_contiguous() &&
+                  plans.numel() >= q.size(0) * 8,
+              "laprune::attn_decode_ragged: plans must hold B lap_row_plan records");
+  TORCH_CHECK(!idx || (idx->is_contiguous() && idx->numel() >= q.size(0) * H_idx * k_cols),
+              "laprune::attn_decode_ragged: idx must hold B * H_idx * k_cols entries");
   check(lap_sparse_attn_decode_ragged(
             ptr(q), q.stride(0), q.stride(1), ptr(keys), ptr(vals), dtype_code(q),
             (int)q.size(0), (int)q.size(1), (int)keys.size(1), (int)keys.size(2),

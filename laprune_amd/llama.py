@@ -30,7 +30,7 @@ import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from .cache import DecodeKVCache
-from .retrieval import DenseDecoder, RetrievalConfig, SparseDecoder
+from .retrieval import DenseDecoder, RetrievalConfig, SparseDecoder, check_step_health
 
 
 @dataclass
@@ -64,10 +64,14 @@ class LAPruneLlama:
       settings: which layers are LAPrune layers and the selection settings.
       batch: sequences decoded together.
       capacity: token capacity of every layer's cache (prompt + new tokens).
+      health_every: decode steps between reads of the one-launch steps'
+        health counters (one synchronisation each; 0 reads only at the end
+        of ``generate``).  A non-zero counter raises
+        :class:`~laprune_amd.retrieval.StepHealthError`.
     """
 
     def __init__(self, model, codebooks: dict[int, torch.Tensor], settings: LAPruneSettings,
-                 batch: int, capacity: int):
+                 batch: int, capacity: int, health_every: int = 64):
         from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
         self._rope = apply_rotary_pos_emb
         self.model = model
@@ -99,6 +103,8 @@ class LAPruneLlama:
             self._fuse_qkv(attn)
             attn.forward = self._make_forward(i, attn)
         self._row = None  # sequence being prefilled alone (ragged prefill)
+        self.health_every = health_every
+        self._since_check = 0
         self._dev_mode = False
         self._graph = None
         self._g = None
@@ -272,7 +278,36 @@ class LAPruneLlama:
         """One decode step for all sequences: tokens [B, 1]; returns logits [B, V]."""
         self._check_room(1)
         pos = torch.tensor(self.lengths, device=self.dev)[:, None]
-        return self._forward(tokens.reshape(self.B, 1).to(self.dev), pos)
+        logits = self._forward(tokens.reshape(self.B, 1).to(self.dev), pos)
+        self._count_step()
+        return logits
+
+    # ------------------------------------------------------------ health
+    def check_health(self) -> None:
+        """Read every LAPrune layer's health counters (one gather, one
+        synchronising copy) and raise StepHealthError naming the layers
+        whose one-launch steps split a row over XCDs or timed out a barrier."""
+        self._since_check = 0
+        decs = [(i, st.sparse) for i, st in enumerate(self.states) if st.sparse is not None]
+        if not decs:
+            return
+        words = torch.stack([d.status_words() for _, d in decs]).cpu()
+        bad = [(i, int(w[0]), int(w[1])) for (i, _), w in zip(decs, words.tolist())
+               if w[0] or w[1]]
+        if bad:
+            check_step_health(sum(b[1] for b in bad), sum(b[2] for b in bad),
+                              who=f"LAPruneLlama (layers {[b[0] for b in bad]})")
+
+    def reset_health(self) -> None:
+        """Zero every LAPrune layer's step workspace after an unhealthy step."""
+        for st in self.states:
+            if st.sparse is not None:
+                st.sparse.reset_health()
+
+    def _count_step(self) -> None:
+        self._since_check += 1
+        if self.health_every and self._since_check >= self.health_every:
+            self.check_health()
 
     # ------------------------------------------------------------ captured decode
     # One decode step of the whole model as one HIP graph.  Per-step values
@@ -385,6 +420,7 @@ class LAPruneLlama:
             self._graph[self._g_flush] = g
         else:
             g.replay()
+        self._count_step()
         return self._g_logits
 
     def next_tokens(self) -> torch.Tensor:
@@ -413,6 +449,7 @@ class LAPruneLlama:
             new.append(tok)
             if eos_token_id is not None and bool((tok == eos_token_id).all()):
                 break
+        self.check_health()
         return torch.cat([ids] + new, dim=1)
 
 

@@ -36,6 +36,27 @@ from . import _native as N
 from ._ops import ops
 
 
+class StepHealthError(RuntimeError):
+    """A one-launch decode step ran outside its guarantees: a KV row whose
+    workgroups did not all run on one XCD (their exchange through that XCD's
+    L2 is then unguaranteed), or a row barrier that gave up waiting.  The
+    results of the steps since the workspace was last zeroed are not to be
+    trusted; zero the workspace (``SparseDecoder.reset_health``) before the
+    next step."""
+
+
+def check_step_health(split_rows: int, timeouts: int, who: str) -> None:
+    """Raise :class:`StepHealthError` naming the counts when either health
+    counter of the one-launch step is non-zero (the status words of
+    ``lap_decode_step_status``); return quietly when both are zero."""
+    if split_rows or timeouts:
+        raise StepHealthError(
+            f"{who}: the one-launch decode step is unhealthy: {split_rows} KV row(s) ran "
+            f"their workgroups on more than one XCD and {timeouts} row barrier(s) timed out; "
+            f"the selections and attention outputs since the workspace was zeroed are "
+            f"undefined")
+
+
 @dataclass
 class RetrievalConfig:
     """Hot-path keys of the reference's ``draft_kwargs`` (defaults as in the
@@ -250,6 +271,8 @@ class SparseDecoder:
         t_total = keys.shape[2] if tt_rows is None else tt_rows[0]
         if t_total > self.T_max or t_codes > t_total:
             raise RuntimeError("cache length exceeds the decoder's max_tokens")
+        if t_total > keys.shape[2] or t_total > vals.shape[2] or t_codes > codes.shape[2]:
+            raise RuntimeError("a sequence length exceeds the cache views")
         p = self.plan(t_codes, t_total)
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
         self._ops.lut_build(qf, self.cb, 4, N.LUT_GMKG, self.lut)
@@ -279,6 +302,23 @@ class SparseDecoder:
         N.call("lap_decode_step_status", N.ptr(self.ws), self.ws.numel(), N.byref(a),
                N.byref(b))
         return int(a.value), int(b.value)
+
+    def status_words(self) -> torch.Tensor:
+        """The two health counters as a device int32 view [2] of the
+        workspace (no copy, no synchronisation): callers that watch many
+        decoders gather these and copy them to the host once."""
+        return self.ws[:8].view(torch.int32)
+
+    def check_health(self) -> None:
+        """Raise :class:`StepHealthError` if any one-launch step on this
+        decoder's workspace split a row over XCDs or timed out a barrier
+        (synchronises)."""
+        check_step_health(*self.fused_status(), who="SparseDecoder")
+
+    def reset_health(self) -> None:
+        """Zero the workspace (counters, barrier words and histograms) after
+        an unhealthy step, so that later steps start from a clean state."""
+        self.ws.zero_()
 
     def _step_ragged(self, q, codes, keys, vals, t_codes: list[int],
                      t_total: list[int]) -> torch.Tensor:

@@ -233,3 +233,42 @@ def test_shipped_codebooks_load():
     assert abs(b0.codebooks.abs().max().item() - 8.82) < 1e-2
     stage_norm = b0.codebooks.norm(dim=2).mean(dim=1)
     assert stage_norm[0] > 4 * stage_norm[-1]
+
+
+def test_step_health_raises_on_nonzero_counters():
+    """The one-launch step's two health counters (rows split over XCDs,
+    barrier time-outs) turn into StepHealthError naming both counts; zeros
+    pass quietly."""
+    R.check_step_health(0, 0, "x")
+    with pytest.raises(R.StepHealthError, match="2 KV row"):
+        R.check_step_health(2, 0, "x")
+    with pytest.raises(R.StepHealthError, match="5 row barrier"):
+        R.check_step_health(0, 5, "x")
+    assert issubclass(R.StepHealthError, RuntimeError)
+
+
+def test_llama_health_check_names_layers():
+    """LAPruneLlama.check_health gathers every LAPrune layer's status words
+    (hand-set here in host workspaces) and names the unhealthy layers."""
+    import types
+    from laprune_amd.llama import LAPruneLlama
+
+    class FakeDec:
+        status_words = R.SparseDecoder.status_words
+
+        def __init__(self, split, tmo):
+            self.ws = torch.zeros(64, dtype=torch.uint8)
+            self.ws[:8].view(torch.int32).copy_(torch.tensor([split, tmo], dtype=torch.int32))
+
+    def st(dec):
+        return types.SimpleNamespace(sparse=dec)
+
+    fake = types.SimpleNamespace(states=[st(None), st(FakeDec(0, 0)), st(FakeDec(1, 0)),
+                                         st(FakeDec(0, 2))], _since_check=7)
+    with pytest.raises(R.StepHealthError) as e:
+        LAPruneLlama.check_health(fake)
+    msg = str(e.value)
+    assert "layers [2, 3]" in msg and "1 KV row" in msg and "2 row barrier" in msg
+    assert fake._since_check == 0
+    fake.states = [st(None), st(FakeDec(0, 0))]
+    LAPruneLlama.check_health(fake)  # healthy: no error

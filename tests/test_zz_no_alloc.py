@@ -5,8 +5,11 @@ Both entry points run the same kernels, so indices and attention outputs
 must be identical bit for bit.  Calls in a row shrink the input: the C2
 shape (one launch, 32 workgroups per KV row), then a shorter partial row,
 then ragged device plans over B = 2 (fewer workgroups per row, more rows),
-then per-head selection (the kernel chain, which uses the scratch past the
-persistent head).  Shapes beyond the scratch are refused before any launch.
+then per-head selection at 8192 columns (the one-launch per-head kernel),
+then head_dim 64, which only the kernel chain serves (the scratch past the
+persistent head: the retrieve and attention workspaces).  After every call
+the scratch's health counters (lap_decode_step_noalloc_status) are zero.
+Shapes beyond the scratch are refused before any launch.
 """
 import math
 
@@ -18,7 +21,7 @@ pytestmark = pytest.mark.gpu
 Hq, Hkv, D = 32, 8, 128
 
 
-def _inputs(seed, B, T, dev):
+def _inputs(seed, B, T, dev, D=D):
     g = torch.Generator().manual_seed(seed)
     cb = torch.randn(32, 256, D, generator=g) * 0.02
     codes = torch.randint(0, 256, (B, Hkv, T, 32), generator=g, dtype=torch.uint8).to(dev)
@@ -33,7 +36,14 @@ def _decoder(cb, B, T, topk, select="group"):
     from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
     cfg = RetrievalConfig(topk=topk, sink_size=4, local_window=64, select=select,
                           score_dtype=torch.bfloat16)
-    return SparseDecoder(cb, B, Hq, Hkv, D, T, cfg, dtype=torch.bfloat16)
+    return SparseDecoder(cb, B, Hq, Hkv, cb.shape[2], T, cfg, dtype=torch.bfloat16)
+
+
+def _scratch_status():
+    from laprune_amd import _native as N
+    a, b = N.u32(), N.u32()
+    N.call("lap_decode_step_noalloc_status", N.byref(a), N.byref(b))
+    return int(a.value), int(b.value)
 
 
 def _noalloc(dec, q, codes, kk, vv, T, T_kv, p, plans=None, k_cols=0, max_sink=0, max_tail=0):
@@ -47,15 +57,16 @@ def _noalloc(dec, q, codes, kk, vv, T, T_kv, p, plans=None, k_cols=0, max_sink=0
            codes.stride(1), codes.stride(2), T, p["cand_start"], p["cand_end"], p["k"],
            p["sink"], p["tail_start"], p["tail_count"], N.ptr(plans), k_cols, max_sink, max_tail,
            dec.key_mode, N.ptr(q), q.stride(0), q.stride(1), N.ptr(kk), N.ptr(vv),
-           N.dtype_code(q.dtype), dec.B, Hq, Hkv, T_kv, D, kk.stride(0), kk.stride(1),
-           kk.stride(2), vv.stride(0), vv.stride(1), vv.stride(2), 1.0 / math.sqrt(D),
+           N.dtype_code(q.dtype), dec.B, Hq, Hkv, T_kv, dec.D, kk.stride(0), kk.stride(1),
+           kk.stride(2), vv.stride(0), vv.stride(1), vv.stride(2), 1.0 / math.sqrt(dec.D),
            N.ptr(idx), N.I32, N.ptr(out), N.stream_of(q))
     torch.cuda.synchronize()
+    assert _scratch_status() == (0, 0)
     return idx, out
 
 
-def _uniform(dev, seed, B, T, tc, topk, select="group"):
-    cb, codes, kk, vv, q = _inputs(seed, B, T, dev)
+def _uniform(dev, seed, B, T, tc, topk, select="group", D=D):
+    cb, codes, kk, vv, q = _inputs(seed, B, T, dev, D)
     dec = _decoder(cb, B, T, topk, select)
     want = dec.step(q, codes[:, :, :tc], kk, vv, t_codes=tc, t_total=T)
     torch.cuda.synchronize()
@@ -91,8 +102,12 @@ def test_noalloc_matches_workspace_step_shrinking(dev):
                         max(pl["sink"] for pl in plans), max(pl["tail_count"] for pl in plans))
     assert torch.equal(idx[..., :k_cols], want_idx[..., :k_cols])
     assert torch.equal(out, want_out)
-    print("noalloc: per-head selection 8192 (kernel chain)", flush=True)
+    print("noalloc: per-head selection 8192 (one-launch per-head kernel)", flush=True)
     _uniform(dev, 903, 1, 8192, 8192, None, select="head")
+    print("noalloc: head_dim 64, 8192 (kernel chain)", flush=True)
+    _uniform(dev, 905, 1, 8192, 8192, 512, D=64)
+    print("noalloc: head_dim 64, per-head selection 4096 (kernel chain)", flush=True)
+    _uniform(dev, 906, 1, 4096, 4096, None, select="head", D=64)
 
 
 def test_noalloc_refuses_oversized_shapes(dev):
