@@ -122,17 +122,22 @@ __device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dt) {
   return dt == LAP_DTYPE_F16 ? h2f(v) : bf2f(v);
 }
 
-// Orderable 16-bit key of a fp16 score: larger score -> larger key; -0 and
-// +0 map to the same key.
-__device__ __forceinline__ uint32_t f16_key(uint16_t h) {
-  if ((h & 0x7fffu) == 0) h = 0;
-  return (h & 0x8000u) ? (~(uint32_t)h & 0xffffu) : ((uint32_t)h | 0x8000u);
+// Orderable 16-bit key of fp16 / bf16 bits b: larger value -> larger key;
+// -0 and +0 map to the same key.  Written with selects (no branches), as it
+// runs once or four times per scored token.
+__device__ __forceinline__ uint32_t orderable16(uint32_t b) {
+  b = (b & 0x7fffu) == 0 ? 0u : b;
+  return b ^ ((b & 0x8000u) ? 0xffffu : 0x8000u);
 }
-// Orderable key of bf16(fp16 score) (the model-dtype cast before top-k).
+// Orderable key of a fp16 score.
+__device__ __forceinline__ uint32_t f16_key(uint16_t h) { return orderable16(h); }
+// Orderable key of bf16(fp16 score) (the model-dtype cast before top-k): the
+// f2bf rounding of the exact fp32 value of h, NaN kept quiet.
 __device__ __forceinline__ uint32_t bf16_key_of_f16(uint16_t h) {
-  uint16_t b = f2bf(h2f(h));
-  if ((b & 0x7fffu) == 0) b = 0;
-  return (b & 0x8000u) ? (~(uint32_t)b & 0xffffu) : ((uint32_t)b | 0x8000u);
+  const uint32_t u = __builtin_bit_cast(uint32_t, h2f(h));
+  const bool nan = (u & 0x7fffffffu) > 0x7f800000u;
+  const uint32_t b = nan ? ((u >> 16) | 0x40u) : ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  return orderable16(b);
 }
 
 // Exact fp32 accumulate of an fp16 value: acc + (float)h with one rounding.

@@ -76,50 +76,15 @@ __device__ __forceinline__ void write_empty_hist(const ScoreOut& so, int r, int 
   write_hists<1>(so, nullptr, r, R, chunk, tid, threads);
 }
 
-// Selection keys and their level-1 histogram counts, in two halves for the
-// pipelined scorer: the counts of token t (LDS atomics over the candidate
-// window, inside the stage loop) and its global stores (fp16 scores, keys),
-// issued after the loop.  A token is held as its four fp16 head scores (two
-// per word) and, for group rows, its key gk: the key of fp16(max of the four
-// fp32 scores), which equals the max of the four fp16 scores' keys since
-// fp16 rounding is monotone.  Per-head rows key each head's own score.
-__device__ __forceinline__ uint32_t key_of_f16(const ScoreOut& so, uint16_t h) {
-  return so.key_mode == LAP_KEY_BF16 ? bf16_key_of_f16(h) : f16_key(h);
+// Selection keys.  A group row keys fp16(max of its four fp32 head scores),
+// which equals the max of the four fp16 scores' keys since fp16 rounding is
+// monotone; per-head rows key each head's own score.  bf16 keys rank the
+// model-dtype cast of the fp16 score (aq_evaluation.py:166).  The key mode is
+// a uniform select, not a branch: this runs once or four times per token.
+__device__ __forceinline__ uint32_t key_of_score(float e, bool kbf) {
+  const uint16_t h = f2h(e);
+  return kbf ? bf16_key_of_f16(h) : f16_key(h);
 }
-template <int HC>
-__device__ __forceinline__ void count_keys(const ScoreOut& so, const RowCols& rc, int t,
-                                           uint32_t h01, uint32_t h23, uint32_t gk,
-                                           HistRows<HC> s_hist) {
-  if (!so.hist || t < rc.cs || t >= rc.ce) return;
-  const int copy = (int)(__lane_id() % HC) * kHPitch;
-  if (so.per_head) {
-    const uint16_t h[kG] = {(uint16_t)h01, (uint16_t)(h01 >> 16), (uint16_t)h23,
-                            (uint16_t)(h23 >> 16)};
-#pragma unroll
-    for (int g = 0; g < kG; ++g) atomicAdd(&s_hist[g][copy + (key_of_f16(so, h[g]) >> 8)], 1u);
-  } else {
-    atomicAdd(&s_hist[0][copy + (gk >> 8)], 1u);
-  }
-}
-__device__ __forceinline__ void store_token(const ScoreOut& so, int r, int T, int t, uint32_t h01,
-                                            uint32_t h23, uint32_t gk) {
-  const uint16_t h[kG] = {(uint16_t)h01, (uint16_t)(h01 >> 16), (uint16_t)h23,
-                          (uint16_t)(h23 >> 16)};
-  if (so.heads) {
-    uint16_t* hp = so.heads + (int64_t)(r * kG) * T + t;
-#pragma unroll
-    for (int g = 0; g < kG; ++g) hp[g * (int64_t)T] = h[g];
-  }
-  if (!so.keys) return;
-  if (so.per_head) {
-#pragma unroll
-    for (int g = 0; g < kG; ++g)
-      so.keys[((int64_t)r * kG + g) * T + t] = (uint16_t)key_of_f16(so, h[g]);
-  } else {
-    so.keys[(int64_t)r * T + t] = (uint16_t)gk;
-  }
-}
-
 
 // Pipelined fused scorer (either table layout).  A workgroup owns THREADS * TOK
 // consecutive tokens of one KV row; thread tid scores tokens
@@ -154,18 +119,13 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
   __shared__ __attribute__((aligned(16))) uint4 s_lut[kLutBytes / 16];
   __shared__ uint32_t s_hist[PH ? kG : 1][HC * kHPitch];
 
+  // The table loads go out first, before anything else reads the kernel
+  // arguments: they need only the row (lut and R), and everything after
+  // them (the row's plan, a second round of argument loads) would otherwise
+  // delay the table, which every lookup waits for, by a scalar-load round
+  // trip or two (about 0.5 us at C2).
   const int r = blockIdx.x % R;
-  const int chunk = blockIdx.x / R;
   const int tid = threadIdx.x;
-  const int b = r / Hkv, hkv = r - b * Hkv;
-  const RowCols rc = row_cols(so, b, T);
-  const int t0 = chunk * (THREADS * TOK);
-  const int t1 = min(rc.t_end, t0 + THREADS * TOK);  // without plans t1 > t0 by the grid
-  if (t0 >= t1) {
-    write_empty_hist(so, r, R, chunk, tid, THREADS);
-    return;
-  }
-
   const uint4* src = reinterpret_cast<const uint4*>(lut + (int64_t)r * (kG * kM * kK));
   // The table: the interleaved layout is copied as is; the reference layout
   // [4][M][K] is read as 8 consecutive entries of each head per group of
@@ -182,6 +142,17 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
 #pragma unroll
       for (int g = 0; g < kG; ++g) f[4 * j + g] = gload16_ordered(hsrc + g * (kM * kK) + e0);
     }
+  }
+
+  const int chunk = blockIdx.x / R;
+  const int b = r / Hkv, hkv = r - b * Hkv;
+  const RowCols rc = row_cols(so, b, T);
+  const int t0 = chunk * (THREADS * TOK);
+  const int t1 = min(rc.t_end, t0 + THREADS * TOK);  // without plans t1 > t0 by the grid
+  if (t0 >= t1) {
+    vm_wait(0, f[0]);  // the table loads drain before the wave ends
+    write_empty_hist(so, r, R, chunk, tid, THREADS);
+    return;
   }
 
   // Rows past the chunk end load the chunk's last row (always in bounds) and
@@ -214,35 +185,77 @@ __global__ __launch_bounds__(THREADS) void score_g4p_kernel(
   // (which every lookup needs) then arrives later than the rows do.
 #pragma unroll
   for (int j = 0; j < kAhead; ++j) request(j);
-  for (int i = tid; i < key_rows(so) * HC * kHPitch; i += THREADS)
+  for (int i = tid; i < (PH ? kG : 1) * HC * kHPitch; i += THREADS)
     s_hist[i / (HC * kHPitch)][i % (HC * kHPitch)] = 0;
   lds_barrier();
 
-  // The scores stay in registers (fp16, two per word) until every stage is
-  // in: a store issued between two stage waits would count in the next
-  // wait (stores and loads share vmcnt), which would then wait for the
-  // store's acknowledgement as well as for the stage.
+  // The scores and keys stay in registers until every stage is in: a store
+  // issued between two stage waits would count in the next wait (stores and
+  // loads share vmcnt), which would then wait for the store's
+  // acknowledgement as well as for the stage.
   const char* lds = reinterpret_cast<const char*>(s_lut);
-  uint32_t h01[TOK], h23[TOK], gk[TOK];
+  const uint32_t copy = (uint32_t)(__lane_id() % HC) * kHPitch;
+  const int lo = max(rc.cs, 0), hi = min(rc.ce, t1);  // histogram window in this chunk
+  const bool kbf = so.key_mode == LAP_KEY_BF16;
+  float sc[TOK][kG];
+  uint32_t kw[TOK][PH ? 2 : 1];  // group key, or the four heads' keys two per word
+  auto count = [&](int j) {
+    if constexpr (PH) {
+      atomicAdd(&s_hist[0][copy + ((kw[j][0] & 0xffffu) >> 8)], 1u);
+      atomicAdd(&s_hist[1][copy + (kw[j][0] >> 24)], 1u);
+      atomicAdd(&s_hist[2][copy + ((kw[j][1] & 0xffffu) >> 8)], 1u);
+      atomicAdd(&s_hist[3][copy + (kw[j][1] >> 24)], 1u);
+    } else {
+      atomicAdd(&s_hist[0][copy + (kw[j][0] >> 8)], 1u);
+    }
+  };
 #pragma unroll
   for (int j = 0; j < TOK; ++j) {
     // Stages requested after stage j so far: j+1 .. min(j+kAhead-1, TOK-1).
     const int later = (j + kAhead - 1 < TOK - 1 ? j + kAhead - 1 : TOK - 1) - j;
     vm_wait(2 * later, c[j][0], c[j][1]);
-    if (j + kAhead < TOK) request(j + kAhead);
     stage_prio(j, TOK);
+    if (j + kAhead < TOK) request(j + kAhead);
     float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
     score_token(lds, as_uint4(c[j][0]), as_uint4(c[j][1]), one, e0, e1, e2, e3);
-    h01[j] = (uint32_t)f2h(e0) | ((uint32_t)f2h(e1) << 16);
-    h23[j] = (uint32_t)f2h(e2) | ((uint32_t)f2h(e3) << 16);
-    gk[j] = so.per_head ? 0u : key_of_f16(so, f2h(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3))));
-    const int t = t0 + j * THREADS + tid;
-    if (t < t1) count_keys<HC>(so, rc, t, h01[j], h23[j], gk[j], s_hist);
+    sc[j][0] = e0;
+    sc[j][1] = e1;
+    sc[j][2] = e2;
+    sc[j][3] = e3;
+    if constexpr (PH) {
+      kw[j][0] = key_of_score(e0, kbf) | (key_of_score(e1, kbf) << 16);
+      kw[j][1] = key_of_score(e2, kbf) | (key_of_score(e3, kbf) << 16);
+    } else {
+      kw[j][0] = key_of_score(fmaxf(fmaxf(e0, e1), fmaxf(e2, e3)), kbf);
+    }
+    if (so.hist) {
+      // a stage wholly inside the window (the common case) counts without a
+      // per-lane test
+      const int ts = t0 + j * THREADS, t = ts + tid;
+      if (ts >= lo && ts + THREADS <= hi) count(j);
+      else if (t >= lo && t < hi) count(j);
+    }
   }
 #pragma unroll
   for (int j = 0; j < TOK; ++j) {
     const int t = t0 + j * THREADS + tid;
-    if (t < t1) store_token(so, r, T, t, h01[j], h23[j], gk[j]);
+    if (t >= t1) continue;
+    if (so.heads) {
+      uint16_t* hp = so.heads + (int64_t)(r * kG) * T + t;
+#pragma unroll
+      for (int g = 0; g < kG; ++g) hp[g * (int64_t)T] = f2h(sc[j][g]);
+    }
+    if (so.keys) {
+      if constexpr (PH) {
+        uint16_t* kp = so.keys + (int64_t)r * kG * T + t;
+        kp[0] = (uint16_t)kw[j][0];
+        kp[T] = (uint16_t)(kw[j][0] >> 16);
+        kp[2 * (int64_t)T] = (uint16_t)kw[j][1];
+        kp[3 * (int64_t)T] = (uint16_t)(kw[j][1] >> 16);
+      } else {
+        so.keys[(int64_t)r * T + t] = (uint16_t)kw[j][0];
+      }
+    }
   }
 
   if (so.hist) {

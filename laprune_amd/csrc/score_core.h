@@ -20,14 +20,44 @@ constexpr int kHPitch = 257;
 template <int HC>
 using HistRows = uint32_t (*)[HC * kHPitch];
 
+// Byte j of code word w times 8 (the table offset of that code within its
+// codebook's 2 KiB slice), one SDWA shift: the compiler extracts bytes 1-3
+// this way by itself but byte 0 with a shift and a mask.  `three` holds 3 in
+// a VGPR (SDWA takes no literal operand).
+template <int J>
+__device__ __forceinline__ uint32_t code_off(uint32_t w, uint32_t three) {
+  uint32_t r;
+  if constexpr (J == 0)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(r) : "v"(three), "v"(w));
+  else if constexpr (J == 1)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(r) : "v"(three), "v"(w));
+  else if constexpr (J == 2)
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(r) : "v"(three), "v"(w));
+  else
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(r) : "v"(three), "v"(w));
+  return r;
+}
+
 // Accumulate one token's 32 lookups into four fp32 head sums.
 __device__ __forceinline__ void score_token(const char* __restrict__ lds, const uint4 c0,
                                             const uint4 c1, _Float16 one, float& a0,
                                             float& a1, float& a2, float& a3) {
   const uint32_t w[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  uint32_t three = 3u;
+  asm("" : "+v"(three));
 #pragma unroll
   for (int m = 0; m < kM; ++m) {
-    const uint32_t off = ((w[m >> 2] >> ((m & 3) * 8)) & 0xffu) << 3;
+    uint32_t off;
+    switch (m & 3) {
+      case 0: off = code_off<0>(w[m >> 2], three); break;
+      case 1: off = code_off<1>(w[m >> 2], three); break;
+      case 2: off = code_off<2>(w[m >> 2], three); break;
+      default: off = code_off<3>(w[m >> 2], three); break;
+    }
     const half4_t v = *reinterpret_cast<const half4_t*>(lds + m * (kK * kG * 2) + off);
     a0 = acc_f16(a0, v.x, one);
     a1 = acc_f16(a1, v.y, one);
