@@ -400,6 +400,27 @@ def ragged_leg(args, dev, cb) -> dict:
     }
 
 
+def ragged_steps(dev, cb, n: int) -> tuple[int, int]:
+    """n eager C5 ragged steps on the ragged leg's inputs (the counters
+    pass); returns the decoder's health counters."""
+    import torch
+    from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
+    g = torch.Generator(device="cpu").manual_seed(5)
+    lens = torch.randint(RAG_T0, RAG_T1 + 1, (RAG_B,), generator=g).tolist()
+    t_codes = [t - (t % 64) for t in lens]
+    cap = RAG_T1 + 64
+    codes = torch.randint(0, 256, (RAG_B, HKV, cap, M), generator=g, dtype=torch.uint8).to(dev)
+    kk = torch.randn(RAG_B, HKV, cap, D, dtype=torch.bfloat16, device=dev)
+    vv = torch.randn(RAG_B, HKV, cap, D, dtype=torch.bfloat16, device=dev)
+    q = torch.randn(RAG_B, HQ, 1, D, generator=g).bfloat16().to(dev)
+    cfg = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=RAG_TOPK, select="group",
+                          score_dtype=torch.bfloat16)
+    dec = SparseDecoder(cb, RAG_B, HQ, HKV, D, cap, cfg)
+    for _ in range(n):
+        dec.step(q, codes, kk, vv, t_codes=t_codes, t_total=lens)
+    return dec.fused_status()
+
+
 def _time_steps(run, steps: int) -> tuple[float, float]:
     """(seconds per step, host issue seconds per step) of `steps` calls of
     run(i) back to back, between two synchronisations."""
@@ -569,12 +590,27 @@ def main():
         b = torch.empty_like(a)
         for _ in range(3):
             torch.neg(a, out=b)
+        del a, b
         for _ in range(4):
             AK.aq_encode_greedy(enc_x, cb, enc_prep)
+        # the one-launch steps: C2 group selection, C2 per-head selection
+        # (the reference's rule, k = 2621) and one C5 ragged layer
+        for i in range(N_CODE_SETS):
+            sparse_step(i)
+        cfg_h = RetrievalConfig(sink_size=SINK, local_window=LOCAL, topk=None, select="head",
+                                score_dtype=torch.bfloat16)
+        dec_h = SparseDecoder(cb, 1, HQ, HKV, D, T, cfg_h)
+        for i in range(N_CODE_SETS):
+            kk, vv = kv_sets[i % N_KV_SETS]
+            c = codes_sets[i % N_CODE_SETS]
+            dec_h.step(q_sets[i], c[:, :, :T], kk[:, :, :T], vv[:, :, :T])
+        rag = ragged_steps(dev, cb, 4)
         torch.cuda.synchronize()
+        health = [dec.fused_status(), dec_h.fused_status(), rag]
         print(f"counters pass: {2 * N_CODE_SETS} scorer launches of {CODE_BYTES} code bytes, "
               f"3 fp32 negate launches of {CALIB_BYTES} bytes read + written, "
-              f"4 C3 encode launches", flush=True)
+              f"4 C3 encode launches, {N_CODE_SETS} C2 group steps, {N_CODE_SETS} C2 "
+              f"per-head steps, 4 C5 ragged steps; step health {health}", flush=True)
         return
 
     log("warm-up")
