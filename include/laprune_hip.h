@@ -490,7 +490,8 @@ int lap_rope_append(const void* q, int64_t q_sb, int64_t q_sh,
                     int t_cap, void* q_out, lap_stream_t stream);
 
 /* ======================================================================= *
- * Measurement kernels (no counterpart in the reference; not on the path).  *
+ * Diagnostics: measurement kernels (no counterpart in the reference; not  *
+ * on the path and never called by it).                                    *
  * They time what the fused G = 4 scorer's launch shape costs before any   *
  * scoring: bench.py reports them beside the scorer.  Both take the        *
  * scorer's grid for R KV rows of T tokens (R * ceil(T / 4096) workgroups   *
