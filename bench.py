@@ -47,8 +47,8 @@ serve the step from cache.
                  (C1: 8192 tokens, top-2048); 3 warm-ups, median of >= 10.
 ``encode``       configs[2] (C3): greedy AQ encode of one 64-token flush of
                  post-RoPE keys (8 KV heads x 64 tokens = 512 rows, 32x256
-                 codebooks), MFMA coarse search + exact recheck, next to the
-                 reference's fp32 greedy path on the host cores.
+                 codebooks), exact fp32 distances to every entry per stage,
+                 next to the reference's fp32 greedy path on the host cores.
 ``reference_mode`` the same C2 step with the reference's own selection: top-k
                  per query head on bf16-cast scores, budget 131004 -
                  int(0.98 * 131004) = 2621, each head attending over its own
@@ -814,9 +814,10 @@ def main():
                         "32x256 fp32 codebooks N(0,0.02); greedy codes + residual norm",
             "us": round(enc_us, 1),
             "rows_per_s": round(HKV * ENC_TOKENS / (enc_us * 1e-6), 1),
-            "mfma_tflops": round(ENC_FLOP / (enc_us * 1e-6) / 1e12, 3),
-            "mfma_peak_tflops_bf16": 2500.0,
-            "search": "bf16 MFMA coarse distances + exact fp32 dot16 recheck",
+            "fp32_tflops": round(ENC_FLOP / (enc_us * 1e-6) / 1e12, 3),
+            "fp32_peak_tflops": 157.3,
+            "search": "exact fp32 dot16 distances to all 256 entries per stage "
+                      "(encode_exact_kernel, 2 rows per workgroup)",
         },
         "roofline": {
             "bound": "hbm",

@@ -23,6 +23,7 @@
 // residual lives in LDS and is read as a broadcast.
 #include "common.h"
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -35,6 +36,7 @@ struct Prep {
   float* scn;      // [M][K] sqrtf(cn)
   uint16_t* frag;  // bf16 MFMA B fragments [M][K/16][D/16][64 lanes][4] (K % 16 == 0)
   uint16_t* frag4; // 4x4x4 B operands [M][ceil(K/64)][D/8][64 lanes][8] (K % 16 == 0)
+  float4* c4;      // [M][D/4][K] float4: entry k's d = 4q .. 4q+3 (the exact kernel's rows)
   size_t bytes;
 };
 
@@ -52,6 +54,8 @@ Prep carve_prep(void* base, int M, int K, int D) {
   if (K % 16 == 0) off = align_up(off + (size_t)M * K * D * 2, 256);
   p.frag4 = reinterpret_cast<uint16_t*>(b ? b + off : nullptr);
   if (K % 16 == 0) off = align_up(off + (size_t)M * ((K + 63) / 64) * 64 * D * 2, 256);
+  p.c4 = reinterpret_cast<float4*>(b ? b + off : nullptr);
+  off = align_up(off + (size_t)M * K * D * 4, 256);
   p.bytes = off;
   return p;
 }
@@ -114,6 +118,21 @@ __global__ __launch_bounds__(256) void encode_prep_transpose(const float* __rest
   for (int i = ty; i < 32; i += 8) {
     const int d = d0 + i, k = k0 + tx;
     if (k < K && d < D) ct[((int64_t)m * D + d) * K + k] = tile[tx][i];
+  }
+}
+
+// c4[m][q][k] = (C[m,k,4q], .., C[m,k,4q+3]): lane k of a wave reads 16 bytes
+// and the 64 lanes one contiguous kilobyte.
+__global__ __launch_bounds__(256) void encode_prep_c4(const float* __restrict__ cb, int M, int K,
+                                                      int D, float4* __restrict__ c4) {
+  const int Q = D / 4;
+  const int64_t n = (int64_t)M * Q * K;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int k = (int)(i % K);
+    const int64_t mq = i / K;
+    const int q = (int)(mq % Q), m = (int)(mq / Q);
+    c4[i] = *reinterpret_cast<const float4*>(cb + ((int64_t)m * K + k) * D + 4 * q);
   }
 }
 
@@ -941,6 +960,212 @@ __global__ __launch_bounds__(256) void encode_mfma4_kernel(
     rnorm[row0 + tid] = sqrtf(s.rn[tid]);
 }
 
+// ------------------------------------------ exact distances (flushes)
+// A decode flush (8 KV heads x 64 tokens = 512 rows) has few rows per CU, and
+// the bf16-MFMA kernels above pay a chain of dependent latencies per stage:
+// coarse pass, survivor ballots, an L2 round trip for each survivor's fp32
+// row, the exact recheck, the residual update.  Here every stage computes
+// the contract's distance exactly for all K entries, with no coarse pass and
+// no survivors: thread k of the 256 owns entry k and holds that entry's fp32
+// row in registers (D values), loaded from the [M][D/4][K] float4 layout of
+// the prep (each wave instruction reads one contiguous kilobyte).  A stage:
+//   A. every thread runs the contract's dot16 (16 fmaf chains of D/16 and
+//      the fold) of its entry against each of the R residuals, read from LDS
+//      as broadcasts; each block of its row is reloaded with the next
+//      stage's as soon as its products are done, so that the codebook
+//      stream (every workgroup reads all of it) runs under the arithmetic;
+//      each wave then takes its minimum of (orderable distance, entry) with
+//      DPP and a ballot.  At C3 (two rows) the products' residual reads and
+//      the stream each take about 0.9 us of a stage's 2 us;
+//   B. (after a barrier) wave v picks row v's winner among the four wave
+//      minima (lowest distance, then lowest entry; NaN and +inf never win;
+//      none finite: entry 0), reads that entry's row from the fp32
+//      codebook, subtracts it from the residual and forms the new
+//      dot16(r, r) in 16 lanes; a second barrier ends the stage.
+template <int D, int R>
+struct ExactShared {
+  float r[R][D];
+  unsigned long long part[R][4];  // (distance key << 32) | entry, per wave
+  float rn[R];
+  uint8_t code[R][kCodeStage];
+};
+
+// Block q of entry kc's row in stage m: a uniform base per block and one
+// 32-bit lane offset (the scalar-base address form: no 64-bit address per
+// load in registers).
+template <int D>
+__device__ __forceinline__ float4 exact_block(const float4* __restrict__ c4, int m, int q, int K,
+                                              uint32_t off) {
+  const char* base = reinterpret_cast<const char*>(c4 + ((int64_t)m * (D / 4) + q) * K);
+  return *reinterpret_cast<const float4*>(base + off);
+}
+
+// Orderable 32-bit key of a distance that may win (-0 as +0); 0xffffffff,
+// above every such key, marks one that may not.
+__device__ __forceinline__ uint32_t dist_key(float E, bool valid) {
+  uint32_t u = __builtin_bit_cast(uint32_t, E == 0.0f ? 0.0f : E);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return valid ? u : 0xffffffffu;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+// Minimum over the wave, uniform: rotations within each row of 16 lanes, then
+// the four row minima through scalar registers.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  x = min(x, dpp_u<0x128>(x));  // row_ror:8
+  x = min(x, dpp_u<0x124>(x));  // row_ror:4
+  x = min(x, dpp_u<0x122>(x));  // row_ror:2
+  x = min(x, dpp_u<0x121>(x));  // row_ror:1
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+  return min(min(a, b), min(c, d));
+}
+
+template <int D, int R>
+__global__ __launch_bounds__(256) void encode_exact_kernel(
+    RowMap rm, int N, const float* __restrict__ cb, const float4* __restrict__ c4,
+    const float* __restrict__ cn, int M, int K, float* __restrict__ rnorm) {
+  static_assert(R >= 1 && R <= 4, "one wave per row for the residual update");
+  constexpr int Q = D / 4, L = D / 16, QC = L / 4;  // float4 per chain
+  constexpr int P = R >= 4 ? 3 : 4;  // residual reads in flight per row (LDS counter: 15)
+  static_assert(L % 4 == 0, "chains of whole float4 blocks");
+  __shared__ __attribute__((aligned(16))) ExactShared<D, R> s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * R;
+  if (rm.ranges) {  // a workgroup with no live row leaves at once (same test in every thread)
+    bool any = false;
+    for (int r = 0; r < R; ++r) any = any || (row0 + r < N && rm.live(row0 + r));
+    if (!any) return;
+  }
+  const bool own = tid < K;
+  const int kc = own ? tid : K - 1;  // dead threads load entry K - 1 (in bounds, never chosen)
+  const uint32_t off = (uint32_t)kc * 16u;
+  float4 c[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) c[q] = exact_block<D>(c4, 0, q, K, off);
+  float cnk = cn[kc];
+  for (int i = tid; i < R * D; i += 256) {
+    const int r = i / D, d = i - r * D;
+    s.r[r][d] = (row0 + r < N && rm.live(row0 + r)) ? rm.xval(row0 + r, d) : 0.f;
+  }
+  lds_barrier();
+  if (wave < R && lane < 16) {
+    const float* rr = s.r[wave] + lane * L;
+    float a2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < L; ++t) a2 = __builtin_fmaf(rr[t], rr[t], a2);
+    a2 = row_fold16(a2);
+    if (lane == 0) s.rn[wave] = a2;
+  }
+  lds_barrier();
+  for (int m = 0; m < M; ++m) {
+    // the stage whose rows are requested behind this one's (the last stage
+    // re-requests itself: every load is unconditional)
+    const int mn = min(m + 1, M - 1);
+    // A: exact distances of this thread's entry to every row
+    float a[R][16];
+#pragma unroll
+    for (int v = 0; v < R; ++v)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a[v][j] = 0.f;
+    // The residual blocks are read P blocks ahead, in a ring; the scheduling
+    // barriers keep the compiler from hoisting every read to the top, which
+    // costs a register per value and pushes the entry rows out of registers.
+    float4 rb[P][R];
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int v = 0; v < R; ++v) rb[p][v] = *reinterpret_cast<const float4*>(&s.r[v][4 * p]);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int j = q / QC;
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        const float4 r4 = rb[q % P][v];
+        a[v][j] = __builtin_fmaf(r4.x, c[q].x, a[v][j]);
+        a[v][j] = __builtin_fmaf(r4.y, c[q].y, a[v][j]);
+        a[v][j] = __builtin_fmaf(r4.z, c[q].z, a[v][j]);
+        a[v][j] = __builtin_fmaf(r4.w, c[q].w, a[v][j]);
+        // pins the chain's progress here: without it the compiler sinks
+        // the later rows' products below the first row's selection and
+        // keeps their residual blocks live meanwhile
+        asm volatile("" : "+v"(a[v][j]));
+      }
+      c[q] = exact_block<D>(c4, mn, q, K, off);
+      if (q + P < Q) {
+#pragma unroll
+        for (int v = 0; v < R; ++v)
+          rb[q % P][v] = *reinterpret_cast<const float4*>(&s.r[v][4 * (q + P)]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int v = 0; v < R; ++v) {
+      const float E = (s.rn[v] + cnk) - 2.0f * fold16(a[v]);
+      const uint32_t key = dist_key(E, own && !(E != E) && E != INFINITY);
+      const uint32_t wmin = wave_min_u32(key);
+      // lanes holding the minimum; taken with the whole wave active (a
+      // ballot sees only active lanes), non-zero whenever wmin is a key
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(key == wmin);
+      if (lane == 0)  // the lowest such lane is the wave's lowest entry
+        s.part[v][wave] = wmin == 0xffffffffu ? ~0ull
+                                              : (((unsigned long long)wmin << 32) |
+                                                 (uint32_t)(wave * 64 + __builtin_ctzll(hit)));
+    }
+    cnk = cn[(int64_t)mn * K + kc];
+    lds_barrier();
+    // B: row `wave`'s winner, residual update and new squared norm
+    if (wave < R && lane < 16) {
+      const int v = wave;
+      unsigned long long b = s.part[v][0];
+#pragma unroll
+      for (int x = 1; x < 4; ++x) b = s.part[v][x] < b ? s.part[v][x] : b;
+      // none finite: entry 0; an entry is always below K (only threads
+      // k < K offer one), and the test keeps the row read in bounds
+      const uint32_t e = (uint32_t)b;
+      const int code = b == ~0ull || e >= (uint32_t)K ? 0 : (int)e;
+      const float* cw = cb + ((int64_t)m * K + code) * D + lane * L;
+      float4 w4[QC];
+#pragma unroll
+      for (int qq = 0; qq < QC; ++qq) w4[qq] = *reinterpret_cast<const float4*>(cw + 4 * qq);
+      float a2 = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < QC; ++qq) {
+        float4 r4 = *reinterpret_cast<const float4*>(&s.r[v][lane * L + 4 * qq]);
+        r4.x = r4.x - w4[qq].x;
+        r4.y = r4.y - w4[qq].y;
+        r4.z = r4.z - w4[qq].z;
+        r4.w = r4.w - w4[qq].w;
+        *reinterpret_cast<float4*>(&s.r[v][lane * L + 4 * qq]) = r4;
+        a2 = __builtin_fmaf(r4.x, r4.x, a2);
+        a2 = __builtin_fmaf(r4.y, r4.y, a2);
+        a2 = __builtin_fmaf(r4.z, r4.z, a2);
+        a2 = __builtin_fmaf(r4.w, r4.w, a2);
+      }
+      a2 = row_fold16(a2);
+      if (lane == 0) {
+        s.rn[v] = a2;
+        if (m < kCodeStage) s.code[v][m] = (uint8_t)code;
+        else if (row0 + v < N && rm.live(row0 + v)) rm.crow(row0 + v)[m] = (uint8_t)code;
+      }
+    }
+    lds_barrier();
+  }
+  const int mc = M < kCodeStage ? M : kCodeStage;
+  for (int i = tid; i < R * mc; i += 256) {
+    const int r = i / mc, mm = i - r * mc;
+    if (row0 + r < N && rm.live(row0 + r)) rm.crow(row0 + r)[mm] = s.code[r][mm];
+  }
+  if (tid < R && rnorm && row0 + tid < N && rm.live(row0 + tid))
+    rnorm[row0 + tid] = sqrtf(s.rn[tid]);
+}
+
 // ------------------------------------------------ large launches (prefill)
 // The same stage as enc_stage for 64 rows per workgroup.  A 16-row workgroup
 // holds its stage fragments (64 KiB at K = 256, D = 128) in registers, twice
@@ -1231,6 +1456,12 @@ extern "C" int lap_encode_prepare(const float* codebooks, int M, int K, int D, v
   hipLaunchKernelGGL(encode_prep_norms, dim3((M * K + 255) / 256), dim3(256), 0, st, codebooks,
                      M, K, D, p.cn, p.scn);
   LAP_LAUNCH_CHECK("encode_prep_norms");
+  {
+    const int64_t n = (int64_t)M * (D / 4) * K;
+    hipLaunchKernelGGL(encode_prep_c4, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)),
+                       dim3(256), 0, st, codebooks, M, K, D, p.c4);
+    LAP_LAUNCH_CHECK("encode_prep_c4");
+  }
   if (K % 16 == 0) {
     const int64_t n = (int64_t)M * (K / 16) * (D / 16) * 64;
     hipLaunchKernelGGL(encode_prep_frag, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
@@ -1274,6 +1505,35 @@ static bool encode_use_rows4(int N, int D) {
   return (int64_t)(N + kR4 - 1) / kR4 <= 2 * (int64_t)cus;
 }
 
+// Flushes take the exact kernel while its workgroups fit once on the chip:
+// one row per workgroup up to one workgroup per CU, two rows up to twice
+// that (a 512-row C3 flush: 256 workgroups).  A workgroup streams the whole
+// codebook whatever its row count, so two workgroups on one CU take about
+// twice as long, and larger flushes go to the 4-row MFMA kernel.
+// LAPRUNE_ENCODE_EXACT=0|1 forces the choice and LAPRUNE_ENCODE_EXACT_ROWS=1|2
+// the rows per workgroup; LAPRUNE_ENCODE_ROWS=4|16 (a forced MFMA kernel)
+// turns it off.  All are read at every call, so that one process can compare
+// them.
+static int encode_cus() {
+  DevInfo di;
+  return device_info(&di) == LAP_OK ? di.cu_count : 256;
+}
+static int encode_exact_rows(int N) {
+  const char* e = getenv("LAPRUNE_ENCODE_EXACT_ROWS");
+  const int r = e ? atoi(e) : 0;
+  if (r == 1 || r == 2) return r;
+  return N <= encode_cus() ? 1 : 2;
+}
+static bool encode_use_exact(int N, int D, int K) {
+  if (!(D == 64 || D == 128) || K > 256) return false;
+  const char* e = getenv("LAPRUNE_ENCODE_EXACT");
+  if (e && (e[0] == '0' || e[0] == '1') && e[1] == 0) return e[0] == '1';
+  const char* rows = getenv("LAPRUNE_ENCODE_ROWS");
+  if (rows && (atoi(rows) == 4 || atoi(rows) == 16)) return false;
+  if (!encode_impl_mfma()) return false;
+  return (int64_t)(N + 1) / 2 <= encode_cus();
+}
+
 // Shared checks and launch of both encode entry points.
 static int run_encode(const RowMap& rm, int N, int D, const float* codebooks, int M, int K,
                       const void* prep, size_t prep_bytes, float* resid_norm,
@@ -1293,6 +1553,21 @@ static int run_encode(const RowMap& rm, int N, int D, const float* codebooks, in
             "%s: codebooks must be 16-byte aligned", who);
   if (N == 0) return LAP_OK;
   hipStream_t st = as_stream(stream);
+  if (encode_use_exact(N, D, K)) {
+    const int R = encode_exact_rows(N);
+    dim3 g((N + R - 1) / R);
+#define LAP_ENCX(D_, R_)                                                                 \
+  hipLaunchKernelGGL((encode_exact_kernel<D_, R_>), g, dim3(256), 0, st, rm, N, codebooks, \
+                     p.c4, p.cn, M, K, resid_norm)
+    if (D == 64) {
+      if (R == 1) LAP_ENCX(64, 1); else LAP_ENCX(64, 2);
+    } else {
+      if (R == 1) LAP_ENCX(128, 1); else LAP_ENCX(128, 2);
+    }
+#undef LAP_ENCX
+    LAP_LAUNCH_CHECK("encode_exact_kernel");
+    return LAP_OK;
+  }
   if (K % 16 == 0 && encode_impl_mfma() && encode_use_tile(N, D, K)) {
     dim3 grid((N + kTileRows - 1) / kTileRows);
     const uint2* fr = reinterpret_cast<const uint2*>(p.frag);

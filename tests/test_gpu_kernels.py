@@ -453,10 +453,15 @@ def test_encode_c3_config(dev, K, orc, encode_rows):
     assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
 
 
-@pytest.fixture(params=["4", "16"])
+@pytest.fixture(params=["4", "16", "x1", "x2"])
 def encode_rows(request, monkeypatch):
-    """Runs a test on the 4-row and on the 16-row workgroup kernel (small
-    encodes take the 4-row one by default)."""
+    """Runs a test on the 4-row and the 16-row MFMA workgroup kernels and on
+    the exact-distance kernel at 1 and 2 rows per workgroup (flushes take
+    the exact kernel by default)."""
+    if request.param.startswith("x"):
+        monkeypatch.setenv("LAPRUNE_ENCODE_EXACT", "1")
+        monkeypatch.setenv("LAPRUNE_ENCODE_EXACT_ROWS", request.param[1:])
+        return int(request.param[1:])
     monkeypatch.setenv("LAPRUNE_ENCODE_ROWS", request.param)
     return int(request.param)
 

@@ -81,11 +81,15 @@ def test_score_residual_codebooks_real_codes(dev, K, orc, cb):
     print(f"stage-0 entries used: {int((used > 0).sum())} of 256")
 
 
-@pytest.mark.parametrize("which", ["4", "16"])
+@pytest.mark.parametrize("which", ["4", "16", "x1", "x2"])
 def test_encode_residual_codebooks(dev, K, orc, cb, which, monkeypatch):
     """C3-shaped keys (norms about 28) against residual codebooks, on the
-    4-row and the 16-row workgroup kernels."""
-    monkeypatch.setenv("LAPRUNE_ENCODE_ROWS", which)
+    4-row and the 16-row MFMA workgroup kernels and the exact-distance one."""
+    if which.startswith("x"):
+        monkeypatch.setenv("LAPRUNE_ENCODE_EXACT", "1")
+        monkeypatch.setenv("LAPRUNE_ENCODE_EXACT_ROWS", which[1:])
+    else:
+        monkeypatch.setenv("LAPRUNE_ENCODE_ROWS", which)
     x = c3_keys(45)
     codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
     torch.cuda.synchronize()
