@@ -158,6 +158,17 @@ int lap_aq_lut_direct(const void* q, const void* codebooks, int dtype,
                       int Q, int N, int M, int K, int D,
                       void* out, lap_stream_t stream);
 
+/* Replaces: AQLayerCodebookManager.reconstruct, laprune/llm/aq_kv.py:431-457.
+ * out[n] = sum over m ascending of codebooks[m][code(n, m)], elementwise fp32
+ * from 0 (the reference's recon += C_m[codes[:, m]] loop).
+ *   codebooks  [M][K][D] fp32 contiguous, 16-byte aligned, D % 4 == 0
+ *   codes      [N][M] rows codes_row_stride elements apart, dtype u8/i8/i64;
+ *              the low 8 bits are read as an unsigned code, clamped to K-1
+ *   out        [N][D] fp32 contiguous, 16-byte aligned */
+int lap_aq_reconstruct(const float* codebooks, int M, int K, int D, const void* codes,
+                       int codes_dtype, int64_t codes_row_stride, int N, float* out,
+                       lap_stream_t stream);
+
 /* ======================================================================= *
  * A3  Top-k selection                                                      *
  * Replaces: torch.topk(scores[..., cand_start:cand_end], k, sorted=False)

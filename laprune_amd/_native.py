@@ -89,6 +89,7 @@ SIGNATURES = {
                                 i32, i32, i32, vp, i64, i64, vp, vp, i32, i32, i32, i32, i32, i32,
                                 i64, i64, i64, i64, i64, i64, f32, vp, i32, vp, vp],
     "lap_encode_prep_size": [i32, i32, i32, psz],
+    "lap_aq_reconstruct": [vp, i32, i32, i32, vp, i32, i64, i32, vp, vp],
     "lap_encode_prepare": [vp, i32, i32, i32, vp, sz, vp],
     "lap_encode_greedy": [vp, i64, i32, i32, vp, i32, i32, vp, sz, vp, i64, vp, vp],
     "lap_encode_keys": [vp, i32, i64, i64, i64, i32, i32, i32, i32, i32, vp, i32, i32, vp, sz,

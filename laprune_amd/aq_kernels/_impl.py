@@ -455,6 +455,35 @@ def aq_encode_greedy(x: torch.Tensor, codebooks: torch.Tensor,
     return codes, rnorm
 
 
+def aq_reconstruct(codebooks: torch.Tensor, codes: torch.Tensor) -> torch.Tensor:
+    """Approximate keys fp32 [N, d] from codes [N, M]: the sum over m ascending
+    of ``codebooks[m, codes[:, m]]`` in fp32 from 0 (laprune/llm/aq_kv.py:431-457,
+    ``AQLayerCodebookManager.reconstruct``).  Codes may be uint8, int8 or
+    int64; the low 8 bits are read as the code, clamped to K - 1."""
+    N.require_cuda(codebooks, codes)
+    _check(codebooks.dim() == 3, "codebooks must be of shape [M, K, d]")
+    _check(codes.dim() == 2, "codes must be of shape [N, M]")
+    _check(codes.dtype in (torch.int64, torch.uint8, torch.int8),
+           "codes must be int64 (Long) or uint8 (Byte) or int8 (Char)")
+    _check(codes.device == codebooks.device, "codes and codebooks must be on the same device")
+    cb = codebooks.to(torch.float32).contiguous()
+    if cb.data_ptr() % 16:  # rows are read as 16-byte vectors
+        cb = cb.clone()
+    M, K, D = cb.shape
+    _check(codes.shape[1] == M, "codes M dimension must match codebooks")
+    _check(D % 4 == 0, "d must be a multiple of 4")
+    if codes.stride(1) != 1:
+        codes = codes.contiguous()
+    n = codes.shape[0]
+    out = torch.empty((n, D), dtype=torch.float32, device=codebooks.device)
+    if n == 0:
+        return out
+    with _device_guard(codebooks):
+        N.call("lap_aq_reconstruct", N.ptr(cb), M, K, D, N.ptr(codes), N.dtype_code(codes.dtype),
+               codes.stride(0), n, N.ptr(out), N.stream_of(codebooks))
+    return out
+
+
 _prep_lock = threading.Lock()
 _prep_cache: dict = {}
 

@@ -7,7 +7,10 @@
   grouped scorer (``lap_lut_score_grouped``, sequential fp32 over m, fp16
   out) for G <= 4, or by the per-head GQA scorer for larger groups.
 * ``approx_inner_product_multihead`` (:519-630): per-head codes, the same LUT
-  summed by the MHA scorer.
+  summed by the MHA scorer; ``approx_inner_product`` (:459-520) is its
+  one-query form with the head's group codebooks.
+* ``reconstruct`` (:431-457): approximate keys from codes
+  (``lap_aq_reconstruct``, fp32 sum over m in the reference's order).
 * ``encode_keys`` / ``encode_keys_batch`` (:347-428): the greedy fp32 encode
   (``lap_encode_greedy``), which is the reference's decode setting
   (``aq_encode_icm_iters_decode`` = 0, aq_evaluation.py:383-396).
@@ -187,6 +190,47 @@ class AQLayerCodebookManager:
         lut = self._lut(layer_idx, q, codes.shape[2])
         Q, M, K = lut.shape
         return _impl.aq_lut_gather_forward(lut.reshape(Q, M * K), codes.contiguous())
+
+    @torch.no_grad()
+    def reconstruct(self, layer_idx: int, head_idx: int, codes: torch.Tensor) -> torch.Tensor:
+        """Approximate keys [N, d] from codes [N, M] with the head's group
+        codebooks (aq_kv.py:431-457): fp32, the sum over m ascending of
+        C_m[codes[:, m]], as the reference's loop adds them."""
+        from .aq_kernels import _impl
+        cfg = self.layer_cfgs[layer_idx]
+        cb = self.codebooks(layer_idx, head_idx // cfg.heads_per_group)
+        codes = codes.to(cb.device)
+        if codes.dim() != 2 or codes.shape[1] != cb.shape[0]:
+            raise ValueError(f"codes must be [N, {cb.shape[0]}], got {tuple(codes.shape)}")
+        return _impl.aq_reconstruct(cb, codes)
+
+    @torch.no_grad()
+    def approx_inner_product(self, layer_idx: int, head_idx: int, q: torch.Tensor,
+                             codes: torch.Tensor) -> torch.Tensor:
+        """Scores [N] of one query q ([d] or [1, d]) against codes [N, M] with
+        the head's group codebooks (aq_kv.py:459-520): the LUT q . C_m[k] and
+        its gather-sum over m, under this path's contract (fp16 LUT from an
+        fp32 fmaf chain over d, sequential fp32 sum over m, fp16 out; the
+        reference sums an fp32 LUT in torch's order in the manager's dtype)."""
+        from .aq_kernels import _impl
+        cfg = self.layer_cfgs[layer_idx]
+        cb = self.codebooks(layer_idx, head_idx // cfg.heads_per_group)
+        if q.dim() == 2:
+            if q.shape[0] != 1:
+                raise ValueError(f"q must be [d] or [1, d], got {tuple(q.shape)}")
+            q = q[0]
+        M, K, d = cb.shape
+        if q.dim() != 1 or q.shape[0] != d:
+            raise ValueError(f"q must have {d} elements, got {tuple(q.shape)}")
+        codes = codes.to(cb.device)
+        if codes.dim() != 2 or codes.shape[1] != M:
+            raise ValueError(f"codes must be [N, {M}], got {tuple(codes.shape)}")
+        N.require_cuda(codes)
+        qv = q.to(cb.device)
+        if qv.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            qv = qv.float()
+        lut = _impl.aq_lut_build(qv[None, :].contiguous(), cb, 1, "hmk")  # fp16 [1, M, K]
+        return _impl.aq_lut_gather_forward(lut.reshape(1, M * K), codes[None].contiguous())[0]
 
     def fit_layer(self, *args, **kwargs):
         raise NotImplementedError("codebook training is an offline path (the reference's "

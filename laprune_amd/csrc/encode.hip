@@ -1166,6 +1166,35 @@ __global__ __launch_bounds__(256) void encode_exact_kernel(
     rnorm[row0 + tid] = sqrtf(s.rn[tid]);
 }
 
+// ------------------------------------------------ reconstruction
+// recon[n] = sum over m ascending of C[m][code(n, m)], elementwise fp32 from
+// 0 (laprune/llm/aq_kv.py:431-457).  A thread owns four consecutive
+// elements of one row; the codebook rows it gathers are 16-byte vectors.
+template <typename CT>
+__global__ __launch_bounds__(256) void aq_reconstruct_kernel(
+    const float* __restrict__ cb, int M, int K, int D, const CT* __restrict__ codes,
+    int64_t cs, int N, float* __restrict__ out) {
+  const int D4 = D / 4;
+  const int64_t total = (int64_t)N * D4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t n = i / D4;
+    const int q = (int)(i - n * D4);
+    const CT* cp = codes + n * cs;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int m = 0; m < M; ++m) {
+      // the low 8 bits as an unsigned code, clamped to the last entry
+      const int c = min((int)(uint8_t)(cp[m] & (CT)0xff), K - 1);
+      const float4 v = *reinterpret_cast<const float4*>(cb + ((int64_t)m * K + c) * D + 4 * q);
+      acc.x = acc.x + v.x;
+      acc.y = acc.y + v.y;
+      acc.z = acc.z + v.z;
+      acc.w = acc.w + v.w;
+    }
+    *reinterpret_cast<float4*>(out + n * D + 4 * q) = acc;
+  }
+}
+
 // ------------------------------------------------ large launches (prefill)
 // The same stage as enc_stage for 64 rows per workgroup.  A 16-row workgroup
 // holds its stage fragments (64 KiB at K = 256, D = 128) in registers, twice
@@ -1674,4 +1703,39 @@ extern "C" int lap_encode_keys_ranges(const void* keys, int key_dtype, int64_t k
                   max_len, Hkv, 0, ranges, t_cap};
   return run_encode(rm, (int)n, D, codebooks, M, K, prep, prep_bytes, nullptr, stream,
                     "lap_encode_keys_ranges");
+}
+
+extern "C" int lap_aq_reconstruct(const float* codebooks, int M, int K, int D, const void* codes,
+                                  int codes_dtype, int64_t codes_row_stride, int N, float* out,
+                                  lap_stream_t stream) {
+  clear_error();
+  LAP_CHECK(codebooks && codes && out, "lap_aq_reconstruct: null pointer");
+  LAP_CHECK(M > 0 && K > 0 && D > 0 && N >= 0, "lap_aq_reconstruct: bad sizes");
+  LAP_CHECK(D % 4 == 0, "lap_aq_reconstruct: D=%d must be a multiple of 4", D);
+  LAP_CHECK(codes_row_stride >= M, "lap_aq_reconstruct: codes row stride %lld < M=%d",
+            (long long)codes_row_stride, M);
+  LAP_CHECK(codes_dtype == LAP_DTYPE_U8 || codes_dtype == LAP_DTYPE_I8 ||
+                codes_dtype == LAP_DTYPE_I64,
+            "codes must be int64 (Long) or uint8 (Byte) or int8 (Char)");
+  LAP_CHECK((reinterpret_cast<uintptr_t>(codebooks) & 15) == 0 &&
+                (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+            "lap_aq_reconstruct: codebooks and out must be 16-byte aligned");
+  if (N == 0) return LAP_OK;
+  DevInfo di;
+  int s = device_info(&di);
+  if (s != LAP_OK) return s;
+  const int64_t total = (int64_t)N * (D / 4);
+  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 16LL * di.cu_count);
+  hipStream_t st = as_stream(stream);
+  if (codes_dtype == LAP_DTYPE_U8)
+    hipLaunchKernelGGL(aq_reconstruct_kernel<uint8_t>, dim3(grid), dim3(256), 0, st, codebooks, M,
+                       K, D, static_cast<const uint8_t*>(codes), codes_row_stride, N, out);
+  else if (codes_dtype == LAP_DTYPE_I8)
+    hipLaunchKernelGGL(aq_reconstruct_kernel<int8_t>, dim3(grid), dim3(256), 0, st, codebooks, M,
+                       K, D, static_cast<const int8_t*>(codes), codes_row_stride, N, out);
+  else
+    hipLaunchKernelGGL(aq_reconstruct_kernel<int64_t>, dim3(grid), dim3(256), 0, st, codebooks,
+                       M, K, D, static_cast<const int64_t*>(codes), codes_row_stride, N, out);
+  LAP_LAUNCH_CHECK("aq_reconstruct_kernel");
+  return LAP_OK;
 }

@@ -157,6 +157,25 @@ void orc_score_mha(const void* lut, int lut_f32, const int64_t* codes, int Q, in
     }
 }
 
+/* laprune/llm/aq_kv.py:431-457 (AQLayerCodebookManager.reconstruct):
+ * recon = zeros; for m ascending: recon += C[m][codes[:, m]], elementwise in
+ * fp32.  codes [N][M] as int64 (any source dtype); the low 8 bits are the
+ * code, clamped to K-1 (the reference indexes with the code directly: a code
+ * >= K is an indexing error there). */
+void orc_reconstruct(const float* cb, const int64_t* codes, int N, int M, int K, int D,
+                     float* out) {
+  for (int n = 0; n < N; ++n) {
+    float* o = out + (int64_t)n * D;
+    for (int d = 0; d < D; ++d) o[d] = 0.f;
+    for (int m = 0; m < M; ++m) {
+      int c = (int)(uint8_t)(codes[(int64_t)n * M + m] & 0xff);
+      if (c >= K) c = K - 1;
+      const float* row = cb + ((int64_t)m * K + c) * D;
+      for (int d = 0; d < D; ++d) o[d] = o[d] + row[d];
+    }
+  }
+}
+
 /* aq_kernels/aq_lut.cu:37-149 direct scoring.  f32: one fmaf chain over
  * (m, d); f16 (is_f16 != 0, q/cb given as fp16 bits): per pair
  * p = fp16(q*c) lanewise, acc += (p0 + p1).  Codes >= K are skipped. */

@@ -23,6 +23,10 @@ What pins each function (tests/test_oracle_pins.py):
                  identity, laprune/llm/aq_kv.py:695-699).
   topk           numpy lexsort on (-key, index); closed-form budgets
                  (n=131008 -> 2621, n=8128 -> 163); all-equal rows; k >= n.
+  reconstruct    numpy float32 sequential sum (bit-exact); a crafted case
+                 where the m order changes the fp32 result; one-hot
+                 codebooks give the code pattern; float64 sum within the
+                 fp32 bound.
   encode         exact-rational dot16 on small shapes; float64 argmin with
                  teacher forcing (codes equal except documented near-ties);
                  constructed codebooks (exact recovery, zero input chain).
@@ -64,6 +68,7 @@ def lib():
         L.orc_score_gqa.argtypes = [vp, vp, i64, i64, i32, i32, i32, i32, i32, i32, i32, vp, i32, vp]
         L.orc_score_mha.argtypes = [vp, i32, vp, i32, i32, i32, i32, vp]
         L.orc_aq_direct.argtypes = [vp, vp, i32, vp, i32, i32, i32, i32, i32, vp]
+        L.orc_reconstruct.argtypes = [vp, vp, i32, i32, i32, i32, vp]
         L.orc_topk.argtypes = [vp, i64, i32, i32, i32, i32, i32, i32, vp]
         L.orc_topk.restype = C.c_int
         L.orc_dot16.argtypes = [vp, vp, i32]
@@ -167,6 +172,18 @@ def score_mha(lut: np.ndarray, codes: np.ndarray, f32: bool) -> np.ndarray:
     K = lut.shape[1] // M
     out = np.empty((Q, n), dtype=np.float32 if f32 else np.uint16)
     lib().orc_score_mha(_p(lut), 1 if f32 else 0, _p(codes64), Q, n, M, K, _p(out))
+    return out
+
+
+def reconstruct(cb: np.ndarray, codes: np.ndarray) -> np.ndarray:
+    """float32 [N, D]: sum over m ascending of cb[m, codes[:, m]] (fp32, from 0)."""
+    cb = _c(cb, np.float32)
+    codes64 = _c(codes.astype(np.int64), np.int64)
+    n, M = codes64.shape
+    Mc, K, D = cb.shape
+    assert Mc == M
+    out = np.empty((n, D), dtype=np.float32)
+    lib().orc_reconstruct(_p(cb), _p(codes64), n, M, K, D, _p(out))
     return out
 
 

@@ -213,6 +213,59 @@ def test_aq_lut_direct(dev, K, orc, dt):
         assert np.array_equal(_np_u16(out), want)
 
 
+# ---------------------------------------------------------- reconstruction
+
+@pytest.mark.parametrize("code_dt", [torch.uint8, torch.int8, torch.int64])
+@pytest.mark.parametrize("Kc,D", [(256, 128), (100, 64), (37, 4)])
+def test_aq_reconstruct(dev, K, orc, code_dt, Kc, D):
+    """Approximate keys from codes (aq_kv.py:431-457) bit for bit against the
+    oracle's ascending-m fp32 sum: every code dtype (low 8 bits, clamped to
+    K - 1), rows a strided view (the M codes of each row inside a wider row)."""
+    from laprune_amd.aq_kernels import _impl
+    g = _gen(60 + Kc)
+    M, n = 32, 1000
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    wide = torch.randint(-300 if code_dt == torch.int64 else 0, 600 if code_dt == torch.int64
+                         else 256, (n, M + 5), generator=g, dtype=torch.int64).to(code_dt)
+    codes = wide[:, 2:2 + M]  # row stride M + 5
+    out = _impl.aq_reconstruct(cb.to(dev), codes.to(dev))
+    torch.cuda.synchronize()
+    want = orc.reconstruct(cb.numpy(), codes.numpy().astype(np.int64))
+    assert out.shape == (n, D) and out.dtype == torch.float32
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_manager_reconstruct_and_inner_product(dev, K, orc):
+    """AQLayerCodebookManager.reconstruct / approx_inner_product pick the
+    head's group codebooks (head // heads_per_group) and match the oracle:
+    reconstruction bit-exact; inner products bit-exact to the fp16 LUT and
+    sequential fp32 sum of this path, and close to q . reconstruct(codes)."""
+    from laprune_amd.aq_kv import AQLayerCodebookManager, AQLayerConfig
+    g = _gen(70)
+    M, Kc, D, n = 32, 256, 128, 3000
+    mgr = AQLayerCodebookManager({5: AQLayerConfig(M=M, K=Kc, d=D, heads_per_group=2,
+                                                   num_heads=8)}, device=dev)
+    cbs = [torch.randn(M, Kc, D, generator=g) * 0.05 for _ in range(4)]
+    for gi, cb in enumerate(cbs):
+        mgr.set_codebooks(5, gi, cb)
+    codes = torch.randint(0, Kc, (n, M), generator=g, dtype=torch.uint8)
+    q = torch.randn(D, generator=g)
+    for head in (0, 3, 7):
+        cb = cbs[head // 2]
+        rec = mgr.reconstruct(5, head, codes.to(dev))
+        want = orc.reconstruct(cb.numpy(), codes.numpy())
+        assert np.array_equal(rec.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        s = mgr.approx_inner_product(5, head, q.to(dev)[None, :], codes)
+        torch.cuda.synchronize()
+        lut = orc.lut_build(q.numpy()[None, :], cb.numpy())  # fp16 bits [1, M, K]
+        want_s = orc.score_mha(lut.reshape(1, M * Kc), codes.numpy()[None].astype(np.int64),
+                               False)[0]
+        assert s.shape == (n,) and np.array_equal(_np_u16(s), want_s)
+        exact = want.astype(np.float64) @ q.numpy().astype(np.float64)
+        got = s.float().cpu().numpy()
+        assert np.max(np.abs(got - exact)) < 2e-2 * max(1.0, float(np.max(np.abs(exact))))
+
+
 # ---------------------------------------------------------------- A3 top-k
 
 @pytest.mark.parametrize("group,key_dt", [(1, torch.float16), (4, torch.float16),

@@ -213,6 +213,60 @@ def test_score_mha_clamp_and_signed_codes():
             assert got[q, j] == acc
 
 
+# ------------------------------------------------------- reconstruction
+
+def test_reconstruct_vs_numpy_sequential_and_clamp():
+    """Elementwise fp32 sum over m ascending from 0 (aq_kv.py:454-456),
+    restated with numpy float32 adds; codes read by their low 8 bits and
+    clamped to K - 1."""
+    M, K, D, n = 6, 40, 12, 70
+    cb = RNG.standard_normal((M, K, D)).astype(np.float32)
+    codes = RNG.integers(-300, 600, (n, M)).astype(np.int64)
+    got = orc.reconstruct(cb, codes)
+    want = np.zeros((n, D), dtype=np.float32)
+    for m in range(M):
+        c = np.minimum(codes[:, m] & 0xFF, K - 1)
+        want = (want + cb[m, c]).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_reconstruct_order_is_pinned():
+    """1 + 2^-24 + 2^-24 in fp32 depends on the order: ascending m gives
+    (1 + 2^-24) + 2^-24 = 1 (each add ties to even), the reverse order gives
+    1 + 2^-23.  The oracle must give the ascending-m value."""
+    M, K, D = 3, 2, 4
+    cb = np.zeros((M, K, D), dtype=np.float32)
+    cb[0, 1] = 1.0
+    cb[1, 1] = 2.0 ** -24
+    cb[2, 1] = 2.0 ** -24
+    codes = np.ones((1, M), dtype=np.uint8)
+    got = orc.reconstruct(cb, codes)
+    assert np.all(got == np.float32(1.0))
+    rev = np.float32(np.float32(np.float32(2.0 ** -24) + np.float32(2.0 ** -24)) + np.float32(1.0))
+    assert rev == np.float32(1.0 + 2.0 ** -23)  # the order matters for this input
+
+
+def test_reconstruct_one_hot_and_float64_bound():
+    """Codebook m holding 2^m on coordinate m at entry 1 (zero elsewhere) spells
+    the code pattern exactly; random codebooks stay within the fp32 bound of
+    the float64 sum."""
+    M, K, D = 8, 4, 8
+    cb = np.zeros((M, K, D), dtype=np.float32)
+    for m in range(M):
+        cb[m, 1, m] = 2.0 ** m
+    codes = RNG.integers(0, K, (200, M)).astype(np.uint8)
+    got = orc.reconstruct(cb, codes)
+    want = (codes == 1).astype(np.float32) * (2.0 ** np.arange(M, dtype=np.float32))[None, :]
+    assert np.array_equal(got, want)
+    cb = RNG.standard_normal((32, 256, 16)).astype(np.float32)
+    codes = RNG.integers(0, 256, (300, 32)).astype(np.uint8)
+    got = orc.reconstruct(cb, codes).astype(np.float64)
+    rows = cb[np.arange(32)[None, :], codes]  # [n, M, D]
+    exact = rows.astype(np.float64).sum(axis=1)
+    bound = 32 * 2.0 ** -24 * np.abs(rows).astype(np.float64).sum(axis=1)
+    assert np.all(np.abs(got - exact) <= bound)
+
+
 def test_aq_direct_f32_exact_and_f16_restatement():
     q = RNG.standard_normal((2, 8)).astype(np.float32)
     cb = (RNG.standard_normal((3, 6, 8)) * 0.5).astype(np.float32)
