@@ -711,6 +711,23 @@ def main():
                 floors["launch_us"] + SCORE_TABLE_FILL_US
                 + max(floors["hbm_floor_us"], SCORE_LDS_LOOKUPS_US))
 
+    # ---- C3 encode: one flush of 512 post-RoPE key rows (HIP events).  Timed
+    # before the dense and SDPA legs: right after them the same launches
+    # measured 66-67 us per flush, here 64-65 us (63 us in a process of its own)
+    log("timing the C3 encode")
+    for _ in range(3):
+        AK.aq_encode_greedy(enc_x, cb, enc_prep)
+    torch.cuda.synchronize()
+    n_enc = max(50, args.steps // 10)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(n_enc):
+        AK.aq_encode_greedy(enc_x, cb, enc_prep)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    enc_us = ev0.elapsed_time(ev1) * 1e3 / n_enc
+
     # ---- timed region 1: K full sparse decode steps, issued eagerly
     for i in range(args.warmup):
         sparse_step(i)
@@ -757,20 +774,6 @@ def main():
     # ---- stock framework decode: torch SDPA (fused backends only)
     sdpa_s = sdpa_decode_seconds(args, kv_sets, q_sets)
 
-    # ---- C3 encode: one flush of 512 post-RoPE key rows (HIP events)
-    log("timing the C3 encode")
-    for _ in range(3):
-        AK.aq_encode_greedy(enc_x, cb, enc_prep)
-    torch.cuda.synchronize()
-    n_enc = max(50, args.steps // 10)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(n_enc):
-        AK.aq_encode_greedy(enc_x, cb, enc_prep)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    enc_us = ev0.elapsed_time(ev1) * 1e3 / n_enc
 
     # correctness guard: the selected index sets are valid and the right size
     sparse_step(0)
