@@ -547,6 +547,21 @@ def test_encode_bit_exact_entry_counts(dev, K, orc, Kc, D, encode_rows):
     assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
 
 
+def test_encode_more_stages_than_staged_codes(dev, K, orc, encode_rows):
+    """M = 80 stages: codes of stages 64 and up are stored as they are
+    chosen, the first 64 staged in LDS and stored at the end."""
+    g = _gen(125)
+    M, Kc, D, N = 80, 32, 64, 45
+    x = torch.randn(N, D, generator=g) * 2.0
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    codes, rn = K.aq_encode_greedy(x.to(dev), cb.to(dev))
+    torch.cuda.synchronize()
+    want_c, want_r = orc.encode(x.numpy(), cb.numpy())
+    assert codes.shape == (N, M)
+    assert np.array_equal(codes.cpu().numpy(), want_c)
+    assert np.array_equal(rn.cpu().numpy().view(np.uint32), want_r.view(np.uint32))
+
+
 def test_encode_ties_and_near_ties(dev, K, orc, encode_rows):
     """Duplicate entries (exact ties: the lowest index must win) and entries a
     few ulps apart, far inside the bf16 coarse error, so the exact recheck
