@@ -235,6 +235,21 @@ def test_aq_reconstruct(dev, K, orc, code_dt, Kc, D):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+def test_aq_reconstruct_grid_stride(dev, K, orc):
+    """40003 rows at D = 128: more quads than one pass of the grid, so
+    threads loop; first and last 128 rows and 512 random rows checked."""
+    from laprune_amd.aq_kernels import _impl
+    g = _gen(66)
+    M, Kc, D, n = 32, 256, 128, 40003
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    codes = torch.randint(0, Kc, (n, M), generator=g, dtype=torch.int64).to(torch.uint8)
+    out = _impl.aq_reconstruct(cb.to(dev), codes.to(dev)).cpu().numpy()
+    pick = torch.randperm(n - 256, generator=g)[:512].numpy() + 128
+    rows = np.unique(np.concatenate([np.arange(128), np.arange(n - 128, n), pick]))
+    want = orc.reconstruct(cb.numpy(), codes.numpy()[rows])
+    assert np.array_equal(out[rows].view(np.uint32), want.view(np.uint32))
+
+
 def test_manager_reconstruct_and_inner_product(dev, K, orc):
     """AQLayerCodebookManager.reconstruct / approx_inner_product pick the
     head's group codebooks (head // heads_per_group) and match the oracle:
