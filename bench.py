@@ -63,6 +63,14 @@ serve the step from cache.
                  group + 4 sink + 64 local, the newest < 64 keys of each
                  sequence not yet encoded; sparse step (per-sequence plans) vs
                  the dense decode of each sequence over its own length.
+``e2e``          whole-model greedy decode of configs[3] (C4: batch 1, 131072
+                 context, top-2048) and configs[4] (C5), LAPrune layers 2-31
+                 against the same model decoding densely: tok/s = batch x
+                 (decode - warm-up tokens) / seconds, the reference's decode
+                 benchmark formula (benchmarks/decode.py:102-106), on a
+                 random-init bf16 Llama-3.1-8B geometry.  Run first, by
+                 ``python -m laprune_amd.e2e`` in a child process, before this
+                 process touches the GPU (``--no-e2e`` skips it).
 """
 from __future__ import annotations
 
@@ -117,6 +125,8 @@ def parse():
                     help="skip the per-query-head (reference selection) C2 leg")
     ap.add_argument("--only-ragged", action="store_true",
                     help="run only the C5 ragged-batch leg (for profiling); prints its JSON")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the whole-model C4 / C5 decode leg")
     ap.add_argument("--counters", action="store_true",
                     help="counter-collection pass: eager scorer launches over the rotating "
                          "code sets, then a 256 MiB copy-like kernel (fp32 negate) that "
@@ -514,6 +524,47 @@ def score_floors(score_only, floor_empty, floor_stream, stream, reps: int) -> di
                      "the code bytes at the 8 TB/s peak")}
 
 
+E2E_TIMEOUT_S = 420  # one config, both methods (about 40 s each on MI355X)
+
+
+def e2e_leg() -> dict:
+    """Whole-model decode of C4 and C5 (laprune_amd/e2e.py), each config in a
+    child process of its own, started while this process has not touched
+    the GPU yet; the child's progress goes to stderr, its JSON line to a
+    pipe.  A failed or timed-out config is reported, not fatal."""
+    import subprocess
+    out = {"command": "python -m laprune_amd.e2e --config {c4,c5} --method both",
+           "launch": "one captured graph replayed per decode step",
+           "model": "Llama-3.1-8B geometry, 32 layers, random bf16 N(0, 0.02) weights; "
+                    "LAPrune on layers 2-31, dense on 0-1",
+           "formula": "batch x (decode - warmup tokens) / seconds (benchmarks/decode.py:102-106)"}
+    for cfg in ("c4", "c5"):
+        log(f"e2e {cfg}: child process")
+        try:
+            res = subprocess.run([sys.executable, "-m", "laprune_amd.e2e", "--config", cfg,
+                                  "--method", "both"], cwd=str(ROOT), stdout=subprocess.PIPE,
+                                 text=True, timeout=E2E_TIMEOUT_S)
+        except subprocess.TimeoutExpired:
+            out[cfg] = {"error": f"timed out after {E2E_TIMEOUT_S} s"}
+            continue
+        lines = [l for l in res.stdout.splitlines() if l.startswith("{")]
+        if res.returncode != 0 or not lines:
+            out[cfg] = {"error": f"exit status {res.returncode}"}
+            continue
+        d = json.loads(lines[-1])
+        lp, dn = d["results"]["laprune"], d["results"]["dense"]
+        out[cfg] = {"batch": d["batch"], "context_lengths": d["context_lengths"],
+                    "topk": d["topk"], "decode_tokens": d["decode_tokens"],
+                    "warmup_tokens": d["warmup_tokens"],
+                    "laprune_tokens_per_s": lp["tokens_per_s"],
+                    "dense_tokens_per_s": dn["tokens_per_s"],
+                    "speedup_vs_dense": d.get("speedup_vs_dense"),
+                    "laprune_ms_per_step": lp["ms_per_step"], "dense_ms_per_step": dn["ms_per_step"],
+                    "prefill_s": {"laprune": lp["prefill_s"], "dense": dn["prefill_s"]},
+                    "finite_logits": bool(lp["finite_logits"] and dn["finite_logits"])}
+    return out
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -522,6 +573,8 @@ def main():
               f"in this build (asked for --gpus {args.gpus}, WORLD_SIZE={world}).",
               file=sys.stderr)
         sys.exit(2)
+    # before anything here initialises the GPU: the child decodes on it alone
+    e2e = None if (args.no_e2e or args.only_ragged or args.counters) else e2e_leg()
     import torch
     from laprune_amd import _native as N
     from laprune_amd.retrieval import DenseDecoder, RetrievalConfig, SparseDecoder
@@ -850,6 +903,8 @@ def main():
                                                       dense_s, dense_graph_s)
     if not args.no_ragged:
         result["ragged"] = ragged_leg(args, dev, cb)
+    if e2e is not None:
+        result["e2e"] = e2e
     if not args.no_cpu_baseline:
         log("CPU baseline")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
