@@ -396,6 +396,69 @@ __global__ __launch_bounds__(kThreads) void lut_mfma_kernel(
   }
 }
 
+// The 64 x 64 form over `tpw` consecutive row tiles of one head tile: the
+// workgroup's q fragments stay in registers, the codebook tile is staged in
+// one of two LDS buffers, and the next tile's rows are requested from global
+// memory before the current tile's MFMA chain, so their latency runs under
+// it.  One barrier per tile: after it, the buffer just read may be written.
+// (With every tile its own workgroup, the four workgroups a CU holds load,
+// compute and write in step, and nothing overlaps the loads.)
+template <int QDT, int CDT, int D>
+__global__ __launch_bounds__(kThreads) void lut_mfma_pipe_kernel(
+    const void* __restrict__ q, int64_t q_row_stride,
+    const void* __restrict__ cb, int Hq, int MK, int G, int layout,
+    uint16_t* __restrict__ out, int head_tiles, int tpw) {
+  constexpr int HT = 4, RTW = 4, ROWS = mfma_rows(HT, RTW), HEADS = 16 * HT, P = c_pitch(D);
+  static_assert(ROWS == 64 && HEADS == 64, "64 x 64 tiles");
+  extern __shared__ __attribute__((aligned(16))) float mfma_smem[];
+  float* const buf0 = mfma_smem;
+  float* const buf1 = mfma_smem + ROWS * P;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const TileId ti = tile_of(blockIdx.x, gridDim.x, head_tiles, tpw);
+  const int n_rt = (MK + ROWS - 1) / ROWS;
+  const int n_t = min(tpw, n_rt - ti.row_tile);
+  if (n_t <= 0) return;
+  const int head0 = ti.head_tile * HEADS;
+  MfmaStage<D, ROWS> sc;
+  MfmaStage<D, HEADS> sq;
+  sc.template load<CDT>(cb, D, ti.row_tile * ROWS, MK - 1, tid);
+  sq.template load<QDT>(q, q_row_stride, head0, Hq - 1, tid);
+  sq.store(buf1, tid);
+  sc.store(buf0, tid);
+  __syncthreads();
+  // wave w takes head tile w; every wave covers the tile's four row tiles
+  const int hl = lane & 15, kj = lane >> 4;
+  float4 a[D / 16];
+  {
+    const float* qp = buf1 + (wave * 16 + hl) * P + kj * (D / 4);
+#pragma unroll
+    for (int jb = 0; jb < D / 16; ++jb) a[jb] = *reinterpret_cast<const float4*>(qp + 4 * jb);
+  }
+  __syncthreads();  // buf1 (the q tile) is read: it may take tile 1
+  const int hA = head0 + wave * 16 + 4 * kj;
+  for (int t = 0; t < n_t; ++t) {
+    const float* cur = (t & 1) ? buf1 : buf0;
+    float* nxt = (t & 1) ? buf0 : buf1;
+    const int row0 = (ti.row_tile + t) * ROWS;
+    const bool more = t + 1 < n_t;
+    if (more) sc.template load<CDT>(cb, D, row0 + ROWS, MK - 1, tid);
+    f32x4_t acc[RTW];
+#pragma unroll
+    for (int i = 0; i < RTW; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    mfma_tile_chain<D, RTW>(a, cur + hl * P + kj * (D / 4), acc);
+#pragma unroll
+    for (int i = 0; i < RTW; ++i) {
+      const int row = row0 + i * 16 + hl;
+      if (row >= MK) continue;
+      const float r4[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+      write_row<4>(r4, hA, row, Hq, MK, G, layout, out);
+    }
+    // nxt was last read at tile t - 1 (or held q), before the previous barrier
+    if (more) sc.store(nxt, tid);
+    __syncthreads();
+  }
+}
+
 template <int QDT, int CDT, int HPT>
 __global__ __launch_bounds__(kThreads) void lut_tile_kernel(
     const void* __restrict__ q, int64_t q_row_stride,
@@ -485,11 +548,29 @@ constexpr size_t lut_mfma_smem_bytes(int D, int HT, int RTW) {
   return (size_t)rows * c_pitch(D) * sizeof(float);
 }
 
+// Row tiles per workgroup of the pipelined 64 x 64 form: enough workgroups
+// for two per CU (each holds two 33 KiB tile buffers); 1 keeps one tile per
+// workgroup (lut_mfma_kernel).  LAPRUNE_LUT_MFMA_TPW overrides it (read at
+// every call, for measurements).
+static int lut_mfma_tpw(int64_t tiles, int cus) {
+  const char* e = getenv("LAPRUNE_LUT_MFMA_TPW");
+  if (e && atoi(e) > 0) return atoi(e);
+  const int64_t t = tiles / (2 * (int64_t)cus);
+  return t < 1 ? 1 : (int)std::min<int64_t>(t, 8);
+}
+
 template <int QDT, int CDT, int D>
 void launch_lut_mfma_d(const void* q, int64_t qs, const void* cb, int Hq, int MK, int G,
                        int layout, uint16_t* out, int cus, hipStream_t st) {
   const int64_t big_tiles = (int64_t)((MK + 63) / 64) * ((Hq + 63) / 64);
-  if (Hq >= 64 && big_tiles >= 2 * cus) {
+  const int tpw = lut_mfma_tpw(big_tiles, cus);
+  if (Hq >= 64 && big_tiles >= 2 * cus && tpw > 1) {
+    const int htl = (Hq + 63) / 64;
+    const int units = (int)(((MK + 63) / 64 + tpw - 1) / tpw) * htl;
+    hipLaunchKernelGGL((lut_mfma_pipe_kernel<QDT, CDT, D>), dim3((unsigned)units),
+                       dim3(kThreads), 2 * lut_mfma_smem_bytes(D, 4, 4), st, q, qs, cb, Hq, MK,
+                       G, layout, out, htl, tpw);
+  } else if (Hq >= 64 && big_tiles >= 2 * cus) {
     const int htl = (Hq + 63) / 64;
     const dim3 g((unsigned)(((MK + 63) / 64) * htl));
     hipLaunchKernelGGL((lut_mfma_kernel<QDT, CDT, 4, 4, D>), g, dim3(kThreads),

@@ -82,6 +82,34 @@ def test_lut_build_tiles(dev, K, orc, Hq, D, M, Kc, G, layout, cdt, lut_impl):
     assert np.array_equal(_np_u16(lut), want)
 
 
+@pytest.mark.parametrize("tpw", [2, 3, 5])
+@pytest.mark.parametrize("Hq,D,M,Kc,layout,cdt", [
+    (512, 128, 32, 256, "gmkg", "f32"),  # C5's LUT
+    (448, 128, 40, 206, "gmkg", "f32"),  # partial last row tile, groups cut short
+    (520, 128, 32, 256, "hmk", "f16"),   # partial head tile, reference layout, fp16 codebooks
+    (200, 64, 32, 256, "gmkg", "f32"),   # D = 64
+])
+def test_lut_build_pipelined(dev, K, orc, monkeypatch, Hq, D, M, Kc, layout, cdt, tpw):
+    """The 64 x 64 MFMA form over several row tiles per workgroup (the next
+    tile's rows fetched during the current tile's chain): bit-exact at forced
+    tiles per workgroup, including groups that run past the last row tile."""
+    monkeypatch.setenv("LAPRUNE_LUT_MFMA_TPW", str(tpw))
+    g = _gen(11 + Hq + D + tpw)
+    q = torch.randn(Hq, D, generator=g).bfloat16()
+    cb = torch.randn(M, Kc, D, generator=g) * 0.05
+    cb_dev = cb.to(dev)
+    if cdt == "f16":
+        cb_dev = cb_dev.half()
+        cb = cb.half().float()
+    print(f"lut pipelined: Hq={Hq} D={D} M={M} K={Kc} tpw={tpw}", flush=True)
+    lut = K.aq_lut_build(q.to(dev), cb_dev, G=4, layout=layout)
+    torch.cuda.synchronize()
+    want = orc.lut_build(q.float().numpy(), cb.numpy())
+    if layout == "gmkg":
+        want = orc.lut_to_gmkg(want, 4)
+    assert np.array_equal(_np_u16(lut), want)
+
+
 @pytest.mark.parametrize("cdt", [torch.float32, torch.float16])
 def test_lut_build_wide_range(dev, K, orc, lut_impl, cdt):
     """Operands spread over many binades, exact zeros, signed zeros and
