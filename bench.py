@@ -49,6 +49,10 @@ serve the step from cache.
                  post-RoPE keys (8 KV heads x 64 tokens = 512 rows, 32x256
                  codebooks), exact fp32 distances to every entry per stage,
                  next to the reference's fp32 greedy path on the host cores.
+``prefill_encode`` one layer's prefill encode at C4 (8 KV heads x 131072
+                 post-RoPE key rows): the large-N kernel, bf16 MFMA distances
+                 to every entry (the coarse pass) and an exact fp32 recheck;
+                 ``search_tflops`` counts the coarse pass's MFMA flops.
 ``reference_mode`` the same C2 step with the reference's own selection: top-k
                  per query head on bf16-cast scores, budget 131004 -
                  int(0.98 * 131004) = 2621, each head attending over its own
@@ -104,6 +108,10 @@ SCORE_TRIAL_LAUNCHES = 108  # scorer launches per trial (nine replays of 12)
 CALIB_BYTES = 256 << 20   # copy-like calibration kernel: bytes read (= bytes written)
 ENC_TOKENS, ENC_POS0, ROPE_THETA = 64, 131008, 500000.0
 ENC_FLOP = 2 * HKV * ENC_TOKENS * M * K * D  # 1,073,741,824 dot-product flops per flush
+# one layer's prefill encode at C4 (8 KV heads x 131072 prompt tokens): the
+# large-N kernel's bf16 MFMA coarse search over every entry of every stage
+PREFILL_ROWS = HKV * 131072
+PREFILL_FLOP = 2 * PREFILL_ROWS * M * K * D  # 2,199,023,255,552
 RAG_B, RAG_T0, RAG_T1, RAG_TOPK, RAG_SETS = 16, 16384, 32768, 1024, 2
 
 
@@ -219,6 +227,24 @@ def c3_keys(g, dev):
     sin = torch.cat([ang.sin(), ang.sin()], -1).float()
     rot = torch.cat([-k[..., D // 2:], k[..., :D // 2]], -1)
     return (k * cos + rot * sin).reshape(HKV * ENC_TOKENS, D).to(dev)
+
+
+def prefill_keys(dev):
+    """One layer's prefill keys at C4: pre-RoPE keys bf16 N(0,1) x per-channel
+    U(0.5, 4), RoPE (as c3_keys) at positions 0..131071, [8 * 131072, 128] fp32
+    rows, generated on the device (seeded)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    n = PREFILL_ROWS // HKV
+    k = (torch.randn(HKV, n, D, generator=g, device=dev) *
+         (torch.rand(D, generator=g, device=dev) * 3.5 + 0.5)).bfloat16().float()
+    inv = ROPE_THETA ** (-torch.arange(0, D, 2, dtype=torch.float64, device=dev) / D)
+    ang = torch.arange(n, dtype=torch.float64, device=dev)[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).float()
+    sin = torch.cat([ang.sin(), ang.sin()], -1).float()
+    rot = torch.cat([-k[..., D // 2:], k[..., :D // 2]], -1)
+    return (k * cos + rot * sin).reshape(PREFILL_ROWS, D)
 
 
 def encode_cpu_baseline(x, cb, seconds: float) -> dict:
@@ -653,6 +679,10 @@ def main():
         del a, b
         for _ in range(4):
             AK.aq_encode_greedy(enc_x, cb, enc_prep)
+        pf_x = prefill_keys(dev)
+        for _ in range(2):
+            AK.aq_encode_greedy(pf_x, cb, enc_prep)
+        del pf_x
         # the one-launch steps: C2 group selection, C2 per-head selection
         # (the reference's rule, k = 2621) and one C5 ragged layer
         for i in range(N_CODE_SETS):
@@ -781,6 +811,20 @@ def main():
     torch.cuda.synchronize()
     enc_us = ev0.elapsed_time(ev1) * 1e3 / n_enc
 
+    # ---- N3: one layer's prefill encode (the large-N kernel), HIP events
+    log("timing the prefill encode")
+    pf_x = prefill_keys(dev)
+    AK.aq_encode_greedy(pf_x, cb, enc_prep)
+    torch.cuda.synchronize()
+    n_pf = 3
+    ev0.record(stream)
+    for _ in range(n_pf):
+        AK.aq_encode_greedy(pf_x, cb, enc_prep)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    pf_ms = ev0.elapsed_time(ev1) / n_pf
+    del pf_x
+
     # ---- timed region 1: K full sparse decode steps, issued eagerly
     for i in range(args.warmup):
         sparse_step(i)
@@ -884,6 +928,18 @@ def main():
             "fp32_peak_tflops": 157.3,
             "search": "exact fp32 dot16 distances to all 256 entries per stage "
                       "(encode_exact_kernel, 2 rows per workgroup)",
+        },
+        "prefill_encode": {
+            "workload": "one layer's C4 prefill: 8 KV heads x 131072 post-RoPE key rows "
+                        "(positions 0..131071), D=128, the same codebooks; greedy codes + "
+                        "residual norm",
+            "rows": PREFILL_ROWS,
+            "ms": round(pf_ms, 3),
+            "rows_per_s": round(PREFILL_ROWS / (pf_ms * 1e-3), 1),
+            "search_tflops": round(PREFILL_FLOP / (pf_ms * 1e-3) / 1e12, 2),
+            "bf16_mfma_peak_tflops": 2500.0,
+            "search": "bf16 MFMA distances to all 256 entries per stage (the coarse pass) "
+                      "+ exact fp32 recheck of the shortlist (encode_tile_kernel)",
         },
         "roofline": {
             "bound": "hbm",
