@@ -391,7 +391,10 @@ __device__ __forceinline__ uint2 bf16x4_bits(const float4 v) {
 template <int D>
 struct EncShared {
   float r[16][D];
-  uint16_t rb[16][D];  // bf16(r): the MFMA A operand
+  // bf16(r): the MFMA A operand.  The pitch (D + 8) puts the 16 rows of one
+  // operand read in different banks (a pitch of D, a multiple of 64 banks,
+  // would put them all in the same two)
+  uint16_t rb[16][D + 8];
   float rn[16];
   float u[16][EncCfg<D>::WAVES];  // per row, per wave: min of the upper bounds
   uint16_t mask[16][16];          // per row, per 16-entry tile: coarse-pass survivors
@@ -1213,7 +1216,10 @@ struct TileShared {
   static constexpr int KS = D / 16;
   uint2 frag[16 * KS * 64];    // stage fragments [tile][ks][lane], K <= 256
   float r[kTileRows][D];
-  uint16_t rb[kTileRows][D];   // bf16(r): the MFMA A operand
+  // bf16(r): the MFMA A operand.  The pitch (D + 8) puts the 16 rows of one
+  // operand read in different banks (a pitch of D, a multiple of 64 banks,
+  // would put them all in the same two)
+  uint16_t rb[kTileRows][D + 8];
   float rn[kTileRows];
   float u[4][kTileRows];       // per tile quarter: min of G + eps per row
   uint32_t cnt[kTileRows];
