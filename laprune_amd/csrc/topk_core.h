@@ -27,8 +27,8 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
 // reversed bins), then the unique bin b with S(b) >= target > S(b+1).
 // s_res = {b, S(b+1)}; every thread of the block synchronises.  target must
 // satisfy 1 <= target <= S(0); the block has at least 256 threads.
-__device__ void select_bin(const uint32_t* s_h, uint32_t target, uint32_t* s_wsum,
-                           uint32_t* s_res) {
+[[maybe_unused]] __device__ void select_bin(const uint32_t* s_h, uint32_t target, uint32_t* s_wsum,
+                                            uint32_t* s_res) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t x = 0, h = 0;
   if (wave < 4) {
