@@ -351,10 +351,15 @@ int lap_sparse_attn_decode_ragged(const void* q, int64_t q_sb, int64_t q_sh,
  *   codes  u8 [B][Hkv][>=T][32] strides (b, h, t, 1), 16-byte aligned (may
  *          be NULL when the call selects nothing: k = 0, or k_cols = 0)
  *   T      code columns scored (the grid; plans clamp to it), T_kv K/V rows
- *   q, K, V as lap_sparse_attn_decode; G = Hq / Hkv must be 4
- * With D = 128, group and per-head selection run as one launch (per KV
- * row, the workgroups of one XCD score, select and attend, and the last
- * merges); other shapes run the kernel chain.  Workspace: lap_decode_step_workspace_size
+ *   q, K, V as lap_sparse_attn_decode; G = Hq / Hkv of 1, 2, 4 or 8
+ *   lut_gmkg  fp16 LUT of the B * Hq query heads: G = 4, LAP_LUT_GMKG
+ *          [B * Hkv][32][256][4]; other G, LAP_LUT_HMK [B * Hq][32][256]
+ * With G = 4 and D = 128, group and per-head selection run as one launch
+ * (per KV row, the workgroups of one XCD score, select and attend, and the
+ * last merges); other shapes run the kernel chain (G = 4: lap_retrieve_topk;
+ * other G: lap_lut_score_gqa of every head, then lap_topk_select (_ragged)
+ * over the group max or each head's row; then the sparse attention).
+ * Workspace: lap_decode_step_workspace_size
  * with keep_max = k + sink + tail (ragged: k_cols + max_sink + max_tail).  It
  * must be zero-filled once before its first use; every call leaves its
  * barrier words and histograms at zero again.  Their layout does not depend

@@ -1362,18 +1362,32 @@ using namespace lap;
 namespace {
 
 // Rows a selection serves per KV row: 4 with LAP_SELECT_PER_HEAD, else 1.
-int step_rows_per_kv(int key_mode) { return (key_mode & LAP_SELECT_PER_HEAD) ? 4 : 1; }
+// Selection rows per KV head: its G query heads (LAP_SELECT_PER_HEAD) or
+// one group row.
+int step_rows_per_kv(int key_mode, int G) { return (key_mode & LAP_SELECT_PER_HEAD) ? G : 1; }
 
 // The chain's part of the workspace (after the fused part): the retrieve
 // workspace, then the attention partials.
+// The kernel chain's workspace: the retrieval part (G = 4: the fused
+// scorer's keys and histograms; other G: fp16 per-head scores [B * Hq][T],
+// `scores` bytes, then the top-k's workspace) and the attention's partials.
 struct ChainWs {
-  size_t ret, attn;
+  size_t ret, attn, scores;
 };
 int chain_ws(int B, int Hq, int Hkv, int T, int D, int keep_max, int key_mode, ChainWs* w) {
+  const int G = Hq / Hkv;
   size_t r = 0, a = 0;
-  int s = lap_retrieve_workspace_size(B * Hkv * step_rows_per_kv(key_mode), T, &r);
-  if (s != LAP_OK) return s;
-  s = lap_attn_decode_workspace_size(B, Hq, D, keep_max, &a);
+  w->scores = 0;
+  if (G == 4) {
+    int s = lap_retrieve_workspace_size(B * Hkv * step_rows_per_kv(key_mode, G), T, &r);
+    if (s != LAP_OK) return s;
+  } else {
+    w->scores = align_up((size_t)B * Hq * T * sizeof(uint16_t), 256);
+    int s = lap_topk_workspace_size(B * Hkv * step_rows_per_kv(key_mode, G), T, &r);
+    if (s != LAP_OK) return s;
+    r += w->scores;
+  }
+  int s = lap_attn_decode_workspace_size(B, Hq, D, keep_max, &a);
   if (s != LAP_OK) return s;
   w->ret = align_up(r, 256);
   w->attn = align_up(a, 256);
@@ -1401,7 +1415,10 @@ int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
                     bool need_all, lap_stream_t stream) {
   LAP_CHECK(lut_gmkg && q && keys && vals && out, "%s: null pointer", who);
   LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T > 0 && T_kv > 0 && D > 0, "%s: bad sizes", who);
-  LAP_CHECK(Hq == 4 * Hkv, "%s: the fused scorer serves G = 4 query heads per KV head", who);
+  LAP_CHECK(Hq % Hkv == 0, "%s: Hq=%d is not a multiple of Hkv=%d", who, Hq, Hkv);
+  const int G = Hq / Hkv;
+  LAP_CHECK_CODE(G == 1 || G == 2 || G == 4 || G == 8, LAP_ERR_UNSUPPORTED,
+                 "%s: group size %d unsupported (1, 2, 4 or 8 query heads per KV head)", who, G);
   LAP_CHECK(dtype == LAP_DTYPE_BF16 || dtype == LAP_DTYPE_F16, "%s: q/K/V must be bf16 or fp16",
             who);
   LAP_CHECK(idx_dtype == LAP_DTYPE_I32 || idx_dtype == LAP_DTYPE_I64,
@@ -1433,7 +1450,7 @@ int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
     LAP_CHECK_CODE(workspace && workspace_bytes >= fused + cw.ret + cw.attn, LAP_ERR_WORKSPACE,
                    "%s: workspace of %zu bytes needed", who, fused + cw.ret + cw.attn);
   hipStream_t st = as_stream(stream);
-  if (D == 128) {
+  if (D == 128 && G == 4) {
     s = decode_step_fused(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, q, q_sb,
                           q_sh, keys, vals, dtype, B, Hkv, T_kv, k_sb, k_sh, k_st, v_sb, v_sh,
                           v_st, T, cand_start, cand_end, k_eff, sink_count, tail_start,
@@ -1450,9 +1467,34 @@ int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
   char* base = static_cast<char*>(workspace) + fused;
   void* ws_r = base;
   void* ws_a = base + cw.ret;
-  const int H_idx = Hkv * step_rows_per_kv(key_mode);
+  const int rows = step_rows_per_kv(key_mode, G);
+  const int H_idx = Hkv * rows;
+  if (G != 4) {
+    // Per-head fp16 scores of every code column (lap_lut_score_gqa over the
+    // [B * Hq][32][256] table), then the top-k of the group max (group
+    // selection) or of each head's row.
+    if (selects) {
+      uint16_t* sc = reinterpret_cast<uint16_t*>(base);
+      const uint16_t* lut = static_cast<const uint16_t*>(lut_gmkg);
+      for (int b = 0; b < B; ++b) {
+        s = lap_lut_score_gqa(lut + (int64_t)b * Hq * kM * kK, codes + b * codes_stride_b,
+                              codes_stride_h, codes_stride_t, Hkv, G, T, kM, kK, 0, kM, nullptr,
+                              T, sc + (int64_t)b * Hq * T, stream);
+        if (s != LAP_OK) return s;
+      }
+      void* ws_t = base + cw.scores;
+      const size_t ws_t_bytes = cw.ret - cw.scores;
+      if (!plans)
+        s = lap_topk_select(sc, T, B * H_idx, G / rows, T, cand_start, cand_end, k_eff, km,
+                            out_idx, idx_dtype, ws_t, ws_t_bytes, stream);
+      else
+        s = lap_topk_select_ragged(sc, T, B * H_idx, G / rows, H_idx, T, plans, k_cols, km,
+                                   out_idx, idx_dtype, ws_t, ws_t_bytes, stream);
+      if (s != LAP_OK) return s;
+    }
+  }
   if (!plans) {
-    if (k_eff > 0) {
+    if (k_eff > 0 && G == 4) {
       s = lap_retrieve_topk(lut_gmkg, codes, codes_stride_b, codes_stride_h, codes_stride_t, B,
                             Hkv, T, cand_start, cand_end, k_eff, key_mode, nullptr, out_idx,
                             idx_dtype, ws_r, cw.ret, stream);
@@ -1463,7 +1505,7 @@ int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
                                   sink_count, tail_start, tail_count, scale, out, ws_a, cw.attn,
                                   stream);
   }
-  if (k_cols > 0) {
+  if (k_cols > 0 && G == 4) {
     s = lap_retrieve_topk_ragged(lut_gmkg, codes, codes_stride_b, codes_stride_h,
                                  codes_stride_t, B, Hkv, T, plans, k_cols, key_mode, nullptr,
                                  out_idx, idx_dtype, ws_r, cw.ret, stream);

@@ -102,10 +102,12 @@ void decode_step(const at::Tensor& lut, const std::optional<at::Tensor>& codes, 
               "laprune::decode_step: keys / vals must be [B, Hkv, T_kv, D] of q's B and D");
   TORCH_CHECK(out.is_contiguous() && out.numel() >= B * Hq * D,
               "laprune::decode_step: out must be contiguous with at least B * Hq * D elements");
+  TORCH_CHECK(Hkv > 0 && Hq % Hkv == 0, "laprune::decode_step: Hq must be a multiple of Hkv");
   TORCH_CHECK(lut.scalar_type() == at::kHalf && lut.is_contiguous() &&
-                  lut.numel() >= B * Hkv * 32 * 256 * 4,
-              "laprune::decode_step: lut must be the contiguous fp16 [B * Hkv, 32, 256, 4] table");
-  const int64_t rows = Hkv * ((key_mode & LAP_SELECT_PER_HEAD) ? 4 : 1);
+                  lut.numel() >= B * Hq * 32 * 256,
+              "laprune::decode_step: lut must be the contiguous fp16 table of B * Hq heads "
+              "([B * Hkv, 32, 256, 4] for G = 4, else [B * Hq, 32, 256])");
+  const int64_t rows = (key_mode & LAP_SELECT_PER_HEAD) ? Hq : Hkv;
   const int64_t cols = plans ? k_cols : std::max<int64_t>(0, std::min(k, cand_end - cand_start));
   if (cols > 0) {
     TORCH_CHECK(idx.is_contiguous() && idx.numel() >= B * rows * cols &&

@@ -174,7 +174,9 @@ class SparseDecoder:
 
     Args:
       codebooks: [M=32, K=256, D] fp32 (or fp16) AQ codebooks on the GPU.
-      batch, num_q_heads, num_kv_heads, head_dim: attention geometry (G = 4).
+      batch, num_q_heads, num_kv_heads, head_dim: attention geometry; G = Hq / Hkv
+        of 1, 2, 4 or 8 (G = 4 with D = 128 runs the one-launch step, other
+        shapes the kernel chain).
       max_tokens: largest cache length the step will see (sizes scratch).
       cfg: selection settings.
     """
@@ -188,8 +190,9 @@ class SparseDecoder:
         N.require_cuda(codebooks)
         if tuple(codebooks.shape) != (self.M, self.K, head_dim):
             raise RuntimeError(f"codebooks must be [32, 256, {head_dim}]")
-        if num_q_heads != 4 * num_kv_heads:
-            raise RuntimeError("the fused scorer serves G = 4 query heads per KV head")
+        if num_kv_heads <= 0 or num_q_heads % num_kv_heads or \
+                num_q_heads // num_kv_heads not in (1, 2, 4, 8):
+            raise RuntimeError("the decode step serves G = 1, 2, 4 or 8 query heads per KV head")
         self.cfg = cfg or RetrievalConfig()
         self.dev = codebooks.device
         self.cb = codebooks.contiguous()
@@ -198,7 +201,15 @@ class SparseDecoder:
         self.T_max = max_tokens
         self.dtype = dtype
         R = batch * num_kv_heads
-        self.lut = torch.empty((R, self.M, self.K, 4), dtype=torch.float16, device=self.dev)
+        # G = 4: the interleaved [B * Hkv, M, K, 4] table of the fused scorer;
+        # other G: the per-head [B * Hq, M, K] table of the kernel chain
+        if self.G == 4:
+            self.lut_layout = N.LUT_GMKG
+            self.lut = torch.empty((R, self.M, self.K, 4), dtype=torch.float16, device=self.dev)
+        else:
+            self.lut_layout = N.LUT_HMK
+            self.lut = torch.empty((batch * num_q_heads, self.M, self.K), dtype=torch.float16,
+                                   device=self.dev)
         k_cap = self._k_cap(max_tokens)
         # selection rows per batch row: KV groups (group max) or query heads
         rows = num_kv_heads if self.cfg.select == "group" else num_q_heads
@@ -275,7 +286,7 @@ class SparseDecoder:
             raise RuntimeError("a sequence length exceeds the cache views")
         p = self.plan(t_codes, t_total)
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
-        self._ops.lut_build(qf, self.cb, 4, N.LUT_GMKG, self.lut)
+        self._ops.lut_build(qf, self.cb, self.G, self.lut_layout, self.lut)
         self.last_k = p["k"]
         self._decode_step(q, codes, keys, vals, max(t_codes, 1), t_total, p, None, 0, 0, 0)
         return self.out.unsqueeze(2)
@@ -338,7 +349,7 @@ class SparseDecoder:
             self._plan_key = key
         pdev = self._plans.dev
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
-        self._ops.lut_build(qf, self.cb, 4, N.LUT_GMKG, self.lut)
+        self._ops.lut_build(qf, self.cb, self.G, self.lut_layout, self.lut)
         k_cols = max(p["k"] for p in plans)
         T = max(max(t_codes), 1)
         self.last_k = k_cols
@@ -369,7 +380,7 @@ class SparseDecoder:
         B, Hq, Hkv, D = self.B, self.Hq, self.Hkv, self.D
         T = min(codes.shape[2], self.T_max)
         qf = q.reshape(B * Hq, D) if q.is_contiguous() else q.contiguous().reshape(B * Hq, D)
-        self._ops.lut_build(qf, self.cb, 4, N.LUT_GMKG, self.lut)
+        self._ops.lut_build(qf, self.cb, self.G, self.lut_layout, self.lut)
         k_cols = self.k_cols
         self.last_k = k_cols
         self._decode_step(q, codes, keys, vals, T, keys.shape[2], None, plans, k_cols,
