@@ -4,6 +4,7 @@ serves too: its scores come from the GQA gather kernel for any G
 (aq_kv.py:684-699 -> aq_kernels/aq_lut_gqa.cu:350-422) before the same
 window, budget and torch.topk (aq_evaluation.py:160-205).
 
+Head dim 256 (with G = 4, the fused scorer's chain) is covered here too.
 These shapes take the kernel chain: the per-head [B * Hq][32][256] table,
 lap_lut_score_gqa of every head, lap_topk_select (_ragged) over the group
 max (group selection) or each head's row, then the split-K sparse
@@ -66,6 +67,8 @@ def _decoder(cb, dev, B, Hq, D, T, topk, select):
     (2, 64, 1, 4096, None, "head"),
     (8, 128, 1, 8192, 512, "group"),    # Llama-3-70B-like grouping
     (8, 128, 2, 5000, None, "head"),
+    (4, 256, 1, 4096, 200, "group"),    # head_dim 256: the chain with the fused scorer
+    (2, 256, 1, 4096, None, "head"),
 ])
 def test_step_other_groups(dev, orc, G, D, B, T, topk, select):
     per_head = select == "head"
