@@ -351,7 +351,7 @@ int lap_sparse_attn_decode_ragged(const void* q, int64_t q_sb, int64_t q_sh,
  *   codes  u8 [B][Hkv][>=T][32] strides (b, h, t, 1), 16-byte aligned (may
  *          be NULL when the call selects nothing: k = 0, or k_cols = 0)
  *   T      code columns scored (the grid; plans clamp to it), T_kv K/V rows
- *   q, K, V as lap_sparse_attn_decode; G = Hq / Hkv of 1, 2, 4 or 8
+ *   q, K, V as lap_sparse_attn_decode; G = Hq / Hkv from 1 to 8
  *   lut_gmkg  fp16 LUT of the B * Hq query heads: G = 4, LAP_LUT_GMKG
  *          [B * Hkv][32][256][4]; other G, LAP_LUT_HMK [B * Hq][32][256]
  * With G = 4 and D = 128, group and per-head selection run as one launch

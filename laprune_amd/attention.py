@@ -41,7 +41,7 @@ def _decode_kernel_fits(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bo
     Hkv = k.shape[1]
     if k.shape[0] != B or k.shape[3] != D or D not in (64, 128, 256) or k.shape[2] < 1:
         return False
-    if Hq % Hkv or Hq // Hkv not in (1, 2, 4, 8):
+    if Hq % Hkv or not 1 <= Hq // Hkv <= 8:
         return False
     if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
         return False

@@ -12,8 +12,9 @@
 // L = [0, T).
 //
 // Work shape: workgroup = (b, selection row, split) with 256 threads; a row
-// carries HPR query heads (HPR = G when one list serves a KV group, 1 for
-// per-head lists) so K/V rows are read once per group.  Each wave runs its
+// carries nh query heads (G when one list serves a KV group, 1 for per-head
+// lists; the kernel is built for HPR = 1, 2, 4 or 8 heads and leaves the
+// lanes past nh out) so K/V rows are read once per group.  Each wave runs its
 // own online softmax over steps of 16 keys of the split (waves take steps
 // round-robin); q.k and p.V of a step are 16x16x16 MFMAs (layouts below), so
 // the VALU only does the softmax.  Memory is software-pipelined per wave: a
@@ -41,6 +42,7 @@ struct AttnArgs {
   int B, Hq, Hkv, T;
   const void* idx;
   int H_idx, n_idx, sink, tail_start, tail_count;
+  int nh;            // query heads per index row (1, or G = Hq / Hkv), <= HPR
   float scale_log2;  // softmax scale * log2(e)
   int per_split, nsplit;
   uint16_t* out;     // [B][Hq][D]
@@ -91,6 +93,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   const int br = blockIdx.x / a.nsplit;
   const int b = br / a.H_idx, ri = br - b * a.H_idx;
   const int G = a.Hq / a.Hkv;
+  const int nh = a.nh;
   const int h0 = (a.H_idx == a.Hq) ? ri : ri * G;  // first query head of the row
   const int hkv = h0 / G;
   const RowKeep rk = row_keep(a, b);
@@ -105,13 +108,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   WaveState<DT, HPR, D> ws;
   {
     const int r = lane >> 4, c = lane & 15;
-    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (c < HPR ? c : 0)) * a.q_sh;
+    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(h0 + (c < nh ? c : 0)) * a.q_sh;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
       const uint16_t* q4 = qp + r * (D / 4) + 4 * ks;  // q may be only 2-byte aligned
       i16x4 f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) f[e] = c < HPR ? (short)q4[e] : (short)0;
+      for (int e = 0; e < 4; ++e) f[e] = c < nh ? (short)q4[e] : (short)0;
       ws.qf[ks] = f;
       ws.acc[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -159,20 +162,20 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
   // Merge the four waves' states.
   {
     const int r = lane >> 4, c = lane & 15;
-    if (lane < HPR) {
+    if (lane < nh) {
       s_m[wave][lane] = ws.m;
       s_l[wave][lane] = ws.l;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int h = 4 * r + e;
-      if (h < HPR)
+      if (h < nh)
 #pragma unroll
         for (int ch = 0; ch < D / 16; ++ch) s_o[wave][h][c * (D / 16) + ch] = ws.acc[ch][e];
     }
   }
   __syncthreads();
-  for (int i = tid; i < HPR * D; i += kThreads) {
+  for (int i = tid; i < nh * D; i += kThreads) {
     const int g = i / D, d = i - g * D;
     const float M = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
     float l = 0.f, o = 0.f;
@@ -298,7 +301,10 @@ int run_attn(AttnArgs a, int dtype, int idx_dtype, int D, void* workspace, size_
              hipStream_t st) {
   const int L = a.n_idx + a.sink + a.tail_count;
   const int G = a.Hq / a.Hkv;
-  const int hpr = (a.H_idx == a.Hq) ? 1 : G;
+  a.nh = (a.H_idx == a.Hq) ? 1 : G;
+  // the kernel's head capacity per row: the next of 1, 2, 4, 8 (lanes past
+  // nh compute on zero queries and write nothing)
+  const int hpr = a.nh <= 1 ? 1 : a.nh <= 2 ? 2 : a.nh <= 4 ? 4 : 8;
   a.nsplit = choose_nsplit(a.B * a.H_idx, L > 0 ? L : 1);
   LAP_CHECK_CODE(a.nsplit > 0, LAP_ERR_HIP, "attention: device query failed");
   a.per_split = (L + a.nsplit - 1) / a.nsplit;
@@ -342,8 +348,8 @@ int check_common(const void* q, const void* keys, const void* vals, void* out, i
   LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T > 0, "attention decode: bad sizes (T must be >= 1)");
   LAP_CHECK(Hq % Hkv == 0, "invalid GQA head counts: Hq=%d, Hkv=%d", Hq, Hkv);
   const int G = Hq / Hkv;
-  LAP_CHECK_CODE(G == 1 || G == 2 || G == 4 || G == 8, LAP_ERR_UNSUPPORTED,
-                 "attention decode: group size %d unsupported", G);
+  LAP_CHECK_CODE(G >= 1 && G <= 8, LAP_ERR_UNSUPPORTED,
+                 "attention decode: group size %d unsupported (1 to 8)", G);
   LAP_CHECK_CODE(D == 64 || D == 128 || D == 256, LAP_ERR_UNSUPPORTED,
                  "attention decode: head dim %d unsupported (64/128/256)", D);
   LAP_CHECK(q_sh >= D && k_st >= D && v_st >= D, "attention decode: strides smaller than D");

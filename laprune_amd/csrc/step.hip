@@ -1417,8 +1417,8 @@ int decode_step_run(const char* who, const void* lut_gmkg, const uint8_t* codes,
   LAP_CHECK(B > 0 && Hq > 0 && Hkv > 0 && T > 0 && T_kv > 0 && D > 0, "%s: bad sizes", who);
   LAP_CHECK(Hq % Hkv == 0, "%s: Hq=%d is not a multiple of Hkv=%d", who, Hq, Hkv);
   const int G = Hq / Hkv;
-  LAP_CHECK_CODE(G == 1 || G == 2 || G == 4 || G == 8, LAP_ERR_UNSUPPORTED,
-                 "%s: group size %d unsupported (1, 2, 4 or 8 query heads per KV head)", who, G);
+  LAP_CHECK_CODE(G >= 1 && G <= 8, LAP_ERR_UNSUPPORTED,
+                 "%s: group size %d unsupported (1 to 8 query heads per KV head)", who, G);
   LAP_CHECK(dtype == LAP_DTYPE_BF16 || dtype == LAP_DTYPE_F16, "%s: q/K/V must be bf16 or fp16",
             who);
   LAP_CHECK(idx_dtype == LAP_DTYPE_I32 || idx_dtype == LAP_DTYPE_I64,

@@ -175,7 +175,7 @@ class SparseDecoder:
     Args:
       codebooks: [M=32, K=256, D] fp32 (or fp16) AQ codebooks on the GPU.
       batch, num_q_heads, num_kv_heads, head_dim: attention geometry; G = Hq / Hkv
-        of 1, 2, 4 or 8 (G = 4 with D = 128 runs the one-launch step, other
+        from 1 to 8 (G = 4 with D = 128 runs the one-launch step, other
         shapes the kernel chain).
       max_tokens: largest cache length the step will see (sizes scratch).
       cfg: selection settings.
@@ -191,8 +191,8 @@ class SparseDecoder:
         if tuple(codebooks.shape) != (self.M, self.K, head_dim):
             raise RuntimeError(f"codebooks must be [32, 256, {head_dim}]")
         if num_kv_heads <= 0 or num_q_heads % num_kv_heads or \
-                num_q_heads // num_kv_heads not in (1, 2, 4, 8):
-            raise RuntimeError("the decode step serves G = 1, 2, 4 or 8 query heads per KV head")
+                not 1 <= num_q_heads // num_kv_heads <= 8:
+            raise RuntimeError("the decode step serves G = 1 to 8 query heads per KV head")
         self.cfg = cfg or RetrievalConfig()
         self.dev = codebooks.device
         self.cb = codebooks.contiguous()

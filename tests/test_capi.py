@@ -135,9 +135,8 @@ def test_cpu_tensors_are_rejected_loudly():
 
 def test_decode_step_argument_checks(lib):
     """lap_decode_step validates before touching the device: null inputs,
-    head counts that do not group, a group size without an attention kernel
-    (3), and a missing workspace (also for G = 2, which the kernel chain
-    serves)."""
+    head counts that do not group, a group size above 8, and a missing
+    workspace (also for G = 2, which the kernel chain serves)."""
     from laprune_amd import _native as N
     one = C.c_void_p(4096)  # never dereferenced
     args = dict(lut=one, codes=one, T=1024, cs=4, ce=960, k=64, sink=4, ts=960, tc=64, key=N.KEY_BF16,
@@ -154,7 +153,7 @@ def test_decode_step_argument_checks(lib):
 
     assert call(lut=None) == N.LAP_ERR_INVALID and "null pointer" in _err(lib)
     assert call(Hq=20) == N.LAP_ERR_INVALID and "not a multiple" in _err(lib)
-    assert call(Hq=24) == N.LAP_ERR_UNSUPPORTED and "group size 3" in _err(lib)
+    assert call(Hq=72) == N.LAP_ERR_UNSUPPORTED and "group size 9" in _err(lib)
     assert call(Hq=16) == N.LAP_ERR_WORKSPACE and "workspace of" in _err(lib)
     assert call(ce=2000) == N.LAP_ERR_INVALID and "candidate window" in _err(lib)
     assert call(key=7) == N.LAP_ERR_INVALID and "key mode" in _err(lib)

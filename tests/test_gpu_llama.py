@@ -7,7 +7,7 @@
   attention kernels round differently; measured 0.009).  Control: keeping
   only top-1 + sink + local moves the logits by far more (measured 0.94), so
   the comparison does see the attention.
-  The same holds with G = 1, 2 and 8 query heads per KV head (the kernel
+  The same holds with G = 1, 2, 7 and 8 query heads per KV head (the kernel
   chain's per-head table, GQA scorer and top-k).
 * A ragged batch decodes each sequence as that sequence alone (same
   tolerance: batched GEMMs may round differently from batch-1 GEMMs).
@@ -22,7 +22,8 @@ VOCAB = 1000
 
 def _tiny(heads=8, kv_heads=2):
     from transformers import LlamaConfig
-    return LlamaConfig(vocab_size=VOCAB, hidden_size=512, intermediate_size=1024,
+    hidden = 512 if 512 % heads == 0 else 64 * heads  # transformers wants heads | hidden
+    return LlamaConfig(vocab_size=VOCAB, hidden_size=hidden, intermediate_size=1024,
                        num_hidden_layers=3, num_attention_heads=heads, num_key_value_heads=kv_heads,
                        head_dim=64, max_position_embeddings=4096, rope_theta=10000.0,
                        attn_implementation="sdpa")
@@ -38,7 +39,7 @@ def _rel(a, b):
     return float((a - b).abs().max() / b.abs().max().clamp_min(1e-6))
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (8, 1), (4, 4), (8, 4)])  # G = 4, 8, 1, 2
+@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (8, 1), (4, 4), (8, 4), (7, 1)])  # G = 4, 8, 1, 2, 7
 def test_keep_all_matches_dense_model(dev, heads, kv_heads):
     from laprune_amd.llama import LAPruneLlama, LAPruneSettings, random_model
     from laprune_amd.retrieval import RetrievalConfig

@@ -1,5 +1,6 @@
 """The decode step (lap_decode_step through SparseDecoder) for G = Hq / Hkv
-of 1, 2 and 8 query heads per KV head, which the reference's decode path
+other than 4 (1, 2, 3, 6, 7 and 8 query heads per KV head), which the
+reference's decode path
 serves too: its scores come from the GQA gather kernel for any G
 (aq_kv.py:684-699 -> aq_kernels/aq_lut_gqa.cu:350-422) before the same
 window, budget and torch.topk (aq_evaluation.py:160-205).
@@ -69,6 +70,9 @@ def _decoder(cb, dev, B, Hq, D, T, topk, select):
     (8, 128, 2, 5000, None, "head"),
     (4, 256, 1, 4096, 200, "group"),    # head_dim 256: the chain with the fused scorer
     (2, 256, 1, 4096, None, "head"),
+    (7, 128, 2, 6000, 300, "group"),    # Qwen2.5-7B-like grouping (28 q / 4 KV heads)
+    (3, 128, 1, 5000, None, "head"),
+    (6, 64, 1, 4096, 256, "group"),
 ])
 def test_step_other_groups(dev, orc, G, D, B, T, topk, select):
     per_head = select == "head"
@@ -87,7 +91,7 @@ def test_step_other_groups(dev, orc, G, D, B, T, topk, select):
         _check_attn(orc, out, q, kk, vv, want, b, T, G, per_head)
 
 
-@pytest.mark.parametrize("G,select", [(8, "group"), (2, "head")])
+@pytest.mark.parametrize("G,select", [(8, "group"), (2, "head"), (7, "group")])
 def test_step_other_groups_ragged_graph(dev, orc, G, select):
     """B = 3 ragged lengths through device plans, eager and replayed from a
     captured graph (twice, with the decoder's eager steps between)."""
@@ -130,8 +134,9 @@ def test_step_other_groups_ragged_graph(dev, orc, G, select):
 
 
 def test_step_group_size_refused(dev):
-    """G = 3 has no attention kernel: the decoder refuses it up front."""
+    """More than 8 query heads per KV head exceed the attention kernel's
+    16-lane head tile as laid out: the decoder refuses them up front."""
     from laprune_amd.retrieval import SparseDecoder
     cb = torch.zeros(32, 256, 128, device=dev)
-    with pytest.raises(RuntimeError, match="G = 1, 2, 4 or 8"):
-        SparseDecoder(cb, 1, 12, 4, 128, 1024)
+    with pytest.raises(RuntimeError, match="G = 1 to 8"):
+        SparseDecoder(cb, 1, 48, 4, 128, 1024)
