@@ -27,21 +27,21 @@ def _rel(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-6))
 
 
-def _inputs(seed, B, Hq, T, D, dev):
+def _inputs(seed, B, Hq, T, D, dev, dt=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     cb = torch.randn(32, 256, D, generator=g) * 0.02
     codes = torch.randint(0, 256, (B, Hkv, T, 32), generator=g, dtype=torch.uint8)
-    q = torch.randn(B, Hq, 1, D, generator=g).bfloat16()
-    kk = torch.randn(B, Hkv, T, D, generator=g).bfloat16().to(dev)
-    vv = torch.randn(B, Hkv, T, D, generator=g).bfloat16().to(dev)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(dt)
+    kk = torch.randn(B, Hkv, T, D, generator=g).to(dt).to(dev)
+    vv = torch.randn(B, Hkv, T, D, generator=g).to(dt).to(dev)
     return cb, codes, kk, vv, q
 
 
-def _want_idx(orc, cb, codes_b, q_b, plan, G, per_head):
+def _want_idx(orc, cb, codes_b, q_b, plan, G, per_head, key_bf16=True):
     lut = orc.lut_build(q_b.float().numpy(), cb.numpy())
     s = orc.score_grouped(lut, codes_b[:, :plan["t_codes"]].numpy(), G)
     return orc.topk(s, plan["k"], 1 if per_head else G, plan["cand_start"], plan["cand_end"],
-                    key_bf16=True)
+                    key_bf16=key_bf16)
 
 
 def _check_attn(orc, out, q, kk, vv, want_b, b, t_total, G, per_head):
@@ -54,11 +54,11 @@ def _check_attn(orc, out, q, kk, vv, want_b, b, t_total, G, per_head):
     assert _rel(out[b:b + 1, :, 0].double().cpu().numpy(), ref) < 1e-2, b
 
 
-def _decoder(cb, dev, B, Hq, D, T, topk, select):
+def _decoder(cb, dev, B, Hq, D, T, topk, select, dt=torch.bfloat16, key_dt=torch.bfloat16):
     from laprune_amd.retrieval import RetrievalConfig, SparseDecoder
     cfg = RetrievalConfig(topk=topk, sink_size=SINK, local_window=LOCAL, select=select,
-                          score_dtype=torch.bfloat16)
-    return SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg, dtype=torch.bfloat16)
+                          score_dtype=key_dt)
+    return SparseDecoder(cb.to(dev), B, Hq, Hkv, D, T, cfg, dtype=dt)
 
 
 @pytest.mark.parametrize("G,D,B,T,topk,select", [
@@ -131,6 +131,23 @@ def test_step_other_groups_ragged_graph(dev, orc, G, select):
         check(out_g.clone())
         dec.step(qd, cd, kk, vv, t_codes=t_codes, t_total=t_total)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("G,select", [(8, "group"), (3, "head")])
+def test_step_other_groups_fp16(dev, orc, G, select):
+    """fp16 queries, K/V and output with fp16 selection keys."""
+    per_head, Hq, B, T, D = select == "head", Hkv * G, 2, 5000, 128
+    print(f"group size {G}: fp16 {select}", flush=True)
+    cb, codes, kk, vv, q = _inputs(980 + G, B, Hq, T, D, dev, torch.float16)
+    dec = _decoder(cb, dev, B, Hq, D, T, 333, select, torch.float16, torch.float16)
+    tc = T - T % 64
+    out = dec.step(q.to(dev), codes.to(dev), kk, vv, t_codes=tc, t_total=T).clone()
+    sel = dec.selected().cpu().numpy()
+    p = dict(t_codes=tc, **dec.plan(tc, T))
+    for b in range(B):
+        want = _want_idx(orc, cb, codes[b], q[b, :, 0], p, G, per_head, key_bf16=False)
+        assert np.array_equal(sel[b].astype(np.int64), want), b
+        _check_attn(orc, out, q, kk, vv, want, b, T, G, per_head)
 
 
 def test_step_group_size_refused(dev):
